@@ -61,6 +61,75 @@ int lollm_gdn_verify(const void* q, const void* k, const void* v, const float* g
 int lollm_gdn_select_state(const float* snapshots, const int32_t* slot, float* state_out,
                            int B, int T, int Hv, int Dk, int Dv, void* stream);
 
+/* Gated GQA attention for T new queries per sequence over its KV cache.
+ *
+ * Replaces: attention() / torch_attention (src/attention.py:43-51,84-91), the KV
+ * expansion _repeat_kv (src/qwen3_5/blocks.py:152-156,229) and the output gate
+ * (blocks.py:235) of GatedAttention.forward; supersedes the Triton kv_fwd_kernel
+ * (src/_triton_attn.py:37-111).
+ *
+ *   q        (B, T, Hq, D) bf16, after QK-norm and RoPE
+ *   k_cache, v_cache  bf16; rows of D for (b, kv-head, position) at
+ *            base + b * seq_stride + kvh * head_stride + pos * D   (elements)
+ *   kv_len   (B) int32 keys per sequence INCLUDING the T new ones, which sit at
+ *            positions kv_len - T .. kv_len - 1; query i attends positions
+ *            <= kv_len - T + i (offset-causal)
+ *   gate     (B, T, Hq * D) bf16 or NULL; out = attn * sigmoid(gate)
+ *   out      (B, T, Hq * D) bf16
+ *   workspace  split-K partials, lollm_attn_workspace_bytes() bytes (may be NULL
+ *            when max_len <= chunk)
+ *   chunk    keys per split (multiple of 128); scale: softmax scale (D^-0.5)
+ * Supported: D == 256, Hq / Hkv <= 32. */
+long long lollm_attn_workspace_bytes(int B, int T, int Hq, int Hkv, int D, int max_len,
+                                     int chunk);
+int lollm_attn_verify(const void* q, const void* k_cache, const void* v_cache,
+                      const int32_t* kv_len, const void* gate, void* out, void* workspace,
+                      long long workspace_bytes, int B, int T, int Hq, int Hkv, int D,
+                      int max_len, long long seq_stride, long long head_stride, int chunk,
+                      float scale, void* stream);
+
+/* Speculative-sampling acceptance over the full vocabulary for B sequences with k
+ * drafts each, and the residual / bonus draw.
+ *
+ * Replaces: the accept/reject step of generate_mtp (src/qwen3_5/mtp.py:144-162) --
+ * there sample-and-match with k = 1 -- by the rejection rule (accept draft d at
+ * position i iff u q_i(d) < p_i(d); at the first rejection draw from
+ * norm(max(0, p_i - q_i)); if all k are accepted draw the bonus from p_k), with p and
+ * q formed as sample_next does (src/generate.py:17-37: temperature, top-k >= k-th
+ * value, top-p on the mass ranked strictly above a token, greedy at T <= 0).
+ *
+ *   target   (B, k+1, V) bf16 logits of the verify pass
+ *   draft    (B, k, V) bf16 draft logits, or NULL: q is one-hot at the draft token
+ *            (argmax drafts, mtp.py:138)
+ *   drafts   (B, k) int32 draft tokens
+ *   inv_temperature  1/T as fp32 (0 = greedy); top_k (0 = off); top_p (>= 1 = off)
+ *   seed, offset     Philox4x32-10 key and step counter; offset_dev, if not NULL, is a
+ *            device pointer the offset is read from instead (for captured graphs)
+ *   n_accepted (B) int32 in 0..k; next_token (B) int32
+ *   workspace  lollm_spec_workspace_bytes(B, k, draft != NULL) bytes
+ * Outputs are bit-exact to the integer specification in oracle/sampler_ref.c.
+ * Supported: V % 8 == 0, T <= 1000. */
+long long lollm_spec_workspace_bytes(int B, int k, int with_draft);
+int lollm_spec_accept(const void* target, const void* draft, const int32_t* drafts, int B, int k,
+                      int V, float inv_temperature, int top_k, float top_p, uint64_t seed,
+                      uint64_t offset, const uint64_t* offset_dev, int32_t* n_accepted,
+                      int32_t* next_token, void* workspace, long long workspace_bytes,
+                      void* stream);
+
+/* One draw per row from its temperature / top-k / top-p distribution (the
+ * multinomial of src/generate.py:37 on explicit uniforms); greedy rows return the
+ * first argmax (generate.py:24).  Row r uses Philox row row_base + r and `slot`.
+ * workspace: rows * 24 bytes. */
+int lollm_sample_rows(const void* logits, int rows, int V, float inv_temperature, int top_k,
+                      float top_p, uint64_t seed, uint64_t offset, const uint64_t* offset_dev,
+                      int row_base, int slot, int32_t* out, void* workspace,
+                      long long workspace_bytes, void* stream);
+
+/* The 24-bit Philox uniforms the sampler uses: out[r * slots + s] = U(row r, slot s).
+ * No reference counterpart (the reference draws implicitly with torch.multinomial). */
+int lollm_philox_uniform_u24(uint64_t seed, uint64_t offset, int rows, int slots,
+                             uint32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

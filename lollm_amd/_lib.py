@@ -29,6 +29,15 @@ SIGNATURES = {
     "lollm_gdn_verify": ([_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P,
                           _I, _I, _I, _I, _I, _I, _I, _I, _F, _P], _I),
     "lollm_gdn_select_state": ([_P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
+    "lollm_attn_workspace_bytes": ([_I, _I, _I, _I, _I, _I, _I], ctypes.c_longlong),
+    "lollm_attn_verify": ([_P, _P, _P, _P, _P, _P, _P, ctypes.c_longlong, _I, _I, _I, _I, _I,
+                           _I, ctypes.c_longlong, ctypes.c_longlong, _I, _F, _P], _I),
+    "lollm_spec_workspace_bytes": ([_I, _I, _I], ctypes.c_longlong),
+    "lollm_spec_accept": ([_P, _P, _P, _I, _I, _I, _F, _I, _F, _U64, _U64, _P, _P, _P, _P,
+                           ctypes.c_longlong, _P], _I),
+    "lollm_sample_rows": ([_P, _I, _I, _F, _I, _F, _U64, _U64, _P, _I, _I, _P, _P,
+                           ctypes.c_longlong, _P], _I),
+    "lollm_philox_uniform_u24": ([_U64, _U64, _I, _I, _P, _P], _I),
 }
 
 _lib = None
@@ -65,4 +74,5 @@ def header_symbols():
     """Entry points declared in include/lollm_amd.h."""
     with open(HEADER) as f:
         text = f.read()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(lollm_\w+)\s*\(", text, re.M)))
+    pat = r"^(?:const\s+)?(?:long\s+long|int|void|char|float)\s*\*?\s*(lollm_\w+)\s*\("
+    return sorted(set(re.findall(pat, text, re.M)))

@@ -131,3 +131,110 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None,
                              snapshots=False, final_state=True,
                              qk_l2norm=use_qk_l2norm_in_kernel)
     return out, fin
+
+
+# ------------------------------------------------------------------------------------
+# gated GQA attention over the KV cache
+# ------------------------------------------------------------------------------------
+def attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, chunk):
+    n = _lib.lib().lollm_attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, chunk)
+    if n < 0:
+        raise ValueError("unsupported attention geometry")
+    return n
+
+
+def attn_verify(q, k_cache, v_cache, kv_len, gate=None, *, chunk=512, scale=None,
+                workspace=None, out=None):
+    """q (B, T, Hq, D) bf16; k_cache / v_cache (B, Hkv, max_len, D) bf16 with the T
+    new keys already written at positions kv_len-T .. kv_len-1; kv_len (B,) int32;
+    gate (B, T, Hq*D) bf16 or None.  Returns (B, T, Hq*D) bf16."""
+    B, T, Hq, D = q.shape
+    _need(q, "q", torch.bfloat16)
+    if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[3] != D:
+        raise ValueError("k_cache must be (B, Hkv, max_len, D)")
+    Hkv, max_len = k_cache.shape[1], k_cache.shape[2]
+    _need(k_cache, "k_cache", torch.bfloat16)
+    _need(v_cache, "v_cache", torch.bfloat16, tuple(k_cache.shape))
+    _need(kv_len, "kv_len", torch.int32, (B,))
+    if gate is not None:
+        _need(gate, "gate", torch.bfloat16, (B, T, Hq * D))
+    if out is None:
+        out = torch.empty(B, T, Hq * D, dtype=torch.bfloat16, device=q.device)
+    _need(out, "out", torch.bfloat16, (B, T, Hq * D))
+    need = attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, chunk)
+    if max_len > chunk:
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        _need(workspace, "workspace")
+    wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    if scale is None:
+        scale = D ** -0.5
+    rc = _lib.lib().lollm_attn_verify(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(kv_len), _ptr(gate), _ptr(out),
+        _ptr(workspace), wbytes, B, T, Hq, Hkv, D, max_len, Hkv * max_len * D, max_len * D,
+        chunk, float(scale), _stream())
+    _lib.check(rc, "lollm_attn_verify")
+    return out
+
+
+# ------------------------------------------------------------------------------------
+# speculative sampling
+# ------------------------------------------------------------------------------------
+def inv_temperature(temperature: float) -> float:
+    """1/T rounded to fp32 (0 selects greedy, the reference's T <= 0 branch)."""
+    import numpy as np
+    return float(np.float32(1.0 / temperature)) if temperature > 0 else 0.0
+
+
+def spec_accept(target, draft, drafts, temperature, top_k=0, top_p=1.0, seed=0, offset=0, *,
+                offset_dev=None, workspace=None, n_accepted=None, next_token=None):
+    """target (B, k+1, V) bf16; draft (B, k, V) bf16 or None (argmax drafts);
+    drafts (B, k) int32.  Returns (n_accepted (B,), next_token (B,)) int32."""
+    B, T, V = target.shape
+    k = T - 1
+    _need(target, "target", torch.bfloat16)
+    if draft is not None:
+        _need(draft, "draft", torch.bfloat16, (B, k, V))
+    _need(drafts, "drafts", torch.int32, (B, k))
+    if offset_dev is not None:
+        _need(offset_dev, "offset_dev", torch.int64, (1,))
+    need = _lib.lib().lollm_spec_workspace_bytes(B, k, int(draft is not None))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=target.device)
+    _need(workspace, "workspace")
+    if n_accepted is None:
+        n_accepted = torch.empty(B, dtype=torch.int32, device=target.device)
+    if next_token is None:
+        next_token = torch.empty(B, dtype=torch.int32, device=target.device)
+    rc = _lib.lib().lollm_spec_accept(
+        _ptr(target), _ptr(draft), _ptr(drafts), B, k, V, inv_temperature(temperature),
+        int(top_k or 0), float(top_p if top_p is not None else 1.0), seed, offset,
+        _ptr(offset_dev), _ptr(n_accepted), _ptr(next_token), _ptr(workspace),
+        workspace.numel(), _stream())
+    _lib.check(rc, "lollm_spec_accept")
+    return n_accepted, next_token
+
+
+def sample_rows(logits, temperature, top_k=0, top_p=1.0, seed=0, offset=0, row_base=0, slot=0,
+                *, offset_dev=None, workspace=None, out=None):
+    """One token per row of logits (rows, V) bf16.  Returns (rows,) int32."""
+    rows, V = logits.shape
+    _need(logits, "logits", torch.bfloat16)
+    if workspace is None:
+        workspace = torch.empty(rows * 24, dtype=torch.uint8, device=logits.device)
+    _need(workspace, "workspace")
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    rc = _lib.lib().lollm_sample_rows(
+        _ptr(logits), rows, V, inv_temperature(temperature), int(top_k or 0),
+        float(top_p if top_p is not None else 1.0), seed, offset, _ptr(offset_dev), row_base,
+        slot, _ptr(out), _ptr(workspace), workspace.numel(), _stream())
+    _lib.check(rc, "lollm_sample_rows")
+    return out
+
+
+def philox_u24(seed, offset, rows, slots, device="cuda"):
+    out = torch.empty(rows, slots, dtype=torch.int32, device=device)
+    rc = _lib.lib().lollm_philox_uniform_u24(seed, offset, rows, slots, _ptr(out), _stream())
+    _lib.check(rc, "lollm_philox_uniform_u24")
+    return out

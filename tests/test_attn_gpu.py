@@ -1,0 +1,94 @@
+"""Gated GQA verify attention vs the oracle (src/attention.py:43-51 offset-causal SDPA
++ src/qwen3_5/blocks.py:229-235 GQA expansion and sigmoid gate), restated in
+oracle/qwen3_5_ref.py.  The oracle runs in fp32 on the same bf16 inputs; the kernel
+output is bf16, so the tolerance is bf16's (rtol 2e-2, atol 2e-2)."""
+
+import pytest
+import torch
+
+from oracle import qwen3_5_ref as R
+
+pytestmark = pytest.mark.gpu
+TOL = dict(rtol=2e-2, atol=2e-2)
+D = 256
+
+
+def make_case(B, T, Hq, Hkv, lens, seed, max_len=None, nan_tail=True):
+    gen = torch.Generator().manual_seed(seed)
+    max_len = max_len or max(lens)
+    q = torch.randn(B, T, Hq, D, generator=gen).bfloat16()
+    kc = torch.randn(B, Hkv, max_len, D, generator=gen).bfloat16()
+    vc = torch.randn(B, Hkv, max_len, D, generator=gen).bfloat16()
+    if nan_tail:                        # junk beyond each sequence's length must not leak
+        for b, L in enumerate(lens):
+            kc[b, :, L:] = float("nan")
+            vc[b, :, L:] = float("nan")
+    gate = torch.randn(B, T, Hq * D, generator=gen).bfloat16()
+    return q, kc, vc, torch.tensor(lens, dtype=torch.int32), gate
+
+
+def oracle(q, kc, vc, lens, gate):
+    B, T, Hq, _ = q.shape
+    Hkv = kc.shape[1]
+    rep = Hq // Hkv
+    outs = []
+    for b in range(B):
+        L = int(lens[b])
+        o = torch.empty(1, Hq, T, D)
+        for g in range(Hkv):
+            qq = q[b, :, g * rep:(g + 1) * rep].float().transpose(0, 1)[None]   # (1,rep,T,D)
+            kk = kc[b, g, :L].float()[None, None].expand(1, rep, L, D)
+            vv = vc[b, g, :L].float()[None, None].expand(1, rep, L, D)
+            o[:, g * rep:(g + 1) * rep] = R.sdpa_offset_causal(qq, kk, vv)
+        o = o.transpose(1, 2).reshape(T, Hq * D)
+        if gate is not None:
+            o = o * torch.sigmoid(gate[b].float())
+        outs.append(o)
+    return torch.stack(outs)
+
+
+CASES = [
+    # B, T, Hq, Hkv, lens, chunk
+    (3, 4, 16, 2, [4, 37, 700], 512),          # plain causal, one split, two splits
+    (2, 1, 8, 2, [1, 1000], 128),              # decode, many splits
+    (2, 2, 8, 2, [2, 129], 256),               # k = 1 verify, n_rep = 4
+    (2, 8, 16, 2, [8, 300], 128),              # two query blocks (n_rep 8 x 4 queries)
+    (4, 1, 32, 4, [1, 2, 3, 4], 128),          # MTP draft block: tiny causal contexts
+    (2, 4, 4, 2, [5, 64], 128),                # n_rep 2
+]
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,lens,chunk", CASES)
+@pytest.mark.parametrize("gated", [True, False])
+def test_attn_verify_matches_oracle(B, T, Hq, Hkv, lens, chunk, gated):
+    from lollm_amd import ops
+    print(f"case B={B} T={T} Hq={Hq} Hkv={Hkv} lens={lens} chunk={chunk} gated={gated}", flush=True)
+    q, kc, vc, kl, gate = make_case(B, T, Hq, Hkv, lens, seed=sum(lens) + T)
+    ref = oracle(q, kc, vc, kl, gate if gated else None)
+    out = ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(),
+                          gate.cuda() if gated else None, chunk=chunk)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    torch.testing.assert_close(out.cpu().float(), ref, **TOL)
+
+
+def test_attn_verify_long_ragged_contexts():
+    """The isolated verify shape: 16 q / 2 kv heads, dim 256, 1 + k = 4 queries, ragged
+    contexts drawn from U[1024, 32768] (4 sequences here to keep the CPU oracle fast;
+    the full 16-sequence batch runs in the benchmark)."""
+    from lollm_amd import ops
+    gen = torch.Generator().manual_seed(3)
+    lens = torch.randint(1024, 32769, (4,), generator=gen).tolist()
+    q, kc, vc, kl, gate = make_case(4, 4, 16, 2, lens, seed=3, max_len=32768)
+    ref = oracle(q, kc, vc, kl, gate)
+    out = ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda(), chunk=512)
+    torch.testing.assert_close(out.cpu().float(), ref, **TOL)
+
+
+def test_attn_split_invariance():
+    """The split-K combine must not change the answer: chunk 128 == chunk 1024."""
+    from lollm_amd import ops
+    q, kc, vc, kl, gate = make_case(2, 4, 16, 2, [900, 2000], seed=8)
+    a = ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda(), chunk=128)
+    b = ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda(), chunk=1024)
+    torch.testing.assert_close(a.float(), b.float(), rtol=1e-2, atol=1e-2)

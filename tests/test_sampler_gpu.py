@@ -1,0 +1,98 @@
+"""GPU speculative sampler vs the exact C oracle: accept counts, emitted tokens and
+row draws must be bit-exact (identical logits and Philox uniforms)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler_ref as S
+
+pytestmark = pytest.mark.gpu
+
+
+def acceptance_case(B, k, V, seed, noise=1.0, scale=3.0):
+    """The isolated acceptance workload: target = bf16(N(0, scale^2)), draft =
+    bf16(target[:, :k] + N(0, noise^2))."""
+    gen = torch.Generator().manual_seed(seed)
+    tgt = torch.randn(B, k + 1, V, generator=gen) * scale
+    drf = tgt[:, :k] + torch.randn(B, k, V, generator=gen) * noise
+    return tgt.bfloat16(), drf.bfloat16()
+
+
+def test_philox_matches_oracle():
+    from lollm_amd import ops
+    seed, off = 0x0123_4567_89ab_cdef, 3 << 33 | 5
+    u = ops.philox_u24(seed, off, 70, 9).cpu().numpy().astype(np.int64)
+    for r in range(70):
+        for s in range(9):
+            assert u[r, s] == S.uniform_u24(seed, off, r, s)
+
+
+@pytest.mark.parametrize("temp,top_k,top_p", [(0.7, 0, 0.95), (0.7, 20, 0.8), (1.0, 0, 1.0),
+                                              (0.0, 0, 1.0), (1.7, 50, 0.5)])
+def test_sample_rows_bit_exact(temp, top_k, top_p):
+    from lollm_amd import ops
+    print(f"case sample_rows T={temp} top_k={top_k} top_p={top_p}", flush=True)
+    tgt, _ = acceptance_case(8, 3, 151936, seed=4)
+    rows = tgt.reshape(-1, 151936).contiguous()
+    inv = S.inv_temperature(temp)
+    for off in (0, 1, 12345):
+        ref = S.sample_rows(rows, inv, top_k, top_p, 99, off, row_base=2, slot=5)
+        got = ops.sample_rows(rows.cuda(), temp, top_k, top_p, 99, off, row_base=2, slot=5)
+        assert np.array_equal(got.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("with_draft", [True, False])
+@pytest.mark.parametrize("temp,top_k,top_p", [(0.7, 0, 0.95), (0.7, 20, 0.8), (0.0, 0, 1.0)])
+def test_spec_accept_bit_exact_full_vocab(with_draft, temp, top_k, top_p):
+    """B=64, k=3, V=151936 (the isolated acceptance shape); drafts are drawn from the
+    draft rows with the same Philox stream (slot k+1+i), as a sampling draft chain does."""
+    from lollm_amd import ops
+    print(f"case accept draft={with_draft} T={temp} top_k={top_k} top_p={top_p}", flush=True)
+    B, k, V = 64, 3, 151936
+    tgt, drf = acceptance_case(B, k, V, seed=4)
+    inv = S.inv_temperature(temp)
+    drafts = np.stack([S.sample_rows(drf[:, i].contiguous(), inv, top_k, top_p, 7, 0, 0, k + 1 + i)
+                       for i in range(k)], 1).astype(np.int32)
+    if not with_draft:
+        drf = None
+    for off in (0, 9):
+        na_ref, nt_ref = S.spec_accept(tgt, drf, drafts, inv, top_k, top_p, 7, off)
+        na, nt = ops.spec_accept(tgt.cuda(), None if drf is None else drf.cuda(),
+                                 torch.from_numpy(drafts).cuda(), temp, top_k, top_p, 7, off)
+        assert np.array_equal(na.cpu().numpy(), na_ref)
+        assert np.array_equal(nt.cpu().numpy(), nt_ref)
+
+
+def test_spec_accept_small_vocab_ties_and_edges():
+    """Tiny vocabulary with heavy ties, flushed keys and argmax-drawn drafts; many
+    offsets so accepts, residual draws and bonus draws all occur."""
+    from lollm_amd import ops
+    rng = np.random.default_rng(0)
+    B, k, V = 16, 4, 64
+    x = rng.normal(0, 1.0, (B, k + 1, V)).astype(np.float32)
+    x[..., :8] = x[..., 8:9]
+    x[..., 60:] = 1e-7
+    tgt = torch.from_numpy(x).bfloat16()
+    drf = (tgt[:, :k].float() + torch.from_numpy(rng.normal(0, 0.3, (B, k, V)).astype(np.float32))).bfloat16()
+    drafts = drf.float().argmax(-1).int().numpy()
+    seen = set()
+    for off in range(12):
+        for d in (drf, None):
+            na_ref, nt_ref = S.spec_accept(tgt, d, drafts, S.inv_temperature(0.9), 0, 0.9, 3, off)
+            na, nt = ops.spec_accept(tgt.cuda(), None if d is None else d.cuda(),
+                                     torch.from_numpy(drafts).cuda(), 0.9, 0, 0.9, 3, off)
+            assert np.array_equal(na.cpu().numpy(), na_ref)
+            assert np.array_equal(nt.cpu().numpy(), nt_ref)
+            seen.update(int(a) for a in na_ref)
+    assert len(seen) >= 3                   # several acceptance lengths were exercised
+
+
+def test_offset_from_device_memory():
+    from lollm_amd import ops
+    tgt, drf = acceptance_case(4, 3, 4096, seed=1)
+    drafts = torch.randint(0, 4096, (4, 3), dtype=torch.int32)
+    off = torch.tensor([41], dtype=torch.int64).cuda()
+    a = ops.spec_accept(tgt.cuda(), drf.cuda(), drafts.cuda(), 0.7, 0, 0.95, 5, 41)
+    b = ops.spec_accept(tgt.cuda(), drf.cuda(), drafts.cuda(), 0.7, 0, 0.95, 5, 0, offset_dev=off)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
