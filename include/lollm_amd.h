@@ -130,6 +130,71 @@ int lollm_sample_rows(const void* logits, int rows, int V, float inv_temperature
 int lollm_philox_uniform_u24(uint64_t seed, uint64_t offset, int rows, int slots,
                              uint32_t* out, void* stream);
 
+/* RMSNorm with (1 + w) scaling in fp32 (src/qwen3_5/blocks.py:23-35), fused with the
+ * decoder's residual add (src/qwen3_5/modeling_qwen3_5.py:59-60) when residual !=
+ * NULL: x_out = bf16(x + residual), y = norm(x_out).  x, residual, x_out, y: (rows,
+ * H) bf16; w: (H) bf16.  Supported: H % 8 == 0, H <= 8192. */
+int lollm_rmsnorm(const void* x, const void* residual, void* x_out, const void* w, void* y,
+                  int rows, int H, float eps, void* stream);
+
+/* SwiGLU of blocks.py:341-342 on a fused [gate | up] projection: gate_up (rows, 2F)
+ * bf16 -> out (rows, F) = bf16(bf16(silu(gate)) * up).  Supported: F % 8 == 0. */
+int lollm_swiglu(const void* gate_up, void* out, int rows, int F, void* stream);
+
+/* Attention prologue of GatedAttention.forward (blocks.py:214-227): from the fused
+ * [q_proj | k_proj | v_proj] output qkv (B*T, Hq*2D + 2*Hkv*D) -- q_proj packing
+ * [query | gate] per head -- write q (B, T, Hq, D) after QK-norm (1 + w) and partial
+ * rotate-half RoPE (blocks.py:159-183) at positions rope_pos[b] + t (rope_pos NULL:
+ * lengths[b] + t, the cache row; the MTP head uses positions 1..L, mtp.py:66-67), the gate
+ * (B, T, Hq*D), and k (normed, roped) / v into the caches at (b, kvh, lengths[b] + t)
+ * (kv.py:26-33 without the concatenation).  inv_freq: (rotary_dim / 2) fp32.
+ * Supported: D == 256. */
+int lollm_attn_prologue(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                        const float* inv_freq, const int32_t* lengths, const int32_t* rope_pos,
+                        int B, int T, int Hq,
+                        int Hkv, int D, int rotary_dim, float eps, void* q_out, void* gate_out,
+                        void* k_cache, void* v_cache, int max_len, void* stream);
+
+/* The Gated DeltaNet mixer from the in_proj outputs to the gated-norm output
+ * (GatedDeltaNet.forward, blocks.py:288-329, between in_proj and out_proj):
+ * causal conv + SiLU, beta / g gating, L2-normalised delta-rule scan, gated RMSNorm.
+ *   proj      (B, T, proj_stride) bf16: [qkv (conv_dim) | z (Hv*Dv) | b (Hv) | a (Hv)]
+ *   conv_w    (conv_dim, conv_kernel) bf16; A_log, dt_bias (Hv) fp32; norm_w (Dv) bf16
+ *   win       (B, 2 * win_rows, conv_dim) bf16, two window halves: the committed conv
+ *             state is rows conv_off[b] .. conv_off[b] + conv_kernel - 2; the call
+ *             writes the other half (base h = 0 or win_rows): if conv_kernel - 1 + T
+ *             <= win_rows the whole window [state | raw x_0..x_{T-1}] at rows h.. (state
+ *             after c committed tokens = rows h + c ..), else the final state at rows h..
+ *   rec       (B, 2 * slots, Hv, Dk, Dv) fp32, two snapshot halves: the committed state
+ *             is slot rec_slot[b] (ignored when fresh: zero state); the call writes the
+ *             other half (base s = 0 or slots): the state after position t in slot s + t
+ *             if T <= slots, else the final state in slot s
+ *   out       (B, T, Hv*Dv) bf16
+ * Replaces: GatedDeltaNet._conv, the gating, torch_chunk_gated_delta_rule /
+ * torch_recurrent_gated_delta_rule and RMSNormGated (blocks.py:38-51,59-144,268-329),
+ * and the speculative deep copy of the linear state (kv.py:49-54).
+ * Supported: Dk == Dv == 128, conv_kernel <= 4. */
+int lollm_gdn_layer(const void* proj, long long proj_stride, const void* conv_w,
+                    const float* A_log, const float* dt_bias, const void* norm_w, void* win,
+                    const int32_t* conv_off, int win_rows, float* rec, const int32_t* rec_slot,
+                    int slots, int fresh, void* out, int B, int T, int Hk, int Hv, int Dk, int Dv,
+                    int conv_kernel, float eps, void* stream);
+
+/* End of one speculative step, per sequence b with a = n_accepted[b] (of T - 1
+ * drafts): keep a + 1 of the T verified positions (lengths += a + 1, GDN snapshot
+ * slot = written half + a, conv window offset = written half + a + 1, with the halves
+ * of lollm_gdn_layer: slots / win_rows) -- the O(1) form of the snapshot/restore
+ * of src/qwen3_5/mtp.py:141,156-162), append verify_ids[b, 0..a] to out_tokens (cap
+ * columns) at out_count[b], copy hidden[b, a] (B, T, H) to h_last (B, H) (the MTP
+ * input, mtp.py:155,162), set pending = next_token, and increment *offset (the
+ * sampler's Philox step counter).  No reference counterpart as one call: it folds
+ * the reference's per-step host bookkeeping into one kernel so a step needs no sync. */
+int lollm_spec_commit(const int32_t* verify_ids, const int32_t* n_accepted,
+                      const int32_t* next_token, int32_t* lengths, int32_t* rec_slot,
+                      int32_t* conv_off, int32_t* pending, int32_t* out_tokens, int32_t* out_count,
+                      int out_cap, const void* hidden, void* h_last, int B, int T, int H,
+                      int slots, int win_rows, long long* offset, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,248 @@
+// Fused elementwise / normalisation kernels of the qwen3_5 decoder step (gfx950).
+//
+//   rmsnorm      (src/qwen3_5/blocks.py:23-35) y = x * rsqrt(mean x^2 + eps) * (1 + w)
+//                in fp32, optionally fused with the residual add of
+//                modeling_qwen3_5.py:59-60 (x <- x + h, then y = norm(x))
+//   swiglu       (blocks.py:341-342) silu(gate) * up on a fused [gate | up] GEMM output
+//   attn_prologue (blocks.py:214-227 + RoPE blocks.py:166-183 + kv.py:26-33):
+//                split q_proj's per-head [query | gate], QK-norm (1 + w), partial
+//                rotate-half RoPE at absolute positions len_b + t, and write k, v
+//                post-RoPE / pre-GQA into the per-sequence KV cache
+// Activations are bf16; intermediate arithmetic is fp32 with bf16 rounding at the
+// points where the reference's bf16 tensors are materialised.
+#include "common.h"
+
+namespace lollm {
+
+template <int THREADS>
+__device__ __forceinline__ float block_sum_f(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < THREADS / 64; ++w) t += red[w];
+  return t;
+}
+
+// One 256-thread workgroup per row; H % 8 == 0, vector loads of 8 bf16.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ h,
+                                                      uint16_t* __restrict__ x_out,
+                                                      const uint16_t* __restrict__ w,
+                                                      uint16_t* __restrict__ y, int H, float eps) {
+  __shared__ float red[4];
+  const size_t row = blockIdx.x;
+  const uint4* x4 = reinterpret_cast<const uint4*>(x + row * H);
+  const uint4* h4 = h ? reinterpret_cast<const uint4*>(h + row * H) : nullptr;
+  const int n8 = H / 8;
+  constexpr int MAXV = 4;  // H <= 8192
+  float v[MAXV][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int c = threadIdx.x + i * 256;
+    if (c < n8) {
+      uint4 u = x4[c];
+      uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+      uint32_t hd[4] = {0, 0, 0, 0};
+      if (h4) { uint4 hv = h4[c]; hd[0] = hv.x; hd[1] = hv.y; hd[2] = hv.z; hd[3] = hv.w; }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float f = __uint_as_float((e & 1 ? wd[e >> 1] & 0xffff0000u : wd[e >> 1] << 16));
+        if (h4) f = round_bf16(f + __uint_as_float((e & 1 ? hd[e >> 1] & 0xffff0000u : hd[e >> 1] << 16)));
+        v[i][e] = f;
+        ss += f * f;
+      }
+      if (h4 && x_out) {
+        uint4 o;
+        o.x = f32_to_bf16(v[i][0]) | ((uint32_t)f32_to_bf16(v[i][1]) << 16);
+        o.y = f32_to_bf16(v[i][2]) | ((uint32_t)f32_to_bf16(v[i][3]) << 16);
+        o.z = f32_to_bf16(v[i][4]) | ((uint32_t)f32_to_bf16(v[i][5]) << 16);
+        o.w = f32_to_bf16(v[i][6]) | ((uint32_t)f32_to_bf16(v[i][7]) << 16);
+        reinterpret_cast<uint4*>(x_out + row * H)[c] = o;
+      }
+    }
+  }
+  const float r = rsqrtf(block_sum_f<256>(ss, red) / (float)H + eps);
+  const uint4* w4 = reinterpret_cast<const uint4*>(w);
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int c = threadIdx.x + i * 256;
+    if (c < n8) {
+      uint4 wu = w4[c];
+      uint32_t wd[4] = {wu.x, wu.y, wu.z, wu.w};
+      uint32_t od[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float w0 = __uint_as_float(wd[e >> 1] << 16), w1 = __uint_as_float(wd[e >> 1] & 0xffff0000u);
+        od[e >> 1] = f32_to_bf16(v[i][e] * r * (1.f + w0)) | ((uint32_t)f32_to_bf16(v[i][e + 1] * r * (1.f + w1)) << 16);
+      }
+      reinterpret_cast<uint4*>(y + row * H)[c] = make_uint4(od[0], od[1], od[2], od[3]);
+    }
+  }
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
+
+// out[r, j] = bf16(bf16(silu(g)) * u) with g = gu[r, j], u = gu[r, F + j]
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ gu,
+                                                     uint16_t* __restrict__ out, int F,
+                                                     long long n8) {
+  for (long long i = blockIdx.x * 256LL + threadIdx.x; i < n8; i += (long long)gridDim.x * 256) {
+    const long long r = i / (F / 8), c = i % (F / 8);
+    const uint4 g = reinterpret_cast<const uint4*>(gu + r * 2 * F)[c];
+    const uint4 u = reinterpret_cast<const uint4*>(gu + r * 2 * F + F)[c];
+    const uint32_t gd[4] = {g.x, g.y, g.z, g.w}, ud[4] = {u.x, u.y, u.z, u.w};
+    uint32_t od[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float g0 = __uint_as_float(gd[k] << 16), g1 = __uint_as_float(gd[k] & 0xffff0000u);
+      const float u0 = __uint_as_float(ud[k] << 16), u1 = __uint_as_float(ud[k] & 0xffff0000u);
+      od[k] = f32_to_bf16(round_bf16(silu_f(g0)) * u0) |
+              ((uint32_t)f32_to_bf16(round_bf16(silu_f(g1)) * u1) << 16);
+    }
+    reinterpret_cast<uint4*>(out + r * F)[c] = make_uint4(od[0], od[1], od[2], od[3]);
+  }
+}
+
+// One 256-thread workgroup per (token, head slot): slots [0, Hq) are query heads,
+// [Hq, Hq + Hkv) key heads, [Hq + Hkv, Hq + 2 Hkv) value heads.  D == 256: one
+// element per thread.
+__global__ __launch_bounds__(256) void attn_prologue_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qn_w,
+    const uint16_t* __restrict__ kn_w, const float* __restrict__ inv_freq,
+    const int32_t* __restrict__ lengths, const int32_t* __restrict__ rope_pos, int T, int Hq,
+    int Hkv, int rd, float eps,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ gate_out, uint16_t* __restrict__ kc,
+    uint16_t* __restrict__ vc, int max_len) {
+  constexpr int D = 256;
+  __shared__ float red[4];
+  __shared__ float xs[D];
+  const int bt = blockIdx.x, slot = blockIdx.y, d = threadIdx.x;
+  const int b = bt / T, t = bt % T;
+  const long long row_w = (long long)Hq * 2 * D + 2LL * Hkv * D;
+  const uint16_t* src = qkv + (long long)bt * row_w;
+  const int pos = lengths[b] + t;                          // cache row
+  const int rpos = (rope_pos ? rope_pos[b] : lengths[b]) + t;  // RoPE position
+  if (slot >= Hq + Hkv) {  // value head: plain copy into the cache
+    const int kvh = slot - Hq - Hkv;
+    if (pos >= 0 && pos < max_len)
+      vc[(((long long)b * Hkv + kvh) * max_len + pos) * D + d] = src[(long long)Hq * 2 * D + Hkv * D + kvh * D + d];
+    return;
+  }
+  const bool is_q = slot < Hq;
+  const uint16_t* xin = is_q ? src + (long long)slot * 2 * D : src + (long long)Hq * 2 * D + (slot - Hq) * D;
+  if (is_q) gate_out[((long long)bt * Hq + slot) * D + d] = src[(long long)slot * 2 * D + D + d];
+  const float x = bf16_to_f32(xin[d]);
+  const float r = rsqrtf(block_sum_f<256>(x * x, red) / (float)D + eps);
+  const float wv = bf16_to_f32((is_q ? qn_w : kn_w)[d]);
+  const float xn = round_bf16(x * r * (1.f + wv));  // QK-norm output (bf16 tensor)
+  xs[d] = xn;
+  __syncthreads();
+  float y = xn;
+  if (d < rd) {
+    const int half = rd / 2, i = d % half;
+    const float ang = (float)rpos * inv_freq[i];
+    const float c = round_bf16(cosf(ang)), s = round_bf16(sinf(ang));
+    const float rot = d < half ? -xs[d + half] : xs[d - half];
+    y = round_bf16(round_bf16(xn * c) + round_bf16(rot * s));
+  }
+  if (is_q) {
+    q_out[((long long)bt * Hq + slot) * D + d] = f32_to_bf16(y);
+  } else if (pos >= 0 && pos < max_len) {
+    const int kvh = slot - Hq;
+    kc[(((long long)b * Hkv + kvh) * max_len + pos) * D + d] = f32_to_bf16(y);
+  }
+}
+
+// One workgroup per sequence: the bookkeeping that ends a speculative step.
+__global__ __launch_bounds__(256) void spec_commit_kernel(
+    const int32_t* __restrict__ verify_ids, const int32_t* __restrict__ n_acc,
+    const int32_t* __restrict__ next_tok, int32_t* lengths, int32_t* rec_slot, int32_t* conv_off,
+    int32_t* pending, int32_t* out_tokens, int32_t* out_count, int cap,
+    const uint16_t* __restrict__ hidden, uint16_t* __restrict__ h_last, int H, int T, int S,
+    int W, long long* offset) {
+  const int b = blockIdx.x;
+  int a = n_acc[b];
+  a = a < 0 ? 0 : (a > T - 1 ? T - 1 : a);
+  const uint4* src = reinterpret_cast<const uint4*>(hidden + ((size_t)b * T + a) * H);
+  uint4* dst = reinterpret_cast<uint4*>(h_last + (size_t)b * H);
+  for (int i = threadIdx.x; i < H / 8; i += 256) dst[i] = src[i];
+  if (threadIdx.x == 0) {
+    lengths[b] += a + 1;                           // keep a + 1 of the T positions
+    rec_slot[b] = (rec_slot[b] >= S ? 0 : S) + a;  // the half the forward wrote
+    conv_off[b] = (conv_off[b] >= W ? 0 : W) + a + 1;
+    const int c = out_count[b];
+    for (int i = 0; i <= a; ++i)
+      if (c + i < cap) out_tokens[(size_t)b * cap + c + i] = verify_ids[b * T + i];
+    out_count[b] = c + a + 1;
+    pending[b] = next_tok[b];
+    if (b == 0) offset[0] += 1;
+  }
+}
+
+}  // namespace lollm
+
+using namespace lollm;
+
+LOLLM_API int lollm_rmsnorm(const void* x, const void* residual, void* x_out, const void* w,
+                            void* y, int rows, int H, float eps, void* stream) {
+  if (!x || !w || !y || rows <= 0 || H <= 0) return LOLLM_EINVAL;
+  if (H % 8 || H > 8192) return LOLLM_EUNSUPPORTED;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, (const uint16_t*)residual, (uint16_t*)x_out,
+                     (const uint16_t*)w, (uint16_t*)y, H, eps);
+  return launch_status();
+}
+
+LOLLM_API int lollm_swiglu(const void* gate_up, void* out, int rows, int F, void* stream) {
+  if (!gate_up || !out || rows <= 0 || F <= 0) return LOLLM_EINVAL;
+  if (F % 8) return LOLLM_EUNSUPPORTED;
+  const long long n8 = (long long)rows * (F / 8);
+  const long long blocks = (n8 + 255) / 256;
+  hipLaunchKernelGGL(swiglu_kernel, dim3(blocks < 4096 ? blocks : 4096), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)gate_up, (uint16_t*)out, F, n8);
+  return launch_status();
+}
+
+LOLLM_API int lollm_attn_prologue(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                                  const float* inv_freq, const int32_t* lengths,
+                                  const int32_t* rope_pos, int B, int T,
+                                  int Hq, int Hkv, int D, int rotary_dim, float eps, void* q_out,
+                                  void* gate_out, void* k_cache, void* v_cache, int max_len,
+                                  void* stream) {
+  if (!qkv || !q_norm_w || !k_norm_w || !lengths || !q_out || !gate_out || !k_cache || !v_cache)
+    return LOLLM_EINVAL;
+  if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || max_len <= 0) return LOLLM_EINVAL;
+  if (D != 256 || rotary_dim < 0 || rotary_dim > D || rotary_dim % 2) return LOLLM_EUNSUPPORTED;
+  if (rotary_dim > 0 && !inv_freq) return LOLLM_EINVAL;
+  hipLaunchKernelGGL(attn_prologue_kernel, dim3(B * T, Hq + 2 * Hkv), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)qkv, (const uint16_t*)q_norm_w,
+                     (const uint16_t*)k_norm_w, inv_freq, lengths, rope_pos, T, Hq, Hkv,
+                     rotary_dim, eps,
+                     (uint16_t*)q_out, (uint16_t*)gate_out, (uint16_t*)k_cache,
+                     (uint16_t*)v_cache, max_len);
+  return launch_status();
+}
+
+LOLLM_API int lollm_spec_commit(const int32_t* verify_ids, const int32_t* n_accepted,
+                                const int32_t* next_token, int32_t* lengths, int32_t* rec_slot,
+                                int32_t* conv_off, int32_t* pending, int32_t* out_tokens,
+                                int32_t* out_count, int out_cap, const void* hidden, void* h_last,
+                                int B, int T, int H, int slots, int win_rows, long long* offset,
+                                void* stream) {
+  if (!verify_ids || !n_accepted || !next_token || !lengths || !rec_slot || !conv_off ||
+      !pending || !out_tokens || !out_count || !hidden || !h_last || !offset)
+    return LOLLM_EINVAL;
+  if (B <= 0 || T <= 0 || H <= 0 || out_cap <= 0 || slots < T || win_rows <= 0) return LOLLM_EINVAL;
+  if (H % 8) return LOLLM_EUNSUPPORTED;
+  hipLaunchKernelGGL(spec_commit_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, verify_ids,
+                     n_accepted, next_token, lengths, rec_slot, conv_off, pending, out_tokens,
+                     out_count, out_cap, (const uint16_t*)hidden, (uint16_t*)h_last, H, T, slots,
+                     win_rows, offset);
+  return launch_status();
+}

@@ -1,0 +1,285 @@
+// The Gated DeltaNet mixer of one decoder layer, fused from the in_proj outputs to the
+// gated-norm output (gfx950).  Reference: GatedDeltaNet.forward, src/qwen3_5/blocks.py
+// :288-329, i.e. steps 2-6 below; the projections before and out_proj after are GEMMs.
+//
+// Per (sequence b, v-head h) workgroup of 256 threads, tokens in chunks of GL_TC:
+//   1. causal depthwise conv (kernel K, no bias) over [conv state | raw x] for the
+//      384 channels this head reads (q and k of qk-head h / v_per_k, v of head h),
+//      then SiLU (blocks.py:268-286; the new conv state is the last K-1 RAW inputs);
+//   2. beta = sigmoid(b) in bf16, g = -exp(A_log) softplus(a + dt_bias) in fp32
+//      (blocks.py:313-314);
+//   3. the recurrent delta rule with in-kernel L2 norm of q, k and q scaled by
+//      Dk^-0.5 (blocks.py:116-144), the 128 x 128 fp32 state held in registers exactly
+//      as in gdn_verify.hip (wave = 32-column slab, lane = 16 rows x 4 columns);
+//      the state after every position can be written as a snapshot (O(1) rollback);
+//   4. the gated RMSNorm per v-head (blocks.py:38-51,324) and the bf16 output row.
+// State lives in ping-pong buffers selected per sequence on the device: the conv
+// window buffer has two halves of W rows and the recurrent-state buffer two halves of
+// S snapshot slots; a call reads the half holding the committed state (conv_off[b],
+// rec_slot[b]) and writes the other one, so rolling back to `a` accepted drafts is
+// just new indices (other half + a) and no host-side state changes between steps.
+#include "common.h"
+
+namespace lollm {
+
+constexpr int GL_DK = 128;
+constexpr int GL_TC = 8;         // tokens per chunk
+constexpr int GL_KMAX = 4;       // conv kernel width (linear_conv_kernel_dim)
+constexpr int GL_CH = 3 * GL_DK; // q, k, v channels per head
+
+struct GdnLayerArgs {
+  const uint16_t* proj;      // (B, T, P): [qkv (C) | z (value_dim) | b (Hv) | a (Hv)]
+  const uint16_t* conv_w;    // (C, K)
+  const float* A_log;        // (Hv)
+  const float* dt_bias;      // (Hv)
+  const uint16_t* norm_w;    // (Dv)
+  uint16_t* win;             // (B, 2 W, C) conv windows
+  const int32_t* conv_off;   // (B) first committed-state row in win
+  float* rec;                // (B, 2 S, Hv, Dk, Dv) recurrent-state snapshots
+  const int32_t* rec_slot;   // (B) committed-state slot in rec
+  uint16_t* out;             // (B, T, value_dim)
+  long long P;
+  int T, Hk, Hv, C, key_dim, value_dim, K;
+  int W, S, fresh;
+  float eps;
+};
+
+__device__ __forceinline__ float silu_g(float x) { return x / (1.f + __expf(-x)); }
+
+__device__ __forceinline__ float softplus_g(float x) {  // torch: linear above 20
+  return x > 20.f ? x : log1pf(__expf(x));
+}
+
+__global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
+  __shared__ float xin[GL_KMAX - 1 + GL_TC][GL_CH];  // conv inputs (state rows first)
+  __shared__ float act[GL_TC][GL_CH];                // q | k | v after conv + SiLU
+  __shared__ float obuf[GL_TC][GL_DK];               // scan outputs
+  __shared__ float gb[GL_TC][2];                     // g, beta
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cg = lane & 7, rg = lane >> 3;
+  const int b = blockIdx.x / a.Hv, h = blockIdx.x % a.Hv;
+  const int vpk = a.Hv / a.Hk, hk = h / vpk;
+  const bool write_qk = (h % vpk) == 0;  // q/k window channels are shared by vpk heads
+  const int row0 = rg * 16, col0 = wave * 32 + cg * 4;
+  const int Km1 = a.K - 1;
+  const bool full_window = Km1 + a.T <= a.W;
+  const bool snaps = a.T <= a.S;
+  constexpr size_t SS = (size_t)GL_DK * GL_DK;
+  int off = a.conv_off[b];
+  off = off < 0 ? 0 : (off > 2 * a.W - Km1 ? 2 * a.W - Km1 : off);  // never out of range
+  const int wbase = off >= a.W ? 0 : a.W;          // window half written by this call
+  int slot = a.rec_slot[b];
+  slot = slot < 0 ? 0 : (slot >= 2 * a.S ? 2 * a.S - 1 : slot);
+  const int rbase = slot >= a.S ? 0 : a.S;         // snapshot half written by this call
+  const size_t win_b = (size_t)b * 2 * a.W;
+
+  auto gchan = [&](int lc) {  // local channel -> global conv channel
+    return lc < GL_DK ? hk * GL_DK + lc
+                      : (lc < 2 * GL_DK ? a.key_dim + hk * GL_DK + (lc - GL_DK)
+                                        : 2 * a.key_dim + h * GL_DK + (lc - 2 * GL_DK));
+  };
+  auto owns = [&](int lc) { return lc >= 2 * GL_DK || write_qk; };
+
+  // ---- initial conv state ----
+  for (int i = tid; i < Km1 * GL_CH; i += 256) {
+    const int r = i / GL_CH, lc = i % GL_CH, c = gchan(lc);
+    const uint16_t v = a.win[(win_b + off + r) * a.C + c];
+    xin[r][lc] = bf16_to_f32(v);
+    if (full_window && owns(lc)) a.win[(win_b + wbase + r) * a.C + c] = v;
+  }
+  // ---- recurrent state ----
+  float S[16][4];
+  if (!a.fresh) {
+    const float* s0 = a.rec + ((size_t)(b * 2 * a.S + slot) * a.Hv + h) * SS;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float4 f = *reinterpret_cast<const float4*>(s0 + (size_t)(row0 + r) * GL_DK + col0);
+      S[r][0] = f.x; S[r][1] = f.y; S[r][2] = f.z; S[r][3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) S[r][0] = S[r][1] = S[r][2] = S[r][3] = 0.f;
+  }
+  const float a_log = a.A_log[h], dtb = a.dt_bias[h];
+  const float qscale = rsqrtf((float)GL_DK);
+
+  for (int t0 = 0; t0 < a.T; t0 += GL_TC) {
+    const int tc = min(GL_TC, a.T - t0);
+    __syncthreads();  // previous chunk fully consumed
+    // 1a. raw inputs of this chunk (+ window copy)
+    for (int i = tid; i < tc * GL_CH; i += 256) {
+      const int r = i / GL_CH, lc = i % GL_CH, c = gchan(lc);
+      const uint16_t v = a.proj[((size_t)b * a.T + t0 + r) * a.P + c];
+      xin[Km1 + r][lc] = bf16_to_f32(v);
+      if (full_window && owns(lc)) a.win[(win_b + wbase + Km1 + t0 + r) * a.C + c] = v;
+    }
+    if (tid < tc) {
+      const size_t base = ((size_t)b * a.T + t0 + tid) * a.P + a.C + a.value_dim;
+      const float bb = bf16_to_f32(a.proj[base + h]);
+      const float aa = bf16_to_f32(a.proj[base + a.Hv + h]);
+      gb[tid][0] = -__expf(a_log) * softplus_g(aa + dtb);
+      gb[tid][1] = round_bf16(1.f / (1.f + __expf(-bb)));
+    }
+    __syncthreads();
+    // 1b. conv + SiLU (bf16 rounding at the conv output and at the SiLU output)
+    for (int i = tid; i < tc * GL_CH; i += 256) {
+      const int r = i / GL_CH, lc = i % GL_CH, c = gchan(lc);
+      float acc = 0.f;
+      for (int tau = 0; tau < a.K; ++tau)
+        acc = fmaf(bf16_to_f32(a.conv_w[(size_t)c * a.K + tau]), xin[r + tau][lc], acc);
+      act[r][lc] = round_bf16(silu_g(round_bf16(acc)));
+    }
+    __syncthreads();
+    // carry the last K-1 raw inputs as the next chunk's state
+    {
+      float keep[(GL_KMAX - 1) * GL_CH / 256 + 1];
+      int n = 0;
+      for (int i = tid; i < Km1 * GL_CH; i += 256) keep[n++] = xin[tc + i / GL_CH][i % GL_CH];
+      __syncthreads();
+      n = 0;
+      for (int i = tid; i < Km1 * GL_CH; i += 256) xin[i / GL_CH][i % GL_CH] = keep[n++];
+    }
+    // 2. the scan over the chunk
+    for (int i = 0; i < tc; ++i) {
+      const int t = t0 + i;
+      float kr[16], qr[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        qr[r] = act[i][row0 + r];
+        kr[r] = act[i][GL_DK + row0 + r];
+      }
+      float pa[4] = {0.f, 0.f, 0.f, 0.f}, pb[4] = {0.f, 0.f, 0.f, 0.f};
+      float pkq = 0.f, pkk = 0.f, pqq = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          pa[c] = fmaf(S[r][c], kr[r], pa[c]);
+          pb[c] = fmaf(S[r][c], qr[r], pb[c]);
+        }
+        pkq = fmaf(kr[r], qr[r], pkq);
+        pkk = fmaf(kr[r], kr[r], pkk);
+        pqq = fmaf(qr[r], qr[r], pqq);
+      }
+#pragma unroll
+      for (int m = 8; m < 64; m <<= 1) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          pa[c] += wave_xor(pa[c], m);
+          pb[c] += wave_xor(pb[c], m);
+        }
+        pkq += wave_xor(pkq, m);
+        pkk += wave_xor(pkk, m);
+        pqq += wave_xor(pqq, m);
+      }
+      const float rk = rsqrtf(pkk + 1e-6f);
+      const float rq = rsqrtf(pqq + 1e-6f) * qscale;
+      const float kq = pkq * rk * rq;
+      const float gam = __expf(gb[i][0]), bet = gb[i][1];
+      float d[4], o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float vv = act[i][2 * GL_DK + col0 + c];
+        d[c] = (vv - gam * pa[c] * rk) * bet;
+        o[c] = gam * pb[c] * rq + d[c] * kq;
+      }
+      if (rg == 0) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) obuf[i][col0 + c] = o[c];
+      }
+      float* snap = snaps ? a.rec + ((size_t)(b * 2 * a.S + rbase + t) * a.Hv + h) * SS : nullptr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float k_r = kr[r] * rk;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) S[r][c] = fmaf(k_r, d[c], gam * S[r][c]);
+        if (snap)
+          store_nt(snap + (size_t)(row0 + r) * GL_DK + col0,
+                   make_uint4(__float_as_uint(S[r][0]), __float_as_uint(S[r][1]),
+                              __float_as_uint(S[r][2]), __float_as_uint(S[r][3])));
+      }
+    }
+    __syncthreads();
+    // 3. gated RMSNorm of each token's 128 outputs: 16 threads per token, 8 columns each
+    {
+      const int i = tid >> 4, part = tid & 15;
+      float ov[8], ss = 0.f;
+      if (i < tc) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ov[e] = round_bf16(obuf[i][part * 8 + e]);  // core output is a bf16 tensor
+          ss += ov[e] * ov[e];
+        }
+      }
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+      if (i < tc) {
+        const float r = rsqrtf(ss / (float)GL_DK + a.eps);
+        const size_t zb = ((size_t)b * a.T + t0 + i) * a.P + a.C + (size_t)h * GL_DK + part * 8;
+        const uint4 zu = *reinterpret_cast<const uint4*>(a.proj + zb);
+        const uint4 wu = *reinterpret_cast<const uint4*>(a.norm_w + part * 8);
+        const uint32_t zd[4] = {zu.x, zu.y, zu.z, zu.w}, wd[4] = {wu.x, wu.y, wu.z, wu.w};
+        uint32_t od[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          float y2[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int ee = e + u;
+            const float z = __uint_as_float(ee & 1 ? zd[ee >> 1] & 0xffff0000u : zd[ee >> 1] << 16);
+            const float w = __uint_as_float(ee & 1 ? wd[ee >> 1] & 0xffff0000u : wd[ee >> 1] << 16);
+            const float hn = round_bf16(ov[ee] * r);
+            y2[u] = round_bf16(w * hn) * silu_g(z);
+          }
+          od[e >> 1] = f32_to_bf16(y2[0]) | ((uint32_t)f32_to_bf16(y2[1]) << 16);
+        }
+        *reinterpret_cast<uint4*>(a.out + ((size_t)b * a.T + t0 + i) * a.value_dim +
+                                  (size_t)h * GL_DK + part * 8) = make_uint4(od[0], od[1], od[2], od[3]);
+      }
+    }
+  }
+  // ---- long calls: final state in slot 0 and the final conv state in rows [0, K-1) ----
+  if (!snaps) {
+    float* sf = a.rec + ((size_t)(b * 2 * a.S + rbase) * a.Hv + h) * SS;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      *reinterpret_cast<float4*>(sf + (size_t)(row0 + r) * GL_DK + col0) =
+          make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
+  }
+  if (!full_window) {
+    __syncthreads();
+    for (int i = tid; i < Km1 * GL_CH; i += 256) {
+      const int r = i / GL_CH, lc = i % GL_CH;
+      if (owns(lc)) a.win[(win_b + wbase + r) * a.C + gchan(lc)] = f32_to_bf16(xin[r][lc]);
+    }
+  }
+}
+
+}  // namespace lollm
+
+using namespace lollm;
+
+LOLLM_API int lollm_gdn_layer(const void* proj, long long proj_stride, const void* conv_w,
+                              const float* A_log, const float* dt_bias, const void* norm_w,
+                              void* win, const int32_t* conv_off, int win_rows, float* rec,
+                              const int32_t* rec_slot, int slots, int fresh, void* out, int B,
+                              int T, int Hk, int Hv, int Dk, int Dv, int conv_kernel, float eps,
+                              void* stream) {
+  if (!proj || !conv_w || !A_log || !dt_bias || !norm_w || !win || !conv_off || !rec ||
+      !rec_slot || !out)
+    return LOLLM_EINVAL;
+  if (B <= 0 || T <= 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return LOLLM_EINVAL;
+  if (Dk != GL_DK || Dv != GL_DK || conv_kernel < 1 || conv_kernel > GL_KMAX) return LOLLM_EUNSUPPORTED;
+  if (win_rows < conv_kernel - 1 || slots < 1) return LOLLM_EINVAL;
+  const int key_dim = Hk * Dk, value_dim = Hv * Dv, C = 2 * key_dim + value_dim;
+  if (proj_stride < (long long)C + value_dim + 2 * Hv || proj_stride % 8) return LOLLM_EINVAL;
+  GdnLayerArgs a;
+  a.proj = (const uint16_t*)proj; a.conv_w = (const uint16_t*)conv_w; a.A_log = A_log;
+  a.dt_bias = dt_bias; a.norm_w = (const uint16_t*)norm_w; a.win = (uint16_t*)win;
+  a.conv_off = conv_off; a.rec = rec; a.rec_slot = rec_slot; a.out = (uint16_t*)out;
+  a.P = proj_stride; a.T = T; a.Hk = Hk; a.Hv = Hv; a.C = C; a.key_dim = key_dim;
+  a.value_dim = value_dim; a.K = conv_kernel; a.W = win_rows; a.S = slots; a.fresh = fresh ? 1 : 0;
+  a.eps = eps;
+  hipLaunchKernelGGL(gdn_layer_kernel, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);
+  return launch_status();
+}

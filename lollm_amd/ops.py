@@ -238,3 +238,93 @@ def philox_u24(seed, offset, rows, slots, device="cuda"):
     rc = _lib.lib().lollm_philox_uniform_u24(seed, offset, rows, slots, _ptr(out), _stream())
     _lib.check(rc, "lollm_philox_uniform_u24")
     return out
+
+
+# ------------------------------------------------------------------------------------
+# fused decoder-layer kernels
+# ------------------------------------------------------------------------------------
+def rmsnorm(x, w, eps, residual=None, x_out=None, out=None):
+    """y = RMSNorm_{1+w}(x) or, with residual, x_out = x + residual, y = norm(x_out).
+    x: (..., H) bf16.  Returns y, or (y, x_out) when residual is given."""
+    H = x.shape[-1]
+    rows = x.numel() // H
+    _need(x, "x", torch.bfloat16)
+    _need(w, "w", torch.bfloat16, (H,))
+    if residual is not None:
+        _need(residual, "residual", torch.bfloat16, tuple(x.shape))
+        if x_out is None:
+            x_out = torch.empty_like(x)
+    if out is None:
+        out = torch.empty_like(x)
+    rc = _lib.lib().lollm_rmsnorm(_ptr(x), _ptr(residual), _ptr(x_out), _ptr(w), _ptr(out), rows,
+                                  H, float(eps), _stream())
+    _lib.check(rc, "lollm_rmsnorm")
+    return (out, x_out) if residual is not None else out
+
+
+def swiglu(gate_up, out=None):
+    """gate_up (..., 2F) bf16 -> (..., F)."""
+    F2 = gate_up.shape[-1]
+    rows = gate_up.numel() // F2
+    _need(gate_up, "gate_up", torch.bfloat16)
+    if out is None:
+        out = torch.empty(*gate_up.shape[:-1], F2 // 2, dtype=torch.bfloat16, device=gate_up.device)
+    rc = _lib.lib().lollm_swiglu(_ptr(gate_up), _ptr(out), rows, F2 // 2, _stream())
+    _lib.check(rc, "lollm_swiglu")
+    return out
+
+
+def attn_prologue(qkv, q_norm_w, k_norm_w, inv_freq, lengths, B, T, Hq, Hkv, D, rotary_dim, eps,
+                  k_cache, v_cache, q_out=None, gate_out=None, rope_pos=None):
+    _need(qkv, "qkv", torch.bfloat16)
+    if qkv.numel() != B * T * (Hq * 2 * D + 2 * Hkv * D):
+        raise ValueError("qkv has the wrong size")
+    _need(lengths, "lengths", torch.int32, (B,))
+    _need(k_cache, "k_cache", torch.bfloat16)
+    _need(v_cache, "v_cache", torch.bfloat16, tuple(k_cache.shape))
+    max_len = k_cache.shape[2]
+    if q_out is None:
+        q_out = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=qkv.device)
+    if gate_out is None:
+        gate_out = torch.empty(B, T, Hq * D, dtype=torch.bfloat16, device=qkv.device)
+    rc = _lib.lib().lollm_attn_prologue(
+        _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(inv_freq), _ptr(lengths), _ptr(rope_pos),
+        B, T, Hq, Hkv,
+        D, rotary_dim, float(eps), _ptr(q_out), _ptr(gate_out), _ptr(k_cache), _ptr(v_cache),
+        max_len, _stream())
+    _lib.check(rc, "lollm_attn_prologue")
+    return q_out, gate_out
+
+
+def gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, fresh, B, T,
+              Hk, Hv, D, conv_kernel, eps, out=None):
+    """Fused GDN mixer (include/lollm_amd.h).  proj (B, T, P) bf16; win (B, 2W,
+    conv_dim) bf16; rec (B, 2S, Hv, D, D) fp32; conv_off / rec_slot (B,) int32."""
+    P = proj.shape[-1]
+    _need(proj, "proj", torch.bfloat16)
+    _need(win, "win", torch.bfloat16)
+    _need(rec, "rec", torch.float32)
+    _need(conv_off, "conv_off", torch.int32, (B,))
+    _need(rec_slot, "rec_slot", torch.int32, (B,))
+    if win.shape[0] != B or win.shape[1] % 2 or rec.shape[0] != B or rec.shape[1] % 2:
+        raise ValueError("win / rec must hold two halves per sequence")
+    value_dim = Hv * D
+    if out is None:
+        out = torch.empty(B, T, value_dim, dtype=torch.bfloat16, device=proj.device)
+    rc = _lib.lib().lollm_gdn_layer(
+        _ptr(proj), P, _ptr(conv_w), _ptr(A_log), _ptr(dt_bias), _ptr(norm_w), _ptr(win),
+        _ptr(conv_off), win.shape[1] // 2, _ptr(rec), _ptr(rec_slot), rec.shape[1] // 2,
+        int(bool(fresh)), _ptr(out), B, T, Hk, Hv, D, D, conv_kernel, float(eps), _stream())
+    _lib.check(rc, "lollm_gdn_layer")
+    return out
+
+
+def spec_commit(verify_ids, n_accepted, next_token, lengths, rec_slot, conv_off, pending,
+                out_tokens, out_count, hidden, h_last, offset, slots, win_rows):
+    B, T = verify_ids.shape
+    H = hidden.shape[-1]
+    rc = _lib.lib().lollm_spec_commit(
+        _ptr(verify_ids), _ptr(n_accepted), _ptr(next_token), _ptr(lengths), _ptr(rec_slot),
+        _ptr(conv_off), _ptr(pending), _ptr(out_tokens), _ptr(out_count), out_tokens.shape[1],
+        _ptr(hidden), _ptr(h_last), B, T, H, slots, win_rows, _ptr(offset), _stream())
+    _lib.check(rc, "lollm_spec_commit")

@@ -1,0 +1,111 @@
+"""Qwen3.5 decoder blocks on the MI355X kernels.
+
+Each block keeps the reference block's parameters (src/qwen3_5/blocks.py:186-342) but
+stores them the way the verify step consumes them: projections that read the same
+input are concatenated into one GEMM weight (GDN in_proj_qkv|z|b|a, attention
+q|k|v, MLP gate|up), so a layer issues 4 GEMMs (hipBLASLt via torch) plus fused HIP
+kernels for everything between them.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from .. import ops
+from .config import Qwen3_5Config
+
+
+def _cat_rows(*ws):
+    return torch.cat([w.reshape(w.shape[0], -1) for w in ws], 0).contiguous()
+
+
+class RMSNorm:
+    """(1 + w) RMSNorm in fp32 (blocks.py:23-35); optionally fused with the residual
+    add that precedes it in the decoder (modeling_qwen3_5.py:59-60)."""
+
+    def __init__(self, weight, eps):
+        self.weight = weight.to(torch.bfloat16).contiguous()
+        self.eps = eps
+
+    def __call__(self, x, residual=None):
+        x = x.contiguous()
+        if residual is None:
+            return ops.rmsnorm(x, self.weight, self.eps)
+        return ops.rmsnorm(x, self.weight, self.eps, residual=residual.contiguous())
+
+
+class MLP:
+    """SwiGLU (blocks.py:332-342): gate|up as one GEMM, fused silu*up, down."""
+
+    def __init__(self, gate, up, down):
+        self.w_gu = _cat_rows(gate, up)
+        self.w_down = down.contiguous()
+
+    def __call__(self, x):
+        return F.linear(ops.swiglu(F.linear(x, self.w_gu)), self.w_down)
+
+
+class GatedDeltaNet:
+    """GDN mixer (blocks.py:239-329): one in-projection GEMM, the fused conv / gating /
+    scan / gated-norm kernel (lollm_gdn_layer), out_proj."""
+
+    def __init__(self, cfg: Qwen3_5Config, W: dict, p: str):
+        self.cfg = cfg
+        Hv = cfg.linear_num_value_heads
+        w = [W[p + "in_proj_qkv.weight"], W[p + "in_proj_z.weight"], W[p + "in_proj_b.weight"],
+             W[p + "in_proj_a.weight"]]
+        rows = cfg.conv_dim + cfg.value_dim + 2 * Hv
+        pad = (-rows) % 8                      # keep the projection row 16-byte aligned
+        if pad:
+            w.append(torch.zeros(pad, cfg.hidden_size, dtype=w[0].dtype, device=w[0].device))
+        self.w_in = _cat_rows(*w)
+        self.conv_w = W[p + "conv1d.weight"].reshape(cfg.conv_dim, -1).to(torch.bfloat16).contiguous()
+        self.A_log = W[p + "A_log"].float().contiguous()
+        self.dt_bias = W[p + "dt_bias"].float().contiguous()
+        self.norm_w = W[p + "norm.weight"].to(torch.bfloat16).contiguous()
+        self.out_proj = W[p + "out_proj.weight"].contiguous()
+
+    def __call__(self, x, cache, layer):
+        B, T, _ = x.shape
+        cfg = self.cfg
+        proj = F.linear(x, self.w_in)
+        s = cache.layers[layer]
+        core = ops.gdn_layer(proj, self.conv_w, self.A_log, self.dt_bias, self.norm_w, s["win"],
+                             cache.conv_off, s["rec"], cache.rec_slot, cache.fresh, B, T,
+                             cfg.linear_num_key_heads, cfg.linear_num_value_heads,
+                             cfg.linear_key_head_dim, cfg.linear_conv_kernel_dim,
+                             cfg.rms_norm_eps)
+        return F.linear(core, self.out_proj)
+
+
+def rope_inv_freq(rotary_dim, theta, device):
+    """blocks.py:166-168: inv_freq = 1 / theta^(arange(0, rd, 2) / rd) in fp32."""
+    idx = torch.arange(0, rotary_dim, 2, dtype=torch.float32)
+    return (1.0 / (theta ** (idx / rotary_dim))).to(device)
+
+
+class GatedAttention:
+    """Gated full attention (blocks.py:186-236): one q|k|v GEMM, the prologue kernel
+    (gate split, QK-norm, partial RoPE, KV-cache append), the split-K verify
+    attention kernel with the sigmoid gate fused, o_proj."""
+
+    def __init__(self, cfg: Qwen3_5Config, W: dict, p: str, inv_freq):
+        self.cfg = cfg
+        self.w_qkv = _cat_rows(W[p + "q_proj.weight"], W[p + "k_proj.weight"], W[p + "v_proj.weight"])
+        self.q_norm = W[p + "q_norm.weight"].to(torch.bfloat16).contiguous()
+        self.k_norm = W[p + "k_norm.weight"].to(torch.bfloat16).contiguous()
+        self.o_proj = W[p + "o_proj.weight"].contiguous()
+        self.inv_freq = inv_freq
+
+    def __call__(self, x, k_cache, v_cache, lengths, kv_len, rope_pos=None, chunk=512,
+                 workspace=None):
+        B, T, _ = x.shape
+        cfg = self.cfg
+        qkv = F.linear(x, self.w_qkv)
+        q, gate = ops.attn_prologue(qkv, self.q_norm, self.k_norm, self.inv_freq, lengths, B, T,
+                                    cfg.num_attention_heads, cfg.num_key_value_heads,
+                                    cfg.head_dim, cfg.rotary_dim, cfg.rms_norm_eps, k_cache,
+                                    v_cache, rope_pos=rope_pos)
+        o = ops.attn_verify(q, k_cache, v_cache, kv_len, gate, chunk=chunk, workspace=workspace)
+        return F.linear(o, self.o_proj)

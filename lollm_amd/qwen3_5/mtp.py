@@ -1,0 +1,256 @@
+"""MTP draft head, the k-step draft chain and the on-device speculative step.
+
+Reference: src/qwen3_5/mtp.py -- `MTP` (:40-73), `speculate` (:76-89), `generate_mtp`
+(:92-162), `load_mtp` (:171-189).  The reference drafts one token (k = 1) for one
+sequence, deep-copies the cache before the verify pass and re-runs on reject, with
+three host syncs per step.  Here:
+
+  * `MTP.forward(hidden, next_emb, positions=None)` keeps the reference signature and
+    math: fc([RMSNorm(emb) ; RMSNorm(hidden)]) -> one forced full-attention decoder
+    layer with no external cache (attention only inside the call, causal, positions
+    1..L) -> RMSNorm.
+  * The chain to k drafts (not defined by the reference): draft j runs the MTP layer
+    on (hidden input, token) = (h_t, pending) for j = 1 and (m_{j-1}, d_{j-1}) after,
+    where m is the MTP layer output before its final norm; position j; attention over
+    the draft block so far through a small per-step KV cache (rows 0..j-1).  This is
+    exactly the reference's no-cache form applied to the whole block [1..j] (the
+    oracle's `mtp_chain_draft` recomputes it that way and the tests compare), and for
+    k = 1 it is mtp.py:137-138.
+  * `SpecDecoder.step()` runs draft chain -> one verify forward over [pending, d_1..d_k]
+    -> `lollm_spec_accept` (rejection sampling, or argmax matching at temperature 0)
+    -> `lollm_spec_commit` (O(1) rollback, token append, next pending, next hidden)
+    entirely on the device; it can be captured in a HIP graph and replayed.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from .. import ops
+from .blocks import RMSNorm
+from .modeling_qwen3_5 import DecoderLayer, Qwen3_5Model
+from .random_init import weight_shapes
+from .weights import take_weights, to_raw
+
+
+class MTP:
+    def __init__(self, model: Qwen3_5Model, W: dict):
+        cfg = model.cfg
+        self.cfg, self.model = cfg, model
+        eps = cfg.rms_norm_eps
+        self.pre_fc_norm_embedding = RMSNorm(W["mtp.pre_fc_norm_embedding.weight"], eps)
+        self.pre_fc_norm_hidden = RMSNorm(W["mtp.pre_fc_norm_hidden.weight"], eps)
+        self.fc = W["mtp.fc.weight"].contiguous()
+        self.layers = [DecoderLayer(cfg, W, "mtp.layers.0.", "full_attention", model.inv_freq)]
+        self.norm = RMSNorm(W["mtp.norm.weight"], eps)
+
+    def _block(self, hidden, next_emb, k_cache, v_cache, lengths, kv_len, rope_pos, ws):
+        """Returns (MTP layer output before the final norm, normed output)."""
+        x = F.linear(torch.cat([self.pre_fc_norm_embedding(next_emb),
+                                self.pre_fc_norm_hidden(hidden)], -1), self.fc)
+        layer = self.layers[0]
+        h_in = layer.input_layernorm(x)
+        h = layer.self_attn(h_in, k_cache, v_cache, lengths, kv_len, rope_pos=rope_pos,
+                            chunk=128, workspace=ws)
+        y, x = layer.post_attention_layernorm(h, residual=x)
+        m = layer.mlp(y)
+        normed, x = self.norm(m, residual=x)
+        return x, normed
+
+    def scratch_cache(self, B, L):
+        cfg = self.cfg
+        shape = (B, cfg.num_key_value_heads, L, cfg.head_dim)
+        return (torch.zeros(shape, dtype=torch.bfloat16, device=self.model.device),
+                torch.zeros(shape, dtype=torch.bfloat16, device=self.model.device))
+
+    @torch.no_grad()
+    def forward(self, hidden, next_emb, positions=None):
+        """mtp.py:61-73: (B, L, H) -> normalised MTP hidden (B, L, H)."""
+        B, L, _ = hidden.shape
+        dev = self.model.device
+        if positions is None:
+            start = 1
+        else:
+            pos = positions.flatten().tolist()
+            if pos != list(range(pos[0], pos[0] + L)):
+                raise NotImplementedError("MTP positions must be consecutive")
+            start = pos[0]
+        kc, vc = self.scratch_cache(B, L)
+        zeros = torch.zeros(B, dtype=torch.int32, device=dev)
+        kv_len = torch.full((B,), L, dtype=torch.int32, device=dev)
+        rope = torch.full((B,), start, dtype=torch.int32, device=dev)
+        _, normed = self._block(hidden.to(torch.bfloat16).contiguous(),
+                                next_emb.to(torch.bfloat16).contiguous(), kc, vc, zeros, kv_len,
+                                rope, None)
+        return normed
+
+    __call__ = forward
+
+
+@torch.no_grad()
+def speculate(model, mtp: MTP, input_ids):
+    """mtp.py:76-89: MTP logits for position i + 2 given the context up to i + 1."""
+    _, _, hidden = model(input_ids, return_hidden=True)
+    emb = model.model.embed_tokens(input_ids.to(model.device))
+    x = mtp(hidden[:, :-1], emb[:, 1:])
+    return model.lm_head(x)
+
+
+def load_mtp(model, weights: dict, fmt: str, device="cuda", dtype=None) -> MTP:
+    """mtp.py:171-189: strict load of the `mtp.*` tensors; shares embed / lm_head."""
+    cfg = model.cfg
+    names = {k: v for k, v in weight_shapes(cfg, with_mtp=True).items() if k.startswith("mtp.")}
+    names = {to_raw(k, fmt): v for k, v in names.items()}
+    W = take_weights(cfg, weights, names, torch.device(device), dtype or torch.bfloat16,
+                     who="qwen3_5 MTP")
+    return MTP(model, W)
+
+
+class SpecDecoder:
+    """Batched MTP speculative decoding with k drafts per step, device-resident.
+
+    temperature <= 0: greedy (argmax matching; the output equals greedy
+    autoregressive decoding, the invariant of mtp.py:101-103).  temperature > 0:
+    rejection sampling with p = sample_next's distribution (temperature, top-k,
+    top-p) and q one-hot at the argmax draft (draft="argmax", the reference's
+    drafting rule, mtp.py:138) or q = the MTP head's own distribution with sampled
+    drafts (draft="sample")."""
+
+    def __init__(self, model: Qwen3_5Model, mtp: MTP, batch: int, max_len: int, k: int = 3,
+                 temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0, seed: int = 0,
+                 draft: str = "argmax", out_capacity: int = 4096):
+        if draft not in ("argmax", "sample"):
+            raise ValueError("draft must be 'argmax' or 'sample'")
+        self.model, self.mtp, self.k = model, mtp, k
+        self.B = batch
+        self.temperature, self.top_k, self.top_p, self.seed = temperature, top_k, top_p, seed
+        self.draft_mode = draft if temperature > 0 else "argmax"
+        cfg, dev = model.cfg, model.device
+        self.cache = model.new_cache(batch, max_len, spec_slots=k + 1)
+        self.mkc, self.mvc = mtp.scratch_cache(batch, max(k, 1))
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.pending = torch.zeros(batch, **i32)
+        self.h_last = torch.zeros(batch, cfg.hidden_size, dtype=torch.bfloat16, device=dev)
+        self.drafts = torch.zeros(batch, k, **i32)
+        self.n_acc = torch.zeros(batch, **i32)
+        self.next_tok = torch.zeros(batch, **i32)
+        self.out_tokens = torch.zeros(batch, out_capacity, **i32)
+        self.out_count = torch.zeros(batch, **i32)
+        self.offset = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.spec_ws = torch.empty(max(ops._lib.lib().lollm_spec_workspace_bytes(batch, k, 1), 16),
+                                   dtype=torch.uint8, device=dev)
+        self.row_ws = torch.empty(batch * 24, dtype=torch.uint8, device=dev)
+        self.mtp_ws = torch.empty(16, dtype=torch.uint8, device=dev)
+        self.draft_logits = (torch.empty(batch, k, cfg.vocab_size, dtype=torch.bfloat16, device=dev)
+                             if self.draft_mode == "sample" else None)
+        # per-draft-position index tensors (fixed across steps, so a graph can hold them)
+        self.mtp_len = [torch.full((batch,), j, **i32) for j in range(k + 1)]
+        self.graph = None
+        self.steps_done = 0
+
+    # ------------------------------------------------------------------------------
+    @torch.no_grad()
+    def prefill(self, prompts):
+        """prompts (B, L) long, equal lengths.  Runs the prompt through the model
+        (mtp.py:120-122) and samples the first pending token."""
+        logits, _, hidden = self.model(prompts, self.cache, return_hidden=True, logits="last")
+        self.pending.copy_(ops.sample_rows(logits[:, -1].contiguous(), self.temperature,
+                                           self.top_k, self.top_p, self.seed, 0,
+                                           slot=2 * self.k + 2, workspace=self.row_ws))
+        self.h_last.copy_(hidden[:, -1])
+        self.out_count.zero_()
+        self.offset.fill_(1)
+
+    def _draft_chain(self):
+        B, k, model, mtp = self.B, self.k, self.model, self.mtp
+        tok = self.pending
+        h = self.h_last.view(B, 1, -1)
+        for j in range(1, k + 1):
+            emb = model.model.embed_tokens(tok.view(B, 1).long())
+            m, normed = mtp._block(h, emb, self.mkc, self.mvc, self.mtp_len[j - 1],
+                                   self.mtp_len[j], self.mtp_len[j], self.mtp_ws)
+            lg = model.lm_head(normed).view(B, -1)
+            if self.draft_mode == "sample":
+                self.draft_logits[:, j - 1].copy_(lg)
+                d = ops.sample_rows(lg, self.temperature, self.top_k, self.top_p, self.seed, 0,
+                                    slot=k + 1 + j, offset_dev=self.offset, workspace=self.row_ws)
+            else:
+                d = ops.sample_rows(lg, 0.0, workspace=self.row_ws)
+            self.drafts[:, j - 1].copy_(d)
+            tok, h = d, m
+
+    @torch.no_grad()
+    def step(self):
+        """One speculative step: k drafts, one verify pass over 1 + k positions, accept,
+        commit.  Device-only (no host sync)."""
+        B, k, model, cache = self.B, self.k, self.model, self.cache
+        self._draft_chain()
+        verify_ids = torch.cat([self.pending.view(B, 1), self.drafts], 1)
+        hidden, normed = model.hidden_states(verify_ids.long(), cache)
+        logits = model.lm_head(normed)
+        ops.spec_accept(logits, self.draft_logits, self.drafts, self.temperature, self.top_k,
+                        self.top_p, self.seed, 0, offset_dev=self.offset,
+                        workspace=self.spec_ws, n_accepted=self.n_acc, next_token=self.next_tok)
+        ops.spec_commit(verify_ids, self.n_acc, self.next_tok, cache.lengths, cache.rec_slot,
+                        cache.conv_off, self.pending, self.out_tokens, self.out_count,
+                        hidden.contiguous(), self.h_last, self.offset, cache.spec_slots,
+                        cache.win_rows)
+        cache.fresh = False
+
+    def capture(self):
+        """Record step() in a HIP graph (after prefill and at least one eager step);
+        replay with replay().  Capturing executes nothing."""
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.step()
+
+    def replay(self):
+        self.graph.replay()
+
+    @torch.no_grad()
+    def generate(self, n_steps, use_graph=False):
+        for _ in range(n_steps):
+            if use_graph:
+                self.replay()
+            else:
+                self.step()
+            self.steps_done += 1
+
+    def tokens(self):
+        """Committed tokens per sequence (list of lists; host sync)."""
+        cnt = self.out_count.cpu().tolist()
+        out = self.out_tokens.cpu()
+        return [out[b, :min(c, out.shape[1])].tolist() for b, c in enumerate(cnt)]
+
+
+@torch.no_grad()
+def generate_mtp(model, mtp: MTP, ids, decode, stop_ids, device="cuda", *, max_new_tokens=128,
+                 temperature=0.7, top_k=20, top_p=0.8, repetition_penalty=1.1, k=1, seed=0):
+    """Drop-in for the reference's generate_mtp (mtp.py:92-162): yields text pieces.
+    Runs the batched decoder with B = 1 and k drafts (k = 1 by default, as the
+    reference).  A repetition penalty other than 1.0 is not implemented by the
+    on-device sampler and raises."""
+    if repetition_penalty not in (None, 1.0):
+        raise NotImplementedError("repetition_penalty != 1.0 is not supported by the on-device sampler")
+    eos = set(stop_ids)
+    dec = SpecDecoder(model, mtp, 1, len(ids) + max_new_tokens + 2 * k + 8, k=k,
+                      temperature=temperature, top_k=top_k, top_p=top_p, seed=seed,
+                      out_capacity=max_new_tokens + 2 * k + 2)
+    dec.prefill(torch.tensor([ids], device=model.device))
+    generated, prev = [], ""
+    while True:
+        # committed tokens, then the pending one (already final: it is the next
+        # step's first verified position)
+        stream = dec.tokens()[0] + [int(dec.pending[0])]
+        while len(generated) < len(stream):
+            tok = stream[len(generated)]
+            if tok in eos or len(generated) >= max_new_tokens:
+                return
+            generated.append(tok)
+            text = decode(generated)
+            if len(text) > len(prev):
+                yield text[len(prev):]
+                prev = text
+        dec.step()

@@ -452,7 +452,7 @@ def mtp_forward(W, cfg, hidden, next_emb, positions=None):
 
 
 @torch.no_grad()
-def mtp_chain_draft(W, cfg, hidden_last, pending, k):
+def mtp_chain_draft(W, cfg, hidden_last, pending, k, forced=None):
     """The build's k-step draft chain restated in the reference's own no-cache form
     (mtp.py:61-73 with cache=None): draft j runs the MTP block over the whole draft
     block so far -- hidden inputs [h_t, m_1..m_{j-1}], embeddings
@@ -461,7 +461,8 @@ def mtp_chain_draft(W, cfg, hidden_last, pending, k):
     before its final norm.  For k == 1 this is exactly mtp.py:137-138.
 
     hidden_last: (B, 1, H); pending: (B,) long.  Returns drafts (B, k) long and the
-    draft logits (B, k, V)."""
+    draft logits (B, k, V).  `forced` (B, k): feed these tokens forward instead of the
+    argmax (teacher forcing, to score another implementation's drafts)."""
     emb_w = W["model.embed_tokens.weight"]
     hs = [hidden_last]
     toks = [pending]
@@ -476,7 +477,7 @@ def mtp_chain_draft(W, cfg, hidden_last, pending, k):
         drafts.append(d)
         logits.append(lg)
         hs.append(m[:, -1:])
-        toks.append(d)
+        toks.append(d if forced is None else forced[:, j].long())
     return torch.stack(drafts, 1), torch.stack(logits, 1)
 
 

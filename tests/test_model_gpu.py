@@ -1,0 +1,194 @@
+"""The MI355X model, MTP head and speculative decoder vs the oracle.
+
+Float outputs are held to the bf16 bar.  The oracle runs twice on the same
+bf16-rounded weights: in fp32 (the truth) and in bf16 with the reference's dtype flow.
+The build's bf16 logits must satisfy
+    max |got - ref32| <= 2 * max |ref16 - ref32| + 1e-3 * max |ref32|
+(no worse than twice the reference's own bf16 error; on these models that error is
+about 2% of the logit range, i.e. the rtol 2e-2 bar) and, per row,
+    1 - cos(got, ref32) <= max(2 * (1 - cos(ref16, ref32)), 1e-3)
+(the reference's parity gate uses cosine > 0.9999 in fp32, compare_logits.py:130).  Token-level checks use greedy
+decoding, where ties are the only legitimate source of disagreement.
+"""
+
+import pytest
+import torch
+
+from lollm_amd.qwen3_5.config import Qwen3_5Config, micro_config_dict, tiny_config_dict
+from lollm_amd.qwen3_5.random_init import random_weights
+from oracle import qwen3_5_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def close_logits(got, ref, ref16):
+    got = got.float().cpu().reshape(-1, got.shape[-1])
+    ref = ref.float().reshape(-1, ref.shape[-1])
+    ref16 = ref16.float().reshape(-1, ref.shape[-1])
+    scale = ref.abs().max().item()
+    cs = torch.nn.functional.cosine_similarity
+    deficit = (1 - cs(got, ref, dim=-1)).max().item()
+    ref_deficit = (1 - cs(ref16, ref, dim=-1)).max().item()
+    assert deficit <= max(2 * ref_deficit, 1e-3), f"1-cos {deficit:.3g} vs reference bf16 {ref_deficit:.3g}"
+    err = (got - ref).abs().max().item()
+    budget = 2 * (ref16 - ref).abs().max().item() + 1e-3 * scale
+    assert err <= budget, f"max err {err:.4g} > budget {budget:.4g} (scale {scale:.3g})"
+
+
+def build(raw, seed=0):
+    from lollm_amd.qwen3_5 import load, load_mtp
+    cfg = Qwen3_5Config.from_hf(raw)
+    W = random_weights(cfg, seed=seed)
+    Wb = {k: v.to(torch.bfloat16) for k, v in W.items()}       # both sides use bf16 weights
+    ref_W = R.canonical_weights({k: v.float() for k, v in Wb.items()})
+    ref_W16 = R.canonical_weights(dict(Wb))
+    ref_cfg = R.RefConfig.from_dict(raw)
+    weights = dict(Wb)
+    model = load(raw, weights, "hf", device="cuda")
+    mtp = load_mtp(model, weights, "hf", device="cuda")
+    return model, mtp, (ref_W, ref_W16), ref_cfg
+
+
+@pytest.fixture(scope="module")
+def micro():
+    return build(micro_config_dict())
+
+
+def test_forward_prefill_decode_verify(micro):
+    model, _, (W, W16), cfg = micro
+    print("case micro forward", flush=True)
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, cfg.vocab_size, (2, 9), generator=g)
+    steps = torch.randint(0, cfg.vocab_size, (2, 6), generator=g)
+    cache = model.new_cache(2, 64, spec_slots=4)
+    lg, _ = model(prompt.cuda(), cache)
+    ref, past = R.model_forward(W, cfg, prompt)
+    r16, p16 = R.model_forward(W16, cfg, prompt)
+    close_logits(lg, ref, r16)
+    lg, _ = model(steps[:, :1].cuda(), cache)                  # decode T=1
+    ref, past = R.model_forward(W, cfg, steps[:, :1], past)
+    r16, p16 = R.model_forward(W16, cfg, steps[:, :1], p16)
+    close_logits(lg, ref, r16)
+    lg, _ = model(steps[:, 1:5].cuda(), cache)                 # verify-shaped T=4
+    ref, past = R.model_forward(W, cfg, steps[:, 1:5], past)
+    r16, p16 = R.model_forward(W16, cfg, steps[:, 1:5], p16)
+    close_logits(lg, ref, r16)
+    assert cache.seen_tokens == past.seen_tokens == 14
+
+
+def test_rollback_equals_shorter_history(micro):
+    """Verify 4 tokens, keep a+1 of them via rollback; the next step's logits must match
+    a history that only ever saw those a+1 tokens."""
+    model, _, (W, W16), cfg = micro
+    g = torch.Generator().manual_seed(2)
+    prompt = torch.randint(0, cfg.vocab_size, (3, 7), generator=g)
+    blk = torch.randint(0, cfg.vocab_size, (3, 4), generator=g)
+    nxt = torch.randint(0, cfg.vocab_size, (3, 1), generator=g)
+    acc = torch.tensor([0, 2, 3], dtype=torch.int32)
+    cache = model.new_cache(3, 64, spec_slots=4)
+    model(prompt.cuda(), cache)
+    model(blk.cuda(), cache)
+    cache.rollback(acc.cuda())
+    lg, _ = model(nxt.cuda(), cache)
+    for b in range(3):
+        a = int(acc[b]) + 1
+        ids = torch.cat([prompt[b:b + 1], blk[b:b + 1, :a], nxt[b:b + 1]], 1)
+        ref, _ = R.model_forward(W, cfg, ids)
+        r16, _ = R.model_forward(W16, cfg, ids)
+        close_logits(lg[b, -1], ref[0, -1], r16[0, -1])
+
+
+def test_mtp_forward_and_chain(micro):
+    model, mtp, (W, W16), cfg = micro
+    g = torch.Generator().manual_seed(3)
+    h = torch.randn(2, 3, cfg.hidden_size, generator=g).bfloat16()
+    e = torch.randn(2, 3, cfg.hidden_size, generator=g).bfloat16()
+    got = mtp(h.cuda(), e.cuda())
+    ref = R.mtp_forward(W, cfg, h.float(), e.float())
+    close_logits(got, ref, R.mtp_forward(W16, cfg, h, e))
+    # the incremental draft chain == the no-cache recomputation of the draft block
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    prompt = torch.randint(0, cfg.vocab_size, (2, 8), generator=g)
+    dec = SpecDecoder(model, mtp, 2, 64, k=3)
+    dec.prefill(prompt.cuda())
+    dec._draft_chain()
+    got = dec.drafts.cpu().long()
+    h_last = dec.h_last.cpu().float()[:, None]
+    _, lg = R.mtp_chain_draft(W, cfg, h_last, dec.pending.cpu().long(), 3, forced=got)
+    top2 = lg.float().topk(2, -1).values
+    tie = (top2[..., 0] - top2[..., 1]) < 0.05
+    assert bool(((lg.float().argmax(-1) == got) | tie).all())
+
+
+def _check_greedy_trajectory(model, prompts, toks, margin=0.05):
+    """Every emitted token must be the argmax of the model's own logits given the
+    emitted prefix (teacher forcing), except where the top-2 gap is within `margin`."""
+    full = torch.cat([prompts, toks], 1)
+    lg, _ = model(full.cuda(), model.new_cache(full.shape[0], full.shape[1] + 4))
+    lg = lg.float().cpu()[:, prompts.shape[1] - 1:-1]
+    top2 = lg.topk(2, -1).values
+    am = lg.argmax(-1)
+    bad = (am != toks) & ((top2[..., 0] - top2[..., 1]) > margin)
+    assert not bad.any(), f"{int(bad.sum())} non-tie disagreements"
+
+
+@pytest.mark.parametrize("k", [1, 3])
+def test_greedy_spec_decode_is_greedy(micro, k):
+    model, mtp, _, cfg = micro
+    from lollm_amd.generate import greedy_tokens
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    print(f"case greedy spec k={k}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    prompts = torch.randint(0, cfg.vocab_size, (4, 12), generator=g)
+    n = 24
+    dec = SpecDecoder(model, mtp, 4, 12 + n + 2 * k + 4, k=k, temperature=0.0)
+    dec.prefill(prompts.cuda())
+    while int(dec.out_count.min()) < n:
+        dec.step()
+    spec = torch.tensor([t[:n] for t in dec.tokens()])
+    ar = greedy_tokens(model, prompts, n)
+    agree = (spec == ar).float().mean().item()
+    _check_greedy_trajectory(model, prompts, spec)
+    assert agree > 0.9, f"spec vs AR agreement {agree:.3f}"
+
+
+def test_graph_replay_matches_eager(micro):
+    model, mtp, _, cfg = micro
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    g = torch.Generator().manual_seed(6)
+    prompts = torch.randint(0, cfg.vocab_size, (3, 10), generator=g)
+    outs = []
+    for use_graph in (False, True):
+        dec = SpecDecoder(model, mtp, 3, 80, k=3, temperature=0.7, top_p=0.95, seed=9)
+        dec.prefill(prompts.cuda())
+        dec.step()
+        if use_graph:
+            dec.capture()
+        for i in range(6):
+            if use_graph:
+                dec.replay()
+                torch.cuda.synchronize()
+                _ = dec.out_count.cpu()            # eager work between replays
+            else:
+                dec.step()
+        outs.append(dec.tokens())
+    assert outs[0] == outs[1]
+
+
+def test_tiny_config_greedy_spec_k1():
+    """The tiny CPU-runnable config (hidden 1024, 8 layers): 64 greedy tokens from a
+    128-token prompt with k = 1, checked as a greedy trajectory of the model."""
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    model, mtp, (W, W16), cfg = build(tiny_config_dict(), seed=0)
+    g = torch.Generator().manual_seed(1)
+    prompts = torch.randint(0, cfg.vocab_size, (1, 128), generator=g)
+    dec = SpecDecoder(model, mtp, 1, 128 + 64 + 8, k=1, temperature=0.0)
+    dec.prefill(prompts.cuda())
+    while int(dec.out_count.min()) < 64:
+        dec.step()
+    toks = torch.tensor([dec.tokens()[0][:64]])
+    _check_greedy_trajectory(model, prompts, toks)
+    lg, _ = model(prompts.cuda(), model.new_cache(1, 140), logits="last")
+    ref, _ = R.model_forward(W, cfg, prompts)
+    r16, _ = R.model_forward(W16, cfg, prompts)
+    close_logits(lg[0, -1], ref[0, -1], r16[0, -1])
