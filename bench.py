@@ -1,0 +1,373 @@
+"""Benchmark of the qwen3_5 MTP speculative-decode step on one MI355X.
+
+Workload (the headline metric's configuration): a seeded random-init dense 8B-class
+qwen3_5 hybrid decoder (hidden 4096, 32 layers with 3:1 Gated DeltaNet : gated
+attention, GDN 16 qk / 32 v heads of 128, attention 32 q / 4 kv heads of 256, SwiGLU
+12288, vocab 151936, tied embeddings) plus a 1-layer MTP head; B = 16 sequences with
+2048-token uniform-random prompts; k = 3 MTP drafts per step; temperature 0.7,
+top-p 0.95; rejection-sampling acceptance.
+
+A step = draft chain (3 MTP passes + lm_head + argmax) + one verify forward over the
+1 + k positions of all 16 sequences + acceptance + commit, replayed from a HIP graph.
+`value` = emitted tokens per second over the K timed steps (the pending token plus
+the accepted drafts of every sequence; random weights accept almost nothing, so this
+is close to B tokens per step).  Also reported: the accepted-length histogram, the
+verify-step time, the dominant hand-written kernel's bandwidth against the 8 TB/s
+HBM3E peak (measured live with HIP events), the isolated-kernel workloads, and the
+CPU restatement of the reference path timed on the host.
+
+    python bench.py [--gpus 1] [--steps 256] [--warmup 8]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "accepted tok/s at B=16,k=3; verify-step µs; GDN/attn HBM GB/s vs peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_fn(fn, iters, warm=3):
+    """Average µs per call of fn() with HIP events on torch's current stream (every
+    lollm_amd kernel launches on that stream)."""
+    import torch
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / iters
+
+
+# ------------------------------------------------------------------------------------
+# end-to-end speculative decoding
+# ------------------------------------------------------------------------------------
+def build_8b(seed=5):
+    import torch
+    from lollm_amd.qwen3_5 import load, load_mtp
+    from lollm_amd.qwen3_5.config import Qwen3_5Config, dense_8b_config_dict
+    from lollm_amd.qwen3_5.random_init import random_weights
+    raw = dense_8b_config_dict()
+    cfg = Qwen3_5Config.from_hf(raw)
+    W = random_weights(cfg, seed=seed, dtype=torch.bfloat16, device="cuda")
+    keep = dict(W)                       # the loader pops; keep references for the CPU leg
+    model = load(raw, W, "hf", device="cuda")
+    mtp = load_mtp(model, W, "hf", device="cuda")
+    return raw, cfg, model, mtp, keep
+
+
+def run_e2e(model, mtp, cfg, B, prompt_len, k, steps, warmup, temperature, top_p, seed):
+    import torch
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    prompts = torch.randint(0, cfg.vocab_size, (B, prompt_len), device="cuda", generator=gen)
+    max_len = prompt_len + (steps + warmup + 2) * (k + 1) + 8
+    dec = SpecDecoder(model, mtp, B, max_len, k=k, temperature=temperature, top_p=top_p,
+                      seed=seed, out_capacity=(steps + warmup + 2) * (k + 1) + 8)
+    t0 = time.time()
+    dec.prefill(prompts)
+    torch.cuda.synchronize()
+    log(f"prefill {B}x{prompt_len}: {time.time() - t0:.2f} s")
+    n_eager = min(2, warmup)
+    for _ in range(n_eager):
+        dec.step()
+    dec.capture()
+    for _ in range(warmup - n_eager):
+        dec.replay()
+    torch.cuda.synchronize()
+    # timed region: K graph replays; per-step accepted counts read after the region
+    counts_before = dec.out_count.clone()
+    hist_before = dec.accept_hist.clone()
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        dec.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    gpu_s = e0.elapsed_time(e1) / 1000.0
+    emitted = int((dec.out_count - counts_before).sum())
+    hist = (dec.accept_hist - hist_before).cpu().tolist()
+    ctx = dec.cache.lengths.float().mean().item()
+    return dec, {"emitted": emitted, "seconds": gpu_s, "wall_seconds": wall, "hist": hist,
+                 "mean_accepted": sum(i * c for i, c in enumerate(hist)) / max(1, sum(hist)),
+                 "final_context_mean": ctx}
+
+
+def verify_breakdown(dec, iters=20):
+    """Eager timing of the step's parts (µs): draft chain, verify forward, acceptance."""
+    import torch
+    from lollm_amd import ops
+    B, k, model = dec.B, dec.k, dec.model
+    ids = torch.cat([dec.pending.view(B, 1), dec.drafts], 1).long()
+    st = {}
+    st["draft_chain_us"] = time_fn(dec._draft_chain, iters)
+
+    def verify():
+        # the verify pass over 1 + k positions (KV rows / GDN snapshots are written but
+        # not committed, so repeating it is idempotent)
+        hidden, normed = model.hidden_states(ids, dec.cache)
+        return model.lm_head(normed)
+    st["verify_forward_us"] = time_fn(verify, iters)
+    logits = verify()
+    st["accept_us"] = time_fn(lambda: ops.spec_accept(
+        logits, None, dec.drafts, dec.temperature, 0, dec.top_p, dec.seed, 0,
+        offset_dev=dec.offset, workspace=dec.spec_ws, n_accepted=dec.n_acc,
+        next_token=dec.next_tok), iters)
+    return st
+
+
+# ------------------------------------------------------------------------------------
+# the dominant hand-written kernel of the verify step: the fused GDN layer
+# ------------------------------------------------------------------------------------
+def gdn_layer_bytes(cfg, B, T):
+    """Algorithmic HBM bytes of one lollm_gdn_layer launch: read the committed state
+    once (B Hv Dk Dv fp32), write T snapshots, read the projections (B T P bf16) and
+    the conv window (K-1 rows), write the window (K-1+T rows) and the output (B T Hv Dv)."""
+    D, Hv = cfg.linear_key_head_dim, cfg.linear_num_value_heads
+    P = cfg.conv_dim + cfg.value_dim + 2 * Hv
+    K = cfg.linear_conv_kernel_dim
+    state = B * Hv * D * D * 4
+    return (state * (1 + T) + B * T * P * 2 + B * (K - 1) * cfg.conv_dim * 2
+            + B * (K - 1 + T) * cfg.conv_dim * 2 + B * T * cfg.value_dim * 2)
+
+
+def gdn_layer_roofline(model, dec, iters=50):
+    import torch
+    import torch.nn.functional as F
+    cfg = model.cfg
+    B, T = dec.B, dec.k + 1
+    li = next(i for i in range(cfg.num_hidden_layers) if cfg.layer_type(i) != "full_attention")
+    gdn = model.model.layers[li].linear_attn
+    x = torch.randn(B, T, cfg.hidden_size, device="cuda").bfloat16()
+    proj = F.linear(x, gdn.w_in)
+    s = dec.cache.layers[li]
+    from lollm_amd import ops
+    out = torch.empty(B, T, cfg.value_dim, dtype=torch.bfloat16, device="cuda")
+
+    def launch():
+        ops.gdn_layer(proj, gdn.conv_w, gdn.A_log, gdn.dt_bias, gdn.norm_w, s["win"],
+                      dec.cache.conv_off, s["rec"], dec.cache.rec_slot, False, B, T,
+                      cfg.linear_num_key_heads, cfg.linear_num_value_heads,
+                      cfg.linear_key_head_dim, cfg.linear_conv_kernel_dim, cfg.rms_norm_eps,
+                      out=out)
+    us = time_fn(launch, iters)
+    byt = gdn_layer_bytes(cfg, B, T)
+    gbs = byt / us / 1e3
+    return {"kernel": "lollm::gdn_layer_kernel", "shape": f"B={B} T={T} Hv=32 Hk=16 D=128",
+            "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "avg_us": round(us, 2),
+            "bytes_per_launch": byt}
+
+
+# ------------------------------------------------------------------------------------
+# isolated kernel workloads
+# ------------------------------------------------------------------------------------
+def isolated_gdn(B, kd):
+    import torch
+    from lollm_amd import ops
+    Hk, Hv, D, T = 16, 32, 128, 1 + kd
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2)
+    q = torch.nn.functional.normalize(torch.randn(B, T, Hk, D, device="cuda", generator=g), dim=-1).bfloat16()
+    k = torch.nn.functional.normalize(torch.randn(B, T, Hk, D, device="cuda", generator=g), dim=-1).bfloat16()
+    v = torch.randn(B, T, Hv, D, device="cuda", generator=g).bfloat16()
+    beta = torch.sigmoid(torch.randn(B, T, Hv, device="cuda", generator=g)).bfloat16()
+    gg = -torch.nn.functional.softplus(torch.randn(B, T, Hv, device="cuda", generator=g))
+    s0 = torch.randn(B, Hv, D, D, device="cuda", generator=g) * 0.02
+    out = torch.empty(B, T, Hv, D, dtype=torch.bfloat16, device="cuda")
+    snaps = torch.empty(B, T, Hv, D, D, device="cuda")
+    us = time_fn(lambda: ops.gdn_verify(q, k, v, gg, beta, s0, out=out, snap_out=snaps), 50)
+    byt = B * Hv * (1 + T) * D * D * 4 + B * T * (2 * Hk * D * 2 + 2 * Hv * D * 2 + Hv * 6)
+    return {"B": B, "T": T, "us": round(us, 2), "MB": round(byt / 1e6, 1),
+            "GBs": round(byt / us / 1e3, 1), "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
+
+
+def isolated_attn():
+    import torch
+    from lollm_amd import ops
+    g = torch.Generator().manual_seed(3)
+    B, T, Hq, Hkv, D, max_len = 16, 4, 16, 2, 256, 32768
+    lens = torch.randint(1024, 32769, (B,), generator=g)
+    q = torch.randn(B, T, Hq, D, device="cuda").bfloat16()
+    kc = torch.randn(B, Hkv, max_len, D, device="cuda").bfloat16()
+    vc = torch.randn(B, Hkv, max_len, D, device="cuda").bfloat16()
+    gate = torch.randn(B, T, Hq * D, device="cuda").bfloat16()
+    kl = lens.int().cuda()
+    chunk = 512
+    ws = torch.empty(ops.attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, chunk), dtype=torch.uint8, device="cuda")
+    out = torch.empty(B, T, Hq * D, dtype=torch.bfloat16, device="cuda")
+    us = time_fn(lambda: ops.attn_verify(q, kc, vc, kl, gate, chunk=chunk, workspace=ws, out=out), 20)
+    byt = int(lens.sum()) * Hkv * D * 2 * 2 + 3 * B * T * Hq * D * 2
+    del kc, vc
+    return {"B": B, "T": T, "sum_ctx": int(lens.sum()), "us": round(us, 2),
+            "MB": round(byt / 1e6, 1), "GBs": round(byt / us / 1e3, 1),
+            "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
+
+
+def isolated_sampler():
+    import torch
+    from lollm_amd import ops
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    B, k, V = 64, 3, 151936
+    tgt = torch.randn(B, k + 1, V, device="cuda", generator=g) * 3
+    drf = (tgt[:, :k] + torch.randn(B, k, V, device="cuda", generator=g)).bfloat16()
+    tgt = tgt.bfloat16()
+    drafts = torch.stack([ops.sample_rows(drf[:, i].contiguous(), 0.7, 0, 0.95, 7, 0, slot=k + 1 + i)
+                          for i in range(k)], 1)
+    ws = torch.empty(ops._lib.lib().lollm_spec_workspace_bytes(B, k, 1), dtype=torch.uint8, device="cuda")
+    us = time_fn(lambda: ops.spec_accept(tgt, drf, drafts, 0.7, 0, 0.95, 7, 0, workspace=ws), 20)
+    byt = B * (2 * k + 1) * V * 2
+    return {"B": B, "k": k, "V": V, "us": round(us, 2), "MB": round(byt / 1e6, 1),
+            "GBs": round(byt / us / 1e3, 1), "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
+
+
+# ------------------------------------------------------------------------------------
+# CPU baseline: the oracle (torch-on-CPU restatement of the reference path)
+# ------------------------------------------------------------------------------------
+def cpu_baseline(raw, cfg, keep, dec, k, temperature, top_p, seed):
+    """One speculative step of the reference algorithm on the host cores, from the GPU
+    run's committed state: the k-step MTP draft chain, the deep-copy snapshot of the
+    cache (kv.py:49-54), the verify forward over 1 + k positions (chunked GDN for T > 1,
+    SDPA with a bool mask over repeat_kv'd K/V), the rejection test, and the re-run of
+    the pending token from the snapshot (mtp.py:156-162; with random weights every
+    sequence rejects at its first draft, so the re-run is the common case).  fp32, all
+    host threads.  Extrapolated to tok/s as (accepted + 1) * B / step time."""
+    import numpy as np
+    import torch
+    from oracle import qwen3_5_ref as R
+    from oracle import sampler_ref as S
+    torch.set_num_threads(os.cpu_count())
+    t_setup = time.time()
+    W = R.canonical_weights({n: t.float().cpu() for n, t in keep.items()})
+    rcfg = R.RefConfig.from_dict(raw)
+    cache = dec.cache
+    L = int(cache.lengths.min())
+    past = R.RefCache(cfg.num_hidden_layers)
+    for i in range(cfg.num_hidden_layers):
+        if cfg.layer_type(i) == "full_attention":
+            s = cache.layers[i]
+            past.layers[i] = (s["k"][:, :, :L].float().cpu(), s["v"][:, :, :L].float().cpu())
+        else:
+            conv, rec = cache.linear_state(i)
+            past.layers[i] = (conv.float().cpu(), rec.float().cpu())
+    past.seen_tokens = L
+    pending = dec.pending.long().cpu()
+    h_last = dec.h_last.float().cpu()[:, None]
+    log(f"cpu baseline setup {time.time() - t_setup:.1f} s (threads {torch.get_num_threads()})")
+    B = pending.shape[0]
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        drafts, _ = R.mtp_chain_draft(W, rcfg, h_last, pending, k)
+        snap = past.clone()
+        ids = torch.cat([pending[:, None], drafts], 1)
+        logits, past, _ = R.model_forward(W, rcfg, ids, past, return_hidden=True)
+        inv = S.inv_temperature(temperature)
+        na, nt = S.spec_accept(logits.bfloat16(), None, drafts.numpy().astype(np.int32), inv, 0,
+                               top_p, seed, 1)
+        past = snap
+        R.model_forward(W, rcfg, pending[:, None], past, return_hidden=True)
+    step_s = time.perf_counter() - t0
+    toks = int(na.sum()) + B
+    model_name = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model_name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(toks / step_s, 3), "unit": "tok/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"1 speculative step (k={k}, B={B}, context {L}) of the CPU restatement "
+                       f"(oracle/) in fp32 on {os.cpu_count()} host CPUs ({model_name}): "
+                       f"{step_s:.2f} s/step, {toks} tokens; extrapolated to tok/s"),
+            "step_seconds": round(step_s, 3)}
+
+
+# ------------------------------------------------------------------------------------
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--prompt-len", type=int, default=2048)
+    ap.add_argument("--k", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-isolated", action="store_true", help="skip the isolated kernels")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU's share of the workload; --gpus {args.gpus} is not "
+              "supported (this build runs on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from lollm_amd import _lib
+    _lib.lib()                                    # fail loudly if the kernels are not built
+    temperature, top_p, seed = 0.7, 0.95, 5
+    t0 = time.time()
+    raw, cfg, model, mtp, keep = build_8b(seed)
+    log(f"model built in {time.time() - t0:.1f} s")
+    dec, e2e = run_e2e(model, mtp, cfg, args.batch, args.prompt_len, args.k, args.steps,
+                       args.warmup, temperature, top_p, seed)
+    value = e2e["emitted"] / e2e["seconds"]
+    ms_per_step = e2e["seconds"] * 1000.0 / args.steps
+    log(f"e2e: {value:.1f} tok/s, {ms_per_step:.3f} ms/step, hist {e2e['hist']}")
+    parts = verify_breakdown(dec)
+    roof = gdn_layer_roofline(model, dec)
+    log(f"gdn_layer: {roof['avg_us']} us, {roof['achieved']} GB/s")
+    kernels = {"gdn_layer_verify": roof}
+    if not args.no_isolated:
+        kernels["gdn_verify_isolated"] = [isolated_gdn(B, kd) for B in (1, 8, 32) for kd in (1, 2, 4)]
+        kernels["attn_verify_isolated"] = isolated_attn()
+        kernels["spec_accept_isolated"] = isolated_sampler()
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline(raw, cfg, keep, dec, args.k, temperature, top_p, seed)
+        except Exception as exc:                  # the CPU leg must not hide the GPU result
+            log(f"cpu baseline failed: {exc!r}")
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded random-init weights, uniform random prompt ids",
+        "config": {"workload": "qwen3_5 MTP speculative decode: dense 8B-class hybrid "
+                               "(hidden 4096, 32 layers 3:1 GDN:attn, vocab 151936) + 1-layer "
+                               f"MTP, B={args.batch}, {args.prompt_len}-token prompts, "
+                               f"k={args.k}, T=0.7, top-p 0.95",
+                   "global_batch": args.batch, "seq_len": args.prompt_len, "k": args.k,
+                   "parallelism": "single GPU"},
+        "accepted_length_hist": e2e["hist"], "mean_accepted": round(e2e["mean_accepted"], 4),
+        "verify_step_us": round(parts["verify_forward_us"], 1), "step_parts_us":
+            {k_: round(v, 1) for k_, v in parts.items()},
+        "roofline": {k_: roof[k_] for k_ in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+        "roofline_kernel": roof["kernel"],
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

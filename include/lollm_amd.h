@@ -186,14 +186,16 @@ int lollm_gdn_layer(const void* proj, long long proj_stride, const void* conv_w,
  * of lollm_gdn_layer: slots / win_rows) -- the O(1) form of the snapshot/restore
  * of src/qwen3_5/mtp.py:141,156-162), append verify_ids[b, 0..a] to out_tokens (cap
  * columns) at out_count[b], copy hidden[b, a] (B, T, H) to h_last (B, H) (the MTP
- * input, mtp.py:155,162), set pending = next_token, and increment *offset (the
- * sampler's Philox step counter).  No reference counterpart as one call: it folds
+ * input, mtp.py:155,162), set pending = next_token, increment *offset (the
+ * sampler's Philox step counter) and, if accept_hist != NULL, accept_hist[a] (T
+ * counters: the accepted-length histogram).  No reference counterpart as one call: it folds
  * the reference's per-step host bookkeeping into one kernel so a step needs no sync. */
 int lollm_spec_commit(const int32_t* verify_ids, const int32_t* n_accepted,
                       const int32_t* next_token, int32_t* lengths, int32_t* rec_slot,
                       int32_t* conv_off, int32_t* pending, int32_t* out_tokens, int32_t* out_count,
                       int out_cap, const void* hidden, void* h_last, int B, int T, int H,
-                      int slots, int win_rows, long long* offset, void* stream);
+                      int slots, int win_rows, long long* offset, int32_t* accept_hist,
+                      void* stream);
 
 #ifdef __cplusplus
 }

@@ -45,7 +45,7 @@ SIGNATURES = {
     "lollm_gdn_layer": ([_P, ctypes.c_longlong, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P,
                          _I, _I, _I, _I, _I, _I, _I, _F, _P], _I),
     "lollm_spec_commit": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P,
-                           _P], _I),
+                           _P, _P], _I),
 }
 
 _lib = None

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void spec_commit_kernel(
     const int32_t* __restrict__ next_tok, int32_t* lengths, int32_t* rec_slot, int32_t* conv_off,
     int32_t* pending, int32_t* out_tokens, int32_t* out_count, int cap,
     const uint16_t* __restrict__ hidden, uint16_t* __restrict__ h_last, int H, int T, int S,
-    int W, long long* offset) {
+    int W, long long* offset, int* hist) {
   const int b = blockIdx.x;
   int a = n_acc[b];
   a = a < 0 ? 0 : (a > T - 1 ? T - 1 : a);
@@ -181,6 +181,7 @@ __global__ __launch_bounds__(256) void spec_commit_kernel(
       if (c + i < cap) out_tokens[(size_t)b * cap + c + i] = verify_ids[b * T + i];
     out_count[b] = c + a + 1;
     pending[b] = next_tok[b];
+    if (hist) atomicAdd(&hist[a], 1);
     if (b == 0) offset[0] += 1;
   }
 }
@@ -234,7 +235,7 @@ LOLLM_API int lollm_spec_commit(const int32_t* verify_ids, const int32_t* n_acce
                                 int32_t* conv_off, int32_t* pending, int32_t* out_tokens,
                                 int32_t* out_count, int out_cap, const void* hidden, void* h_last,
                                 int B, int T, int H, int slots, int win_rows, long long* offset,
-                                void* stream) {
+                                int32_t* accept_hist, void* stream) {
   if (!verify_ids || !n_accepted || !next_token || !lengths || !rec_slot || !conv_off ||
       !pending || !out_tokens || !out_count || !hidden || !h_last || !offset)
     return LOLLM_EINVAL;
@@ -243,6 +244,6 @@ LOLLM_API int lollm_spec_commit(const int32_t* verify_ids, const int32_t* n_acce
   hipLaunchKernelGGL(spec_commit_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, verify_ids,
                      n_accepted, next_token, lengths, rec_slot, conv_off, pending, out_tokens,
                      out_count, out_cap, (const uint16_t*)hidden, (uint16_t*)h_last, H, T, slots,
-                     win_rows, offset);
+                     win_rows, offset, accept_hist);
   return launch_status();
 }

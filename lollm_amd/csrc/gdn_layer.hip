@@ -50,6 +50,9 @@ __device__ __forceinline__ float softplus_g(float x) {  // torch: linear above 2
   return x > 20.f ? x : log1pf(__expf(x));
 }
 
+// SNAP: the call writes a snapshot per position (T <= S: verify / decode); otherwise
+// it is a long call (prefill) that writes only the final state.
+template <bool SNAP>
 __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
   __shared__ float xin[GL_KMAX - 1 + GL_TC][GL_CH];  // conv inputs (state rows first)
   __shared__ float act[GL_TC][GL_CH];                // q | k | v after conv + SiLU
@@ -63,7 +66,7 @@ __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
   const int row0 = rg * 16, col0 = wave * 32 + cg * 4;
   const int Km1 = a.K - 1;
   const bool full_window = Km1 + a.T <= a.W;
-  const bool snaps = a.T <= a.S;
+  constexpr bool snaps = SNAP;
   constexpr size_t SS = (size_t)GL_DK * GL_DK;
   int off = a.conv_off[b];
   off = off < 0 ? 0 : (off > 2 * a.W - Km1 ? 2 * a.W - Km1 : off);  // never out of range
@@ -280,6 +283,9 @@ LOLLM_API int lollm_gdn_layer(const void* proj, long long proj_stride, const voi
   a.P = proj_stride; a.T = T; a.Hk = Hk; a.Hv = Hv; a.C = C; a.key_dim = key_dim;
   a.value_dim = value_dim; a.K = conv_kernel; a.W = win_rows; a.S = slots; a.fresh = fresh ? 1 : 0;
   a.eps = eps;
-  hipLaunchKernelGGL(gdn_layer_kernel, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);
+  if (T <= slots)
+    hipLaunchKernelGGL(gdn_layer_kernel<true>, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(gdn_layer_kernel<false>, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);
   return launch_status();
 }

@@ -320,11 +320,12 @@ def gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot
 
 
 def spec_commit(verify_ids, n_accepted, next_token, lengths, rec_slot, conv_off, pending,
-                out_tokens, out_count, hidden, h_last, offset, slots, win_rows):
+                out_tokens, out_count, hidden, h_last, offset, slots, win_rows, accept_hist=None):
     B, T = verify_ids.shape
     H = hidden.shape[-1]
     rc = _lib.lib().lollm_spec_commit(
         _ptr(verify_ids), _ptr(n_accepted), _ptr(next_token), _ptr(lengths), _ptr(rec_slot),
         _ptr(conv_off), _ptr(pending), _ptr(out_tokens), _ptr(out_count), out_tokens.shape[1],
-        _ptr(hidden), _ptr(h_last), B, T, H, slots, win_rows, _ptr(offset), _stream())
+        _ptr(hidden), _ptr(h_last), B, T, H, slots, win_rows, _ptr(offset), _ptr(accept_hist),
+        _stream())
     _lib.check(rc, "lollm_spec_commit")

@@ -82,12 +82,23 @@ class Qwen3_5Model:
     def new_cache(self, batch, max_len, spec_slots=4):
         return Qwen3_5Cache(self.cfg, batch, max_len, spec_slots, self.device)
 
-    def attn_workspace(self, B, T, max_len):
+    def attn_chunk_for(self, B, T, max_len):
+        """Keys per attention split: split-K over the context when the query blocks
+        alone cannot fill the GPU (verify, decode), one split for long calls (prefill),
+        where B x KV-heads x query blocks is already large."""
         cfg = self.cfg
-        key = (B, T, max_len)
+        n_rep = cfg.num_attention_heads // cfg.num_key_value_heads
+        qblocks = -(-T // max(1, min(T, 32 // n_rep)))
+        if B * cfg.num_key_value_heads * qblocks >= 1024:
+            return -(-max_len // 64) * 64
+        return self.attn_chunk
+
+    def attn_workspace(self, B, T, max_len, chunk):
+        cfg = self.cfg
+        key = (B, T, max_len, chunk)
         if key not in self._ws:
             n = ops.attn_workspace_bytes(B, T, cfg.num_attention_heads, cfg.num_key_value_heads,
-                                         cfg.head_dim, max_len, self.attn_chunk)
+                                         cfg.head_dim, max_len, chunk)
             self._ws[key] = torch.empty(max(n, 16), dtype=torch.uint8, device=self.device)
         return self._ws[key]
 
@@ -113,7 +124,8 @@ class Qwen3_5Model:
         x = self.model.embed_tokens(input_ids.to(self.device))
         lengths = cache.lengths
         kv_len = lengths + T
-        ws = self.attn_workspace(B, T, cache.max_len)
+        chunk = self.attn_chunk_for(B, T, cache.max_len)
+        ws = self.attn_workspace(B, T, cache.max_len, chunk)
         m = None
         for i, layer in enumerate(self.model.layers):
             if m is None:
@@ -122,7 +134,7 @@ class Qwen3_5Model:
                 h_in, x = layer.input_layernorm(m, residual=x)
             if layer.layer_type == "full_attention":
                 s = cache.layers[i]
-                h = layer.self_attn(h_in, s["k"], s["v"], lengths, kv_len, chunk=self.attn_chunk,
+                h = layer.self_attn(h_in, s["k"], s["v"], lengths, kv_len, chunk=chunk,
                                     workspace=ws)
             else:
                 h = layer.linear_attn(h_in, cache, i)

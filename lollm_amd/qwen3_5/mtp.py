@@ -138,6 +138,7 @@ class SpecDecoder:
         self.out_tokens = torch.zeros(batch, out_capacity, **i32)
         self.out_count = torch.zeros(batch, **i32)
         self.offset = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.accept_hist = torch.zeros(k + 1, **i32)       # accepted-length histogram
         self.spec_ws = torch.empty(max(ops._lib.lib().lollm_spec_workspace_bytes(batch, k, 1), 16),
                                    dtype=torch.uint8, device=dev)
         self.row_ws = torch.empty(batch * 24, dtype=torch.uint8, device=dev)
@@ -195,7 +196,7 @@ class SpecDecoder:
         ops.spec_commit(verify_ids, self.n_acc, self.next_tok, cache.lengths, cache.rec_slot,
                         cache.conv_off, self.pending, self.out_tokens, self.out_count,
                         hidden.contiguous(), self.h_last, self.offset, cache.spec_slots,
-                        cache.win_rows)
+                        cache.win_rows, self.accept_hist)
         cache.fresh = False
 
     def capture(self):
