@@ -212,10 +212,9 @@ def isolated_attn():
     vc = torch.randn(B, Hkv, max_len, D, device="cuda").bfloat16()
     gate = torch.randn(B, T, Hq * D, device="cuda").bfloat16()
     kl = lens.int().cuda()
-    chunk = 512
-    ws = torch.empty(ops.attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, chunk), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(ops.attn_workspace_bytes(B, T, Hq, Hkv, D, max_len), dtype=torch.uint8, device="cuda")
     out = torch.empty(B, T, Hq * D, dtype=torch.bfloat16, device="cuda")
-    us = time_fn(lambda: ops.attn_verify(q, kc, vc, kl, gate, chunk=chunk, workspace=ws, out=out), 20)
+    us = time_fn(lambda: ops.attn_verify(q, kc, vc, kl, gate, workspace=ws, out=out), 20)
     byt = int(lens.sum()) * Hkv * D * 2 * 2 + 3 * B * T * Hq * D * 2
     del kc, vc
     return {"B": B, "T": T, "sum_ctx": int(lens.sum()), "us": round(us, 2),

@@ -23,5 +23,5 @@ def attention(q, k, v):
     kc = k.contiguous().to(torch.bfloat16)
     vc = v.contiguous().to(torch.bfloat16)
     kv_len = torch.full((B,), tk, dtype=torch.int32, device=q.device)
-    o = ops.attn_verify(qq, kc, vc, kv_len, None, chunk=512)           # (B, q_len, H*D)
+    o = ops.attn_verify(qq, kc, vc, kv_len, None)                      # (B, q_len, H*D)
     return o.view(B, ql, H, D).transpose(1, 2).to(q.dtype)

@@ -136,18 +136,20 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None,
 # ------------------------------------------------------------------------------------
 # gated GQA attention over the KV cache
 # ------------------------------------------------------------------------------------
-def attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, chunk):
-    n = _lib.lib().lollm_attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, chunk)
+def attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, grid=0):
+    """Bytes of the split-K partials buffer for `grid` workgroups (0: two per CU)."""
+    n = _lib.lib().lollm_attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, grid)
     if n < 0:
         raise ValueError("unsupported attention geometry")
     return n
 
 
-def attn_verify(q, k_cache, v_cache, kv_len, gate=None, *, chunk=512, scale=None,
+def attn_verify(q, k_cache, v_cache, kv_len, gate=None, *, grid=0, scale=None,
                 workspace=None, out=None):
     """q (B, T, Hq, D) bf16; k_cache / v_cache (B, Hkv, max_len, D) bf16 with the T
     new keys already written at positions kv_len-T .. kv_len-1; kv_len (B,) int32;
-    gate (B, T, Hq*D) bf16 or None.  Returns (B, T, Hq*D) bf16."""
+    gate (B, T, Hq*D) bf16 or None.  Returns (B, T, Hq*D) bf16.  The key blocks of
+    all sequences are dealt out evenly to `grid` workgroups (0: two per CU)."""
     B, T, Hq, D = q.shape
     _need(q, "q", torch.bfloat16)
     if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[3] != D:
@@ -161,18 +163,17 @@ def attn_verify(q, k_cache, v_cache, kv_len, gate=None, *, chunk=512, scale=None
     if out is None:
         out = torch.empty(B, T, Hq * D, dtype=torch.bfloat16, device=q.device)
     _need(out, "out", torch.bfloat16, (B, T, Hq * D))
-    need = attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, chunk)
-    if max_len > chunk:
-        if workspace is None:
-            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
-        _need(workspace, "workspace")
-    wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    if workspace is None:
+        need = attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, grid)
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _need(workspace, "workspace")
+    wbytes = workspace.numel() * workspace.element_size()
     if scale is None:
         scale = D ** -0.5
     rc = _lib.lib().lollm_attn_verify(
         _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(kv_len), _ptr(gate), _ptr(out),
         _ptr(workspace), wbytes, B, T, Hq, Hkv, D, max_len, Hkv * max_len * D, max_len * D,
-        chunk, float(scale), _stream())
+        grid, float(scale), _stream())
     _lib.check(rc, "lollm_attn_verify")
     return out
 

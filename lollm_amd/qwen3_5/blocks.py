@@ -98,7 +98,7 @@ class GatedAttention:
         self.o_proj = W[p + "o_proj.weight"].contiguous()
         self.inv_freq = inv_freq
 
-    def __call__(self, x, k_cache, v_cache, lengths, kv_len, rope_pos=None, chunk=512,
+    def __call__(self, x, k_cache, v_cache, lengths, kv_len, rope_pos=None, grid=0,
                  workspace=None):
         B, T, _ = x.shape
         cfg = self.cfg
@@ -107,5 +107,5 @@ class GatedAttention:
                                     cfg.num_attention_heads, cfg.num_key_value_heads,
                                     cfg.head_dim, cfg.rotary_dim, cfg.rms_norm_eps, k_cache,
                                     v_cache, rope_pos=rope_pos)
-        o = ops.attn_verify(q, k_cache, v_cache, kv_len, gate, chunk=chunk, workspace=workspace)
+        o = ops.attn_verify(q, k_cache, v_cache, kv_len, gate, grid=grid, workspace=workspace)
         return F.linear(o, self.o_proj)

@@ -74,7 +74,7 @@ class Qwen3_5Model:
                              for i in range(cfg.num_hidden_layers)]
         self.model.norm = RMSNorm(W["model.norm.weight"], cfg.rms_norm_eps)
         self.lm_head = _Linear(W["lm_head.weight"])
-        self.attn_chunk = 512
+        self.attn_grid = 0          # attention workgroups (0: two per CU)
         self._ws = {}
         self.default_extra_capacity = 4096
 
@@ -82,23 +82,14 @@ class Qwen3_5Model:
     def new_cache(self, batch, max_len, spec_slots=4):
         return Qwen3_5Cache(self.cfg, batch, max_len, spec_slots, self.device)
 
-    def attn_chunk_for(self, B, T, max_len):
-        """Keys per attention split: split-K over the context when the query blocks
-        alone cannot fill the GPU (verify, decode), one split for long calls (prefill),
-        where B x KV-heads x query blocks is already large."""
+    def attn_workspace(self, B, T, max_len):
+        """Split-K partials buffer of the attention layers (shared by all layers of a
+        call; one per (B, T) shape, kept for graph replays)."""
         cfg = self.cfg
-        n_rep = cfg.num_attention_heads // cfg.num_key_value_heads
-        qblocks = -(-T // max(1, min(T, 32 // n_rep)))
-        if B * cfg.num_key_value_heads * qblocks >= 1024:
-            return -(-max_len // 64) * 64
-        return self.attn_chunk
-
-    def attn_workspace(self, B, T, max_len, chunk):
-        cfg = self.cfg
-        key = (B, T, max_len, chunk)
+        key = (B, T, max_len, self.attn_grid)
         if key not in self._ws:
             n = ops.attn_workspace_bytes(B, T, cfg.num_attention_heads, cfg.num_key_value_heads,
-                                         cfg.head_dim, max_len, chunk)
+                                         cfg.head_dim, max_len, self.attn_grid)
             self._ws[key] = torch.empty(max(n, 16), dtype=torch.uint8, device=self.device)
         return self._ws[key]
 
@@ -124,8 +115,7 @@ class Qwen3_5Model:
         x = self.model.embed_tokens(input_ids.to(self.device))
         lengths = cache.lengths
         kv_len = lengths + T
-        chunk = self.attn_chunk_for(B, T, cache.max_len)
-        ws = self.attn_workspace(B, T, cache.max_len, chunk)
+        ws = self.attn_workspace(B, T, cache.max_len)
         m = None
         for i, layer in enumerate(self.model.layers):
             if m is None:
@@ -134,8 +124,8 @@ class Qwen3_5Model:
                 h_in, x = layer.input_layernorm(m, residual=x)
             if layer.layer_type == "full_attention":
                 s = cache.layers[i]
-                h = layer.self_attn(h_in, s["k"], s["v"], lengths, kv_len, chunk=chunk,
-                                    workspace=ws)
+                h = layer.self_attn(h_in, s["k"], s["v"], lengths, kv_len,
+                                    grid=self.attn_grid, workspace=ws)
             else:
                 h = layer.linear_attn(h_in, cache, i)
             y, x = layer.post_attention_layernorm(h, residual=x)

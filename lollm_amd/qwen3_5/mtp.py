@@ -52,7 +52,7 @@ class MTP:
         layer = self.layers[0]
         h_in = layer.input_layernorm(x)
         h = layer.self_attn(h_in, k_cache, v_cache, lengths, kv_len, rope_pos=rope_pos,
-                            chunk=128, workspace=ws)
+                            grid=self.model.attn_grid, workspace=ws)
         y, x = layer.post_attention_layernorm(h, residual=x)
         m = layer.mlp(y)
         normed, x = self.norm(m, residual=x)
@@ -142,7 +142,7 @@ class SpecDecoder:
         self.spec_ws = torch.empty(max(ops._lib.lib().lollm_spec_workspace_bytes(batch, k, 1), 16),
                                    dtype=torch.uint8, device=dev)
         self.row_ws = torch.empty(batch * 24, dtype=torch.uint8, device=dev)
-        self.mtp_ws = torch.empty(16, dtype=torch.uint8, device=dev)
+        self.mtp_ws = model.attn_workspace(batch, 1, max(k, 1))
         self.draft_logits = (torch.empty(batch, k, cfg.vocab_size, dtype=torch.bfloat16, device=dev)
                              if self.draft_mode == "sample" else None)
         # per-draft-position index tensors (fixed across steps, so a graph can hold them)

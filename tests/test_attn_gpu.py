@@ -48,25 +48,28 @@ def oracle(q, kc, vc, lens, gate):
 
 
 CASES = [
-    # B, T, Hq, Hkv, lens, chunk
-    (3, 4, 16, 2, [4, 37, 700], 512),          # plain causal, one split, two splits
-    (2, 1, 8, 2, [1, 1000], 128),              # decode, many splits
-    (2, 2, 8, 2, [2, 129], 256),               # k = 1 verify, n_rep = 4
-    (2, 8, 16, 2, [8, 300], 128),              # two query blocks (n_rep 8 x 4 queries)
-    (4, 1, 32, 4, [1, 2, 3, 4], 128),          # MTP draft block: tiny causal contexts
-    (2, 4, 4, 2, [5, 64], 128),                # n_rep 2
+    # B, T, Hq, Hkv, lens, grid (workgroups of the balanced split; 0 = two per CU)
+    (3, 4, 16, 2, [4, 37, 700], 0),            # plain causal, whole pairs and cut pairs
+    (2, 1, 8, 2, [1, 1000], 5),                # decode, a long pair cut in many pieces
+    (2, 2, 8, 2, [2, 129], 3),                 # k = 1 verify, n_rep = 4
+    (2, 8, 16, 2, [8, 300], 4),                # two query blocks (n_rep 8 x 4 queries)
+    (4, 1, 32, 4, [1, 2, 3, 4], 0),            # MTP draft block: tiny causal contexts
+    (2, 4, 4, 2, [5, 64], 2),                  # n_rep 2
+    (5, 3, 8, 2, [3, 64, 65, 190, 7], 7),      # ranges spanning several sequences
+    (3, 4, 16, 2, [4, 600, 130], 1),           # one workgroup walks every pair
+    (3, 4, 16, 2, [4, 600, 130], 1024),        # more workgroups than blocks
 ]
 
 
-@pytest.mark.parametrize("B,T,Hq,Hkv,lens,chunk", CASES)
+@pytest.mark.parametrize("B,T,Hq,Hkv,lens,grid", CASES)
 @pytest.mark.parametrize("gated", [True, False])
-def test_attn_verify_matches_oracle(B, T, Hq, Hkv, lens, chunk, gated):
+def test_attn_verify_matches_oracle(B, T, Hq, Hkv, lens, grid, gated):
     from lollm_amd import ops
-    print(f"case B={B} T={T} Hq={Hq} Hkv={Hkv} lens={lens} chunk={chunk} gated={gated}", flush=True)
+    print(f"case B={B} T={T} Hq={Hq} Hkv={Hkv} lens={lens} grid={grid} gated={gated}", flush=True)
     q, kc, vc, kl, gate = make_case(B, T, Hq, Hkv, lens, seed=sum(lens) + T)
     ref = oracle(q, kc, vc, kl, gate if gated else None)
     out = ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(),
-                          gate.cuda() if gated else None, chunk=chunk)
+                          gate.cuda() if gated else None, grid=grid)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
     torch.testing.assert_close(out.cpu().float(), ref, **TOL)
@@ -81,14 +84,27 @@ def test_attn_verify_long_ragged_contexts():
     lens = torch.randint(1024, 32769, (4,), generator=gen).tolist()
     q, kc, vc, kl, gate = make_case(4, 4, 16, 2, lens, seed=3, max_len=32768)
     ref = oracle(q, kc, vc, kl, gate)
-    out = ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda(), chunk=512)
+    out = ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda())
     torch.testing.assert_close(out.cpu().float(), ref, **TOL)
 
 
 def test_attn_split_invariance():
-    """The split-K combine must not change the answer: chunk 128 == chunk 1024."""
+    """The split-K combine must not change the answer: one workgroup per pair, pairs
+    cut in a few pieces, and pairs cut in dozens of pieces agree."""
     from lollm_amd import ops
     q, kc, vc, kl, gate = make_case(2, 4, 16, 2, [900, 2000], seed=8)
-    a = ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda(), chunk=128)
-    b = ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda(), chunk=1024)
-    torch.testing.assert_close(a.float(), b.float(), rtol=1e-2, atol=1e-2)
+    outs = [ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda(), grid=g)
+            for g in (4, 9, 64)]
+    for o in outs[1:]:
+        torch.testing.assert_close(o.float(), outs[0].float(), rtol=1e-2, atol=1e-2)
+
+
+def test_attn_workspace_is_validated():
+    """A workspace smaller than lollm_attn_workspace_bytes is refused, not overrun."""
+    from lollm_amd import ops
+    q, kc, vc, kl, gate = make_case(2, 4, 16, 2, [90, 200], seed=9)
+    need = ops.attn_workspace_bytes(2, 4, 16, 2, D, 200, 8)
+    small = torch.empty(need - 4, dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError):
+        ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda(), grid=8,
+                        workspace=small)
