@@ -172,7 +172,7 @@ def gdn_layer_roofline(model, dec, iters=50):
     us = time_fn(launch, iters)
     byt = gdn_layer_bytes(cfg, B, T)
     gbs = byt / us / 1e3
-    return {"kernel": "lollm::gdn_layer_kernel", "shape": f"B={B} T={T} Hv=32 Hk=16 D=128",
+    return {"kernel": "lollm::gdn_layer_verify_kernel", "shape": f"B={B} T={T} Hv=32 Hk=16 D=128",
             "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "avg_us": round(us, 2),
             "bytes_per_launch": byt}

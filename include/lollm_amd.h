@@ -76,16 +76,18 @@ int lollm_gdn_select_state(const float* snapshots, const int32_t* slot, float* s
  *            <= kv_len - T + i (offset-causal)
  *   gate     (B, T, Hq * D) bf16 or NULL; out = attn * sigmoid(gate)
  *   out      (B, T, Hq * D) bf16
- *   workspace  split-K partials, lollm_attn_workspace_bytes() bytes (may be NULL
- *            when max_len <= chunk)
- *   chunk    keys per split (multiple of 128); scale: softmax scale (D^-0.5)
- * Supported: D == 256, Hq / Hkv <= 32. */
+ *   workspace  split-K partials, lollm_attn_workspace_bytes() bytes (required)
+ *   grid     workgroups of the balanced split (0: two per CU of the current device,
+ *            at most 1024): the 64-key blocks of all (sequence, KV head) pairs are
+ *            dealt out to them in equal contiguous ranges
+ *   scale    softmax scale (D^-0.5)
+ * Supported: D == 256, Hq / Hkv <= 32, B <= 512. */
 long long lollm_attn_workspace_bytes(int B, int T, int Hq, int Hkv, int D, int max_len,
-                                     int chunk);
+                                     int grid);
 int lollm_attn_verify(const void* q, const void* k_cache, const void* v_cache,
                       const int32_t* kv_len, const void* gate, void* out, void* workspace,
                       long long workspace_bytes, int B, int T, int Hq, int Hkv, int D,
-                      int max_len, long long seq_stride, long long head_stride, int chunk,
+                      int max_len, long long seq_stride, long long head_stride, int grid,
                       float scale, void* stream);
 
 /* Speculative-sampling acceptance over the full vocabulary for B sequences with k

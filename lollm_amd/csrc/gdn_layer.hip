@@ -50,6 +50,14 @@ __device__ __forceinline__ float softplus_g(float x) {  // torch: linear above 2
   return x > 20.f ? x : log1pf(__expf(x));
 }
 
+// Workgroup barrier that orders LDS only: outstanding global loads and stores (the
+// snapshot stream) are not waited for.
+__device__ __forceinline__ void lds_only_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // SNAP: the call writes a snapshot per position (T <= S: verify / decode); otherwise
 // it is a long call (prefill) that writes only the final state.
 template <bool SNAP>
@@ -258,6 +266,224 @@ __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------------
+// Verify / decode form (T <= GL_TC tokens, snapshots, conv kernel 4, the new window
+// fits one half): the same math as gdn_layer_kernel<true>, laid out so that a
+// workgroup makes ONE round trip to memory.  Every input -- the recurrent state
+// (registers), the conv window and the T projection rows of its 384 channels, the
+// conv weights, z, the norm weight, b and a -- is requested in one batch before the
+// first barrier; after it the workgroup only computes and stores: snapshots stream
+// out with non-temporal stores and no barrier ever waits for them (barriers order
+// LDS only).
+constexpr int GV_K = 4;
+
+__global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
+  __shared__ __attribute__((aligned(16))) float xin[GV_K - 1 + GL_TC][GL_CH];  // [state | raw]
+  __shared__ __attribute__((aligned(16))) float act[GL_TC][GL_CH];   // q | k | v, conv + SiLU
+  __shared__ __attribute__((aligned(16))) float obuf[GL_TC][GL_DK];  // scan outputs
+  __shared__ __attribute__((aligned(16))) uint16_t cw[GL_CH][GV_K];  // conv weights, 384 channels
+  __shared__ __attribute__((aligned(16))) uint16_t zb[GL_TC][GL_DK]; // z rows of this head
+  __shared__ __attribute__((aligned(16))) uint16_t nw[GL_DK];        // gated-norm weight
+  __shared__ float gb[GL_TC][2];                                     // g, beta
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cg = lane & 7, rg = lane >> 3;
+  const int b = blockIdx.x / a.Hv, h = blockIdx.x % a.Hv;
+  const int vpk = a.Hv / a.Hk, hk = h / vpk;
+  const bool write_qk = (h % vpk) == 0;  // q/k window channels are shared by vpk heads
+  const int row0 = rg * 16, col0 = wave * 32 + cg * 4;
+  const int T = a.T;
+  constexpr int Km1 = GV_K - 1;
+  constexpr size_t SS = (size_t)GL_DK * GL_DK;
+  int off = a.conv_off[b];
+  off = off < 0 ? 0 : (off > 2 * a.W - Km1 ? 2 * a.W - Km1 : off);  // never out of range
+  const int wbase = off >= a.W ? 0 : a.W;          // window half written by this call
+  int slot = a.rec_slot[b];
+  slot = slot < 0 ? 0 : (slot >= 2 * a.S ? 2 * a.S - 1 : slot);
+  const int rbase = slot >= a.S ? 0 : a.S;         // snapshot half written by this call
+  const size_t win_b = (size_t)b * 2 * a.W;
+  // channel group gi (q, k, v) -> first global conv channel
+  auto gbase = [&](int gi) {
+    return gi == 0 ? hk * GL_DK : (gi == 1 ? a.key_dim + hk * GL_DK : 2 * a.key_dim + h * GL_DK);
+  };
+
+  // ---- 1. one batch of loads ----
+  float S[16][4];
+  if (!a.fresh) {
+    const float* s0 = a.rec + ((size_t)(b * 2 * a.S + slot) * a.Hv + h) * SS;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float4 f = *reinterpret_cast<const float4*>(s0 + (size_t)(row0 + r) * GL_DK + col0);
+      S[r][0] = f.x; S[r][1] = f.y; S[r][2] = f.z; S[r][3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) S[r][0] = S[r][1] = S[r][2] = S[r][3] = 0.f;
+  }
+  // conv inputs: (K-1+T) rows x 3 groups x 16 chunks of 8 channels
+  const int nx = (Km1 + T) * 48;
+  uint4 xv[3];
+#pragma unroll
+  for (int it = 0; it < 3; ++it) {
+    const int id = it * 256 + tid;
+    xv[it] = make_uint4(0, 0, 0, 0);
+    if (id < nx) {
+      const int r = id / 48, gi = (id / 16) % 3, part = id % 16;
+      const int c = gbase(gi) + part * 8;
+      const uint16_t* src = r < Km1 ? a.win + (win_b + off + r) * a.C + c
+                                    : a.proj + ((size_t)b * T + r - Km1) * a.P + c;
+      xv[it] = *reinterpret_cast<const uint4*>(src);
+    }
+  }
+  uint4 cwv = make_uint4(0, 0, 0, 0), zv = make_uint4(0, 0, 0, 0), nwv = make_uint4(0, 0, 0, 0);
+  if (tid < 192) {  // 3 groups x 128 channels x 4 taps = 192 chunks of 16 B
+    const int gi = tid / 64, part = tid % 64;
+    cwv = *reinterpret_cast<const uint4*>(a.conv_w + (size_t)gbase(gi) * GV_K + part * 8);
+  }
+  if (tid < T * 16) {
+    const int t = tid / 16, part = tid % 16;
+    zv = *reinterpret_cast<const uint4*>(a.proj + ((size_t)b * T + t) * a.P + a.C +
+                                         (size_t)h * GL_DK + part * 8);
+  }
+  if (tid >= 240) nwv = *reinterpret_cast<const uint4*>(a.norm_w + (tid - 240) * 8);
+  float bb = 0.f, aa = 0.f;
+  if (tid < T) {
+    const size_t base = ((size_t)b * T + tid) * a.P + a.C + a.value_dim;
+    bb = bf16_to_f32(a.proj[base + h]);
+    aa = bf16_to_f32(a.proj[base + a.Hv + h]);
+  }
+  const float a_log = a.A_log[h], dtb = a.dt_bias[h];
+
+  // ---- 2. to LDS, and the new conv window (state rows + raw inputs) to the other half ----
+#pragma unroll
+  for (int it = 0; it < 3; ++it) {
+    const int id = it * 256 + tid;
+    if (id < nx) {
+      const int r = id / 48, gi = (id / 16) % 3, part = id % 16;
+      const uint32_t wd[4] = {xv[it].x, xv[it].y, xv[it].z, xv[it].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xin[r][gi * GL_DK + part * 8 + 2 * e] = __uint_as_float(wd[e] << 16);
+        xin[r][gi * GL_DK + part * 8 + 2 * e + 1] = __uint_as_float(wd[e] & 0xffff0000u);
+      }
+      if (gi == 2 || write_qk)
+        *reinterpret_cast<uint4*>(a.win + (win_b + wbase + r) * a.C + gbase(gi) + part * 8) = xv[it];
+    }
+  }
+  if (tid < 192) *reinterpret_cast<uint4*>(&cw[(tid / 64) * GL_DK + (tid % 64) * 2][0]) = cwv;
+  if (tid < T * 16) *reinterpret_cast<uint4*>(&zb[tid / 16][(tid % 16) * 8]) = zv;
+  if (tid >= 240) *reinterpret_cast<uint4*>(&nw[(tid - 240) * 8]) = nwv;
+  if (tid < T) {
+    gb[tid][0] = -__expf(a_log) * softplus_g(aa + dtb);
+    gb[tid][1] = round_bf16(1.f / (1.f + __expf(-bb)));
+  }
+  lds_only_barrier();
+  // ---- 3. conv + SiLU (bf16 rounding at the conv output and at the SiLU output) ----
+  for (int i = tid; i < T * GL_CH; i += 256) {
+    const int r = i / GL_CH, lc = i % GL_CH;
+    float acc = 0.f;
+#pragma unroll
+    for (int tau = 0; tau < GV_K; ++tau) acc = fmaf(bf16_to_f32(cw[lc][tau]), xin[r + tau][lc], acc);
+    act[r][lc] = round_bf16(silu_g(round_bf16(acc)));
+  }
+  lds_only_barrier();
+  // ---- 4. the scan, a snapshot per position ----
+  const float qscale = rsqrtf((float)GL_DK);
+  for (int t = 0; t < T; ++t) {
+    float kr[16], qr[16];
+#pragma unroll
+    for (int r = 0; r < 16; r += 4) {
+      const float4 q4 = *reinterpret_cast<const float4*>(&act[t][row0 + r]);
+      const float4 k4 = *reinterpret_cast<const float4*>(&act[t][GL_DK + row0 + r]);
+      qr[r] = q4.x; qr[r + 1] = q4.y; qr[r + 2] = q4.z; qr[r + 3] = q4.w;
+      kr[r] = k4.x; kr[r + 1] = k4.y; kr[r + 2] = k4.z; kr[r + 3] = k4.w;
+    }
+    float pa[4] = {0.f, 0.f, 0.f, 0.f}, pb[4] = {0.f, 0.f, 0.f, 0.f};
+    float pkq = 0.f, pkk = 0.f, pqq = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        pa[c] = fmaf(S[r][c], kr[r], pa[c]);
+        pb[c] = fmaf(S[r][c], qr[r], pb[c]);
+      }
+      pkq = fmaf(kr[r], qr[r], pkq);
+      pkk = fmaf(kr[r], kr[r], pkk);
+      pqq = fmaf(qr[r], qr[r], pqq);
+    }
+#pragma unroll
+    for (int m = 8; m < 64; m <<= 1) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        pa[c] += wave_xor(pa[c], m);
+        pb[c] += wave_xor(pb[c], m);
+      }
+      pkq += wave_xor(pkq, m);
+      pkk += wave_xor(pkk, m);
+      pqq += wave_xor(pqq, m);
+    }
+    const float rk = rsqrtf(pkk + 1e-6f);
+    const float rq = rsqrtf(pqq + 1e-6f) * qscale;
+    const float kq = pkq * rk * rq;
+    const float gam = __expf(gb[t][0]), bet = gb[t][1];
+    float d[4], o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float vv = act[t][2 * GL_DK + col0 + c];
+      d[c] = (vv - gam * pa[c] * rk) * bet;
+      o[c] = gam * pb[c] * rq + d[c] * kq;
+    }
+    if (rg == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) obuf[t][col0 + c] = o[c];
+    }
+    float* snap = a.rec + ((size_t)(b * 2 * a.S + rbase + t) * a.Hv + h) * SS;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float k_r = kr[r] * rk;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) S[r][c] = fmaf(k_r, d[c], gam * S[r][c]);
+      store_nt(snap + (size_t)(row0 + r) * GL_DK + col0,
+               make_uint4(__float_as_uint(S[r][0]), __float_as_uint(S[r][1]),
+                          __float_as_uint(S[r][2]), __float_as_uint(S[r][3])));
+    }
+  }
+  lds_only_barrier();
+  // ---- 5. gated RMSNorm of each token's 128 outputs: 16 threads per token ----
+  {
+    const int i = tid >> 4, part = tid & 15;
+    float ov[8], ss = 0.f;
+    if (i < T) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ov[e] = round_bf16(obuf[i][part * 8 + e]);  // core output is a bf16 tensor
+        ss += ov[e] * ov[e];
+      }
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    if (i < T) {
+      const float r = rsqrtf(ss / (float)GL_DK + a.eps);
+      uint32_t od[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float y2[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int ee = e + u;
+          const float z = bf16_to_f32(zb[i][part * 8 + ee]);
+          const float w = bf16_to_f32(nw[part * 8 + ee]);
+          const float hn = round_bf16(ov[ee] * r);
+          y2[u] = round_bf16(w * hn) * silu_g(z);
+        }
+        od[e >> 1] = f32_to_bf16(y2[0]) | ((uint32_t)f32_to_bf16(y2[1]) << 16);
+      }
+      *reinterpret_cast<uint4*>(a.out + ((size_t)b * T + i) * a.value_dim + (size_t)h * GL_DK +
+                                part * 8) = make_uint4(od[0], od[1], od[2], od[3]);
+    }
+  }
+}
+
 }  // namespace lollm
 
 using namespace lollm;
@@ -283,7 +509,11 @@ LOLLM_API int lollm_gdn_layer(const void* proj, long long proj_stride, const voi
   a.P = proj_stride; a.T = T; a.Hk = Hk; a.Hv = Hv; a.C = C; a.key_dim = key_dim;
   a.value_dim = value_dim; a.K = conv_kernel; a.W = win_rows; a.S = slots; a.fresh = fresh ? 1 : 0;
   a.eps = eps;
-  if (T <= slots)
+  const bool verify_form = T <= GL_TC && T <= slots && conv_kernel == GV_K &&
+                           conv_kernel - 1 + T <= win_rows && C % 8 == 0;
+  if (verify_form)
+    hipLaunchKernelGGL(gdn_layer_verify_kernel, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);
+  else if (T <= slots)
     hipLaunchKernelGGL(gdn_layer_kernel<true>, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);
   else
     hipLaunchKernelGGL(gdn_layer_kernel<false>, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);

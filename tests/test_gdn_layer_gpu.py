@@ -1,0 +1,110 @@
+"""The fused Gated DeltaNet mixer (lollm_gdn_layer) vs the oracle, at the dense 8B-class
+head shape (16 qk / 32 v heads of 128, conv kernel 4).
+
+Reference math: GatedDeltaNet.forward from the projections on (src/qwen3_5/blocks.py
+:268-329) -- causal depthwise conv + SiLU over [conv state | raw inputs], beta =
+sigmoid(b), g = -exp(A_log) softplus(a + dt_bias), the recurrent delta rule with
+in-kernel L2 norm (blocks.py:116-144), gated RMSNorm (blocks.py:38-51) -- restated in
+oracle/qwen3_5_ref.py.  The oracle runs twice on the same bf16 inputs: in fp32 (the
+truth) and with the reference's bf16 dtype flow.  Outputs are bf16 after three chained
+bf16 roundings and a silu(z) gate, so elementwise they are held to the bar the model
+tests use: max |got - ref32| <= 2 max |ref16 - ref32| + 1e-3 max |ref32| (no worse than
+twice the reference's own bf16 error), plus rtol/atol 2e-2 on all but 0.1% of the
+elements; snapshots (fp32) to rtol 2e-2 of the state scale.  The conv-window rows the
+call writes are raw copies and must be bit-exact; the halves holding the committed
+state must not be touched (that is what makes rollback O(1))."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import qwen3_5_ref as R
+
+pytestmark = pytest.mark.gpu
+Hk, Hv, D, K = 16, 32, 128, 4
+KEY, VAL = Hk * D, Hv * D
+C = 2 * KEY + VAL
+
+
+def make(B, T, S, seed):
+    gen = torch.Generator().manual_seed(seed)
+    P = C + VAL + 2 * Hv
+    P = -(-P // 8) * 8
+    W = K - 1 + S
+    proj = torch.randn(B, T, P, generator=gen).bfloat16()
+    conv_w = (torch.randn(C, K, generator=gen) * 0.5).bfloat16()
+    A_log = torch.randn(Hv, generator=gen) * 0.5
+    dt_bias = torch.randn(Hv, generator=gen) * 0.5
+    norm_w = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    win = torch.randn(B, 2 * W, C, generator=gen).bfloat16()
+    rec = torch.randn(B, 2 * S, Hv, D, D, generator=gen) * 0.02
+    half = torch.randint(0, 2, (B,), generator=gen)
+    c = torch.randint(0, S + 1, (B,), generator=gen)
+    conv_off = (half * W + c).int()
+    rec_slot = (torch.randint(0, 2, (B,), generator=gen) * S
+                + torch.randint(0, S, (B,), generator=gen)).int()
+    return proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, W
+
+
+def oracle(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, T):
+    B = proj.shape[0]
+    cfg = type("Cfg", (), {"linear_conv_kernel_dim": K})
+    Wd = {"l.conv1d.weight": conv_w.view(C, 1, K)}
+    outs, snaps = [], []
+    for b in range(B):
+        off, slot = int(conv_off[b]), int(rec_slot[b])
+        state = win[b, off:off + K - 1].t()[None]                     # (1, C, K-1)
+        qkv = proj[b:b + 1, :, :C].transpose(1, 2)                    # (1, C, T)
+        act, _ = R.causal_conv(Wd, "l.", cfg, qkv, state)
+        act = act.transpose(1, 2)
+        q = act[..., :KEY].reshape(1, T, Hk, D).repeat_interleave(Hv // Hk, 2)
+        k = act[..., KEY:2 * KEY].reshape(1, T, Hk, D).repeat_interleave(Hv // Hk, 2)
+        v = act[..., 2 * KEY:].reshape(1, T, Hv, D)
+        z = proj[b:b + 1, :, C:C + VAL].reshape(1, T, Hv, D)
+        bb = proj[b:b + 1, :, C + VAL:C + VAL + Hv]
+        aa = proj[b:b + 1, :, C + VAL + Hv:C + VAL + 2 * Hv]
+        beta = torch.sigmoid(bb)
+        g = -A_log.exp() * F.softplus(aa.float() + dt_bias)
+        o, sn = R.gdn_scan_recurrent_snapshots(q, k, v, g, beta, rec[b, slot][None], qk_l2=True)
+        core = R.rmsnorm_gated(o.reshape(-1, D), z.reshape(-1, D), norm_w, 1e-6)
+        outs.append(core.reshape(T, VAL))
+        snaps.append(sn[0])
+    return torch.stack(outs), torch.stack(snaps)
+
+
+@pytest.mark.parametrize("B,T,S", [(3, 4, 4), (2, 1, 4), (2, 2, 2), (2, 5, 5), (2, 8, 8)])
+def test_gdn_layer_verify_matches_oracle(B, T, S):
+    from lollm_amd import ops
+    print(f"case gdn_layer B={B} T={T} S={S}", flush=True)
+    proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, W = make(B, T, S, 10 * T + B)
+    ref_o, _ = oracle(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, T)
+    r32_o, ref_s = oracle(proj.float(), conv_w.float(), A_log, dt_bias, norm_w.float(),
+                          win.float(), conv_off, rec, rec_slot, T)
+    win_d, rec_d = win.cuda(), rec.cuda()
+    out = ops.gdn_layer(proj.cuda(), conv_w.cuda(), A_log.cuda(), dt_bias.cuda(), norm_w.cuda(),
+                        win_d, conv_off.cuda(), rec_d, rec_slot.cuda(), False, B, T, Hk, Hv, D, K,
+                        1e-6)
+    torch.cuda.synchronize()
+    got = out.cpu().float()
+    err = (got - r32_o).abs().max().item()
+    budget = 2 * (ref_o.float() - r32_o).abs().max().item() + 1e-3 * r32_o.abs().max().item()
+    assert err <= budget, f"max err {err:.4g} > budget {budget:.4g}"
+    bad = ~torch.isclose(got, ref_o.float(), rtol=2e-2, atol=2e-2)
+    assert bad.float().mean().item() <= 1e-3, f"{int(bad.sum())} of {bad.numel()} outside 2e-2"
+    win_o, rec_o = win_d.cpu(), rec_d.cpu()
+    for b in range(B):
+        off, slot = int(conv_off[b]), int(rec_slot[b])
+        wbase = 0 if off >= W else W
+        rbase = 0 if slot >= S else S
+        # snapshots of every position in the other half
+        got = rec_o[b, rbase:rbase + T]
+        scale = ref_s[b].abs().max().item()
+        torch.testing.assert_close(got, ref_s[b], rtol=2e-2, atol=2e-2 * scale)
+        # the committed half is untouched
+        keep = slice(S - rbase, 2 * S - rbase)
+        assert torch.equal(rec_o[b, keep], rec[b, keep])
+        # new window: old state rows, then the raw qkv rows, bit for bit
+        assert torch.equal(win_o[b, wbase:wbase + K - 1], win[b, off:off + K - 1])
+        assert torch.equal(win_o[b, wbase + K - 1:wbase + K - 1 + T], proj[b, :, :C])
+        other = slice(W - wbase, 2 * W - wbase)
+        assert torch.equal(win_o[b, other], win[b, other])
