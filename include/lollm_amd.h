@@ -110,7 +110,7 @@ int lollm_attn_verify(const void* q, const void* k_cache, const void* v_cache,
  *   n_accepted (B) int32 in 0..k; next_token (B) int32
  *   workspace  lollm_spec_workspace_bytes(B, k, draft != NULL) bytes
  * Outputs are bit-exact to the integer specification in oracle/sampler_ref.c.
- * Supported: V % 8 == 0, T <= 1000. */
+ * Supported: V % 8 == 0, T <= 1000, k <= 64. */
 long long lollm_spec_workspace_bytes(int B, int k, int with_draft);
 int lollm_spec_accept(const void* target, const void* draft, const int32_t* drafts, int B, int k,
                       int V, float inv_temperature, int top_k, float top_p, uint64_t seed,
@@ -121,7 +121,8 @@ int lollm_spec_accept(const void* target, const void* draft, const int32_t* draf
 /* One draw per row from its temperature / top-k / top-p distribution (the
  * multinomial of src/generate.py:37 on explicit uniforms); greedy rows return the
  * first argmax (generate.py:24).  Row r uses Philox row row_base + r and `slot`.
- * workspace: rows * 24 bytes. */
+ * workspace: lollm_sample_workspace_bytes(rows) bytes. */
+long long lollm_sample_workspace_bytes(int rows);
 int lollm_sample_rows(const void* logits, int rows, int V, float inv_temperature, int top_k,
                       float top_p, uint64_t seed, uint64_t offset, const uint64_t* offset_dev,
                       int row_base, int slot, int32_t* out, void* workspace,

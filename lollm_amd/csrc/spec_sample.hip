@@ -19,11 +19,22 @@
 // so any parallel decomposition gives the same bits.  This file is compiled with
 // -ffp-contract=off.
 //
-// Kernels: row_stats (one 1024-thread workgroup per row: max key / argmax, a
-// per-key count histogram over the NBINS keys below the max held in LDS, then a
-// block scan giving the top-k and top-p cut points and the kept mass Z);
-// spec_accept (one workgroup per sequence: the k accept tests, then a block-scan
-// inverse-CDF over one row for the residual or bonus draw); sample_rows.
+// Kernels:
+//   row_stats    one 1024-thread workgroup per row, ONE pass over HBM: the row is
+//                held in registers (19 x 16 B per thread covers V <= 155648; larger
+//                rows re-read the tail), giving the max key / argmax, then a per-key
+//                count histogram over the NBINS keys below the max in LDS and block
+//                scans for the top-k / top-p cut points and the kept mass Z;
+//   argmax_*     greedy rows: the row split over 16 workgroups, partial maxima
+//                merged by a second tiny kernel (a greedy row needs no histogram);
+//   spec_accept  one workgroup per sequence: the k accept tests in parallel, then
+//                the residual or bonus draw;
+//   sample_rows  one draw per row.
+// A draw is an inverse CDF over token ids in two steps: every wave of the block
+// sums the weights of its own contiguous sixteenth of the row (coalesced, one pass,
+// exact integers), then the one wave whose segment holds the target walks it again
+// with wave-level scans.  Residual masses are 64-bit when q is one-hot (argmax
+// drafts) and 128-bit when q is a sampled distribution.
 #include "common.h"
 
 namespace lollm {
@@ -176,54 +187,113 @@ __device__ T block_max(T v, T* scratch) {
   return r;
 }
 
+// ---------------------------------------------------------------- block primitives
+template <typename T>
+__device__ __forceinline__ T wave_sum_any(T v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += shfl_xor_any(v, m);
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const T o = shfl_up_any(v, d);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T shfl_any(T v, int src) {
+  constexpr int W = (sizeof(T) + 3) / 4;
+  union { T v; uint32_t w[W]; } u, r;
+  u.v = v;
+#pragma unroll
+  for (int i = 0; i < W; ++i) r.w[i] = __shfl(u.w[i], src, 64);
+  return r.v;
+}
+
 // ---------------------------------------------------------------- row statistics
-__device__ void row_stats_block(const uint16_t* __restrict__ x, int V, float inv_temp, int top_k,
-                                float top_p, RowStat* out, uint32_t* hist, uint64_t* s64,
-                                int32_t* shared_cut) {
+constexpr int SP_REG = 19;       // 16-byte chunks per thread held in registers
+constexpr int SP_NSPLIT = 16;    // workgroups per greedy row
+
+__device__ __forceinline__ void scan_chunk(uint4 u, int c, uint64_t& best, int32_t& km) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t b = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+    const uint32_t idx = (uint32_t)(c * 8 + e);
+    const uint64_t packed = ((uint64_t)ord16(b) << 32) | (0xFFFFFFFFu - idx);
+    best = packed > best ? packed : best;
+    const int32_t k = skey(b);
+    km = k > km ? k : km;
+  }
+}
+
+__device__ __forceinline__ void hist_chunk(uint4 u, int32_t km, uint32_t* hist) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t b = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+    const int32_t d = km - skey(b);
+    if (d < SP_NBINS) atomicAdd(&hist[d], 1u);
+  }
+}
+
+__global__ __launch_bounds__(SP_THREADS) void row_stats_kernel(const uint16_t* __restrict__ logits,
+                                                               int V, float inv_temp, int top_k,
+                                                               float top_p, RowStat* stats) {
+  __shared__ uint32_t hist[SP_NBINS];
+  __shared__ uint64_t s64[16];
+  __shared__ int32_t shared_cut;
+  __shared__ uint64_t z_sh;
   const int tid = threadIdx.x;
+  const int row = blockIdx.x;
   const int nch = V >> 3;
-  const uint4* x4 = reinterpret_cast<const uint4*>(x);
+  const uint4* x4 = reinterpret_cast<const uint4*>(logits + (size_t)row * V);
+  const bool greedy = !(inv_temp > 0.0f);
+  // ---- the row into registers (one HBM pass); zero the histogram meanwhile ----
+  uint4 reg[SP_REG];
+#pragma unroll
+  for (int i = 0; i < SP_REG; ++i) {
+    const int c = i * SP_THREADS + tid;
+    reg[i] = c < nch ? x4[c] : make_uint4(0, 0, 0, 0);
+  }
+  if (!greedy)
+    for (int i = tid; i < SP_NBINS; i += SP_THREADS) hist[i] = 0;
   uint64_t best = 0;
   int32_t km = INT32_MIN;
-  for (int c = tid; c < nch; c += SP_THREADS) {
-    const uint4 u = x4[c];
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t b = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-      const uint32_t idx = (uint32_t)(c * 8 + e);
-      const uint64_t packed = ((uint64_t)ord16(b) << 32) | (0xFFFFFFFFu - idx);
-      best = packed > best ? packed : best;
-      const int32_t k = skey(b);
-      km = k > km ? k : km;
-    }
+  for (int i = 0; i < SP_REG; ++i) {
+    const int c = i * SP_THREADS + tid;
+    if (c < nch) scan_chunk(reg[i], c, best, km);
   }
+  for (int c = SP_REG * SP_THREADS + tid; c < nch; c += SP_THREADS) scan_chunk(x4[c], c, best, km);
   best = block_max<uint64_t>(best, s64);
-  km = (int32_t)block_max<int64_t>((int64_t)km, reinterpret_cast<int64_t*>(s64));
   RowStat st;
   st.argmax = (int32_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu));
-  st.kmax = km;
-  st.greedy = !(inv_temp > 0.0f);
-  if (st.greedy) {
+  st.greedy = greedy;
+  if (greedy) {
+    st.kmax = 0;
     st.cut = 0;
     st.Z = 1;
-    if (tid == 0) *out = st;
+    if (tid == 0) stats[row] = st;
     return;
   }
-  for (int i = tid; i < SP_NBINS; i += SP_THREADS) hist[i] = 0;
-  __syncthreads();
-  for (int c = tid; c < nch; c += SP_THREADS) {
-    const uint4 u = x4[c];
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  km = (int32_t)block_max<int64_t>((int64_t)km, reinterpret_cast<int64_t*>(s64));
+  st.kmax = km;
+  // ---- per-key counts below the max (from registers) ----
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t b = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-      const int32_t d = km - skey(b);
-      if (d < SP_NBINS) atomicAdd(&hist[d], 1u);
-    }
+  for (int i = 0; i < SP_REG; ++i) {
+    const int c = i * SP_THREADS + tid;
+    if (c < nch) hist_chunk(reg[i], km, hist);
   }
+  for (int c = SP_REG * SP_THREADS + tid; c < nch; c += SP_THREADS) hist_chunk(x4[c], km, hist);
   __syncthreads();
-  // thread t owns bins [8t, 8t + 8)
+  // ---- cut points and kept mass: thread t owns bins [8t, 8t + 8) ----
   constexpr int PER = SP_NBINS / SP_THREADS;
   const float xmax = key_value(km);
   const float c = inv_temp * 1.44269504088896341f;
@@ -237,7 +307,7 @@ __device__ void row_stats_block(const uint16_t* __restrict__ x, int V, float inv
     mass[j] = cnt[j] ? (uint64_t)cnt[j] * weight_of(key_value(km - d), xmax, c) : 0;
     csum += cnt[j];
   }
-  if (tid == 0) *shared_cut = SP_NBINS - 1;
+  if (tid == 0) shared_cut = SP_NBINS - 1;
   __syncthreads();
   if (top_k > 0) {
     uint64_t ctot;
@@ -248,12 +318,12 @@ __device__ void row_stats_block(const uint16_t* __restrict__ x, int V, float inv
 #pragma unroll
       for (int j = 0; j < PER; ++j) {
         run += cnt[j];
-        if (run >= (uint64_t)top_k) { *shared_cut = tid * PER + j; break; }
+        if (run >= (uint64_t)top_k) { shared_cut = tid * PER + j; break; }
       }
     }
     __syncthreads();
   }
-  const int32_t cut_k = *shared_cut;
+  const int32_t cut_k = shared_cut;
   uint64_t msum = 0;
 #pragma unroll
   for (int j = 0; j < PER; ++j)
@@ -266,74 +336,164 @@ __device__ void row_stats_block(const uint16_t* __restrict__ x, int V, float inv
     const uint32_t p24 = (uint32_t)(top_p * 16777216.0f);
     const uint64_t tm = (uint64_t)(((u128)W * p24) >> 24);
     const uint64_t m0 = minc - msum;
-    __shared__ uint64_t z_sh;
     if (m0 <= tm && minc > tm) {
       uint64_t run = m0;
 #pragma unroll
       for (int j = 0; j < PER; ++j) {
         if (tid * PER + j > cut_k) break;
         run += mass[j];
-        if (run > tm) { *shared_cut = tid * PER + j; z_sh = run; break; }
+        if (run > tm) { shared_cut = tid * PER + j; z_sh = run; break; }
       }
     }
     __syncthreads();
-    st.cut = *shared_cut;
+    st.cut = shared_cut;
     st.Z = z_sh;
   }
-  if (tid == 0) *out = st;
+  if (tid == 0) stats[row] = st;
 }
 
-__global__ __launch_bounds__(SP_THREADS) void row_stats_kernel(const uint16_t* __restrict__ logits,
-                                                               int V, float inv_temp, int top_k,
-                                                               float top_p, RowStat* stats) {
-  __shared__ uint32_t hist[SP_NBINS];
-  __shared__ uint64_t s64[16];
-  __shared__ int32_t cut;
-  const int row = blockIdx.x;
-  row_stats_block(logits + (size_t)row * V, V, inv_temp, top_k, top_p, stats + row, hist, s64,
-                  &cut);
+// Greedy rows: 16 workgroups per row each reduce a slice to a packed
+// (order key, ~index) maximum; a second kernel merges them into RowStat / a token.
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const uint16_t* __restrict__ logits,
+                                                             int V, uint64_t* __restrict__ part) {
+  __shared__ uint64_t s64[4];
+  const int row = blockIdx.y, split = blockIdx.x;
+  const int nch = V >> 3, per = (nch + SP_NSPLIT - 1) / SP_NSPLIT;
+  const int c0 = split * per, c1 = min(nch, c0 + per);
+  const uint4* x4 = reinterpret_cast<const uint4*>(logits + (size_t)row * V);
+  uint64_t best = 0;
+  int32_t km = 0;
+  for (int c = c0 + threadIdx.x; c < c1; c += 256) scan_chunk(x4[c], c, best, km);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const uint64_t o = shfl_xor_any(best, m);
+    best = o > best ? o : best;
+  }
+  if (lane == 0) s64[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t r = s64[0];
+    for (int w = 1; w < 4; ++w) r = s64[w] > r ? s64[w] : r;
+    part[(size_t)row * SP_NSPLIT + split] = r;
+  }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* __restrict__ part,
+                                                          RowStat* __restrict__ stats,
+                                                          int32_t* __restrict__ tokens) {
+  const int row = blockIdx.x, lane = threadIdx.x;
+  uint64_t best = lane < SP_NSPLIT ? part[(size_t)row * SP_NSPLIT + lane] : 0;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const uint64_t o = shfl_xor_any(best, m);
+    best = o > best ? o : best;
+  }
+  if (lane == 0) {
+    const int32_t am = (int32_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu));
+    if (stats) {
+      RowStat st;
+      st.argmax = am; st.kmax = 0; st.cut = 0; st.greedy = 1; st.Z = 1;
+      stats[row] = st;
+    }
+    if (tokens) tokens[row] = am;
+  }
 }
 
 // ---------------------------------------------------------------- inverse-CDF draw
-// First token (in id order) whose inclusive prefix of wfn(token) exceeds `target`.
-template <typename Acc, typename WFn>
-__device__ int32_t block_draw(int V, Acc target, WFn wfn, Acc* scratch) {
-  __shared__ int32_t found;
-  const int tid = threadIdx.x;
-  if (tid == 0) found = -1;
-  __syncthreads();
-  Acc run = 0;
-  for (int base = 0; base < V; base += SP_THREADS * 8) {
-    const int t0 = base + tid * 8;
+// Wave w of the 16 owns chunks [w * seg, min((w + 1) * seg, nch)).  W8(c, w[8]) gives
+// the weights of the 8 tokens of chunk c.
+template <typename Acc, typename W8>
+__device__ Acc draw_totals(int nch, int seg, W8 w8, Acc* wtot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();  // wtot may still be read by a previous draw's waves
+  const int c0 = wave * seg, c1 = min(c0 + seg, nch);
+  Acc acc = 0;
+  for (int c = c0 + lane; c < c1; c += 64) {
     Acc w[8];
-    Acc loc = 0;
+    w8(c, w);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      w[e] = (t0 + e < V) ? wfn(t0 + e) : (Acc)0;
-      loc += w[e];
-    }
-    Acc total;
-    const Acc inc = block_inclusive_scan<Acc>(loc, scratch, &total);
-    const Acc before = run + inc - loc;
-    if (before <= target && run + inc > target) {
-      Acc r = before;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        r += w[e];
-        if (r > target) { found = t0 + e; break; }
-      }
-    }
-    __syncthreads();
-    if (found >= 0) break;
-    run += total;
+    for (int e = 0; e < 8; ++e) acc += w[e];
   }
-  const int32_t f = found;
+  acc = wave_sum_any(acc);
+  if (lane == 0) wtot[wave] = acc;
   __syncthreads();
+  Acc tot = 0;
+#pragma unroll
+  for (int w = 0; w < SP_THREADS / 64; ++w) tot += wtot[w];
+  return tot;
+}
+
+// The first token whose inclusive prefix exceeds target (< the row total).
+template <typename Acc, typename W8>
+__device__ int32_t draw_find(int nch, int seg, W8 w8, const Acc* wtot, Acc target, int V,
+                             int32_t* found) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  Acc before = 0;
+  int ow = SP_THREADS / 64 - 1;
+  for (int w = 0; w < SP_THREADS / 64; ++w) {
+    if (before + wtot[w] > target) { ow = w; break; }
+    before += wtot[w];
+  }
+  if (threadIdx.x == 0) *found = -1;
+  __syncthreads();
+  if (wave == ow) {
+    const int c0 = ow * seg, c1 = min(c0 + seg, nch);
+    Acc run = before;
+    for (int cb = c0; cb < c1; cb += 64) {
+      const int c = cb + lane;
+      Acc w[8];
+      Acc sum = 0;
+      if (c < c1) {
+        w8(c, w);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = 0;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += w[e];
+      const Acc inc = wave_incl_scan(sum);
+      const Acc tot = shfl_any(inc, 63);
+      if (run + tot > target) {
+        const Acc ex = run + inc - sum;
+        if (ex <= target && run + inc > target) {
+          Acc r = ex;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            r += w[e];
+            if (r > target) { *found = c * 8 + e; break; }
+          }
+        }
+        break;
+      }
+      run += tot;
+    }
+  }
+  __syncthreads();
+  const int32_t f = *found;
   return f < 0 ? V - 1 : f;
 }
 
 __device__ __forceinline__ u128 scaled_target(uint32_t U, u128 M) {
   return (u128)U * (M >> 24) + (((u128)U * (uint64_t)(M & 0xFFFFFFu)) >> 24);
+}
+
+// Plain draw from a row's own distribution p (u64 masses, target floor(U Z / 2^24)).
+__device__ int32_t draw_plain(const uint16_t* xp, const RowStat& sp, float c, uint32_t U, int V,
+                              uint64_t* wtot, int32_t* found) {
+  if (sp.greedy) return sp.argmax;
+  const int nch = V >> 3, seg = (nch + SP_THREADS / 64 - 1) / (SP_THREADS / 64);
+  const uint4* x4 = reinterpret_cast<const uint4*>(xp);
+  auto w8 = [&](int ch, uint64_t* w) {
+    const uint4 u = x4[ch];
+    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      w[e] = token_weight(sp, c, (wd[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, ch * 8 + e);
+  };
+  draw_totals<uint64_t>(nch, seg, w8, wtot);
+  const uint64_t tgt = (uint64_t)(((u128)U * sp.Z) >> 24);
+  return draw_find<uint64_t>(nch, seg, w8, wtot, tgt, V, found);
 }
 
 __global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
@@ -342,81 +502,88 @@ __global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
     uint64_t offset_arg, const uint64_t* __restrict__ offset_dev, const RowStat* __restrict__ st_t,
     const RowStat* __restrict__ st_d, int32_t* __restrict__ n_accepted,
     int32_t* __restrict__ next_token) {
-  __shared__ u128 scratch[16];
-  __shared__ int32_t sh_a, sh_rej;
+  __shared__ u128 wt128[SP_THREADS / 64];
+  __shared__ uint64_t wt64[SP_THREADS / 64];
+  __shared__ int32_t found;
+  __shared__ int32_t ok[64];
   const int b = blockIdx.x;
+  const int tid = threadIdx.x;
   const uint64_t offset = offset_dev ? *offset_dev : offset_arg;
   const float c = inv_temp * 1.44269504088896341f;
-  if (threadIdx.x == 0) {
-    int a = 0, rej = 0;
-    for (int i = 0; i < k; ++i) {
-      int32_t d = drafts[b * k + i];
-      d = d < 0 ? 0 : (d >= V ? V - 1 : d);
-      const RowStat sp = st_t[b * (k + 1) + i];
-      const uint16_t* xp = target + ((size_t)b * (k + 1) + i) * V;
-      const uint64_t wp = token_weight(sp, c, xp[d], d), Zp = sp.Z;
-      uint64_t wq = 1, Zq = 1;
-      if (draft) {
-        const RowStat sq = st_d[b * k + i];
-        wq = token_weight(sq, c, draft[((size_t)b * k + i) * V + d], d);
-        Zq = sq.Z;
-      }
-      const uint32_t U = philox_u24(seed, offset, (uint32_t)b, (uint32_t)i);
-      const u128 lhs = (u128)U * wq * Zp;
-      const u128 rhs = ((u128)wp * Zq) << 24;
-      if (!(lhs < rhs)) { rej = 1; break; }
-      ++a;
+  // ---- the k accept tests, one thread each ----
+  for (int i = tid; i < k; i += SP_THREADS) {
+    int32_t d = drafts[b * k + i];
+    d = d < 0 ? 0 : (d >= V ? V - 1 : d);
+    const RowStat sp = st_t[b * (k + 1) + i];
+    const uint16_t* xp = target + ((size_t)b * (k + 1) + i) * V;
+    const uint64_t wp = token_weight(sp, c, xp[d], d), Zp = sp.Z;
+    uint64_t wq = 1, Zq = 1;
+    if (draft) {
+      const RowStat sq = st_d[b * k + i];
+      wq = token_weight(sq, c, draft[((size_t)b * k + i) * V + d], d);
+      Zq = sq.Z;
     }
-    sh_a = a;
-    sh_rej = rej;
+    const uint32_t U = philox_u24(seed, offset, (uint32_t)b, (uint32_t)i);
+    const u128 lhs = (u128)U * wq * Zp;
+    const u128 rhs = ((u128)wp * Zq) << 24;
+    if (i < 64) ok[i] = lhs < rhs;
   }
   __syncthreads();
-  const int a = sh_a;
+  int a = 0;
+  while (a < k && a < 64 && ok[a]) ++a;
+  const bool rej = a < k;
   const uint32_t U = philox_u24(seed, offset, (uint32_t)b, (uint32_t)k);
   int32_t tok;
-  if (!sh_rej) {
+  if (!rej) {
     const RowStat sp = st_t[b * (k + 1) + k];
-    const uint16_t* xp = target + ((size_t)b * (k + 1) + k) * V;
-    if (sp.greedy) {
-      tok = sp.argmax;
-    } else {
-      const u128 tgt = ((u128)U * sp.Z) >> 24;
-      tok = block_draw<u128>(V, tgt, [&](int t) { return (u128)token_weight(sp, c, xp[t], t); },
-                             scratch);
-    }
+    tok = draw_plain(target + ((size_t)b * (k + 1) + k) * V, sp, c, U, V, wt64, &found);
   } else {
     const RowStat sp = st_t[b * (k + 1) + a];
     const uint16_t* xp = target + ((size_t)b * (k + 1) + a) * V;
     int32_t d = drafts[b * k + a];
     d = d < 0 ? 0 : (d >= V ? V - 1 : d);
-    RowStat sq;
-    const uint16_t* xq = nullptr;
-    uint64_t Zq = 1;
+    const int nch = V >> 3, seg = (nch + SP_THREADS / 64 - 1) / (SP_THREADS / 64);
+    const uint4* xp4 = reinterpret_cast<const uint4*>(xp);
     if (draft) {
-      sq = st_d[b * k + a];
-      xq = draft + ((size_t)b * k + a) * V;
-      Zq = sq.Z;
-    }
-    auto resid = [&](int t) -> u128 {
-      const uint64_t wpt = token_weight(sp, c, xp[t], t);
-      const uint64_t wqt = xq ? token_weight(sq, c, xq[t], t) : (uint64_t)(t == d);
-      const u128 l = (u128)wpt * Zq, r = (u128)wqt * sp.Z;
-      return l > r ? l - r : (u128)0;
-    };
-    // total residual mass
-    u128 R = 0;
-    for (int t = threadIdx.x; t < V; t += SP_THREADS) R += resid(t);
-    R = block_sum<u128>(R, scratch);
-    if (R == 0) {
-      const u128 tgt = ((u128)U * sp.Z) >> 24;
-      tok = sp.greedy ? sp.argmax
-                      : block_draw<u128>(V, tgt, [&](int t) { return (u128)token_weight(sp, c, xp[t], t); },
-                                         scratch);
+      // q a sampled distribution: residual wp Zq - wq Zp in 128 bits
+      const RowStat sq = st_d[b * k + a];
+      const uint4* xq4 = reinterpret_cast<const uint4*>(draft + ((size_t)b * k + a) * V);
+      const uint64_t Zq = sq.Z;
+      auto w8 = [&](int ch, u128* w) {
+        const uint4 up = xp4[ch], uq = xq4[ch];
+        const uint32_t pw[4] = {up.x, up.y, up.z, up.w}, qw[4] = {uq.x, uq.y, uq.z, uq.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int t = ch * 8 + e;
+          const uint64_t wpt = token_weight(sp, c, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
+          const uint64_t wqt = token_weight(sq, c, (qw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
+          const u128 l = (u128)wpt * Zq, r = (u128)wqt * sp.Z;
+          w[e] = l > r ? l - r : (u128)0;
+        }
+      };
+      const u128 R = draw_totals<u128>(nch, seg, w8, wt128);
+      tok = R == 0 ? draw_plain(xp, sp, c, U, V, wt64, &found)
+                   : draw_find<u128>(nch, seg, w8, wt128, scaled_target(U, R), V, &found);
     } else {
-      tok = block_draw<u128>(V, scaled_target(U, R), resid, scratch);
+      // q one-hot at d: residual wp - [t == d] Zp fits 64 bits
+      auto w8 = [&](int ch, uint64_t* w) {
+        const uint4 up = xp4[ch];
+        const uint32_t pw[4] = {up.x, up.y, up.z, up.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int t = ch * 8 + e;
+          const uint64_t wpt = token_weight(sp, c, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
+          const uint64_t r = t == d ? sp.Z : 0;
+          w[e] = wpt > r ? wpt - r : 0;
+        }
+      };
+      const uint64_t R = draw_totals<uint64_t>(nch, seg, w8, wt64);
+      tok = R == 0 ? draw_plain(xp, sp, c, U, V, wt64, &found)
+                   : draw_find<uint64_t>(nch, seg, w8, wt64,
+                                         (uint64_t)scaled_target(U, (u128)R), V, &found);
     }
   }
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     n_accepted[b] = a;
     next_token[b] = tok;
   }
@@ -426,21 +593,14 @@ __global__ __launch_bounds__(SP_THREADS) void sample_rows_kernel(
     const uint16_t* __restrict__ logits, int V, float inv_temp, uint64_t seed, uint64_t offset_arg,
     const uint64_t* __restrict__ offset_dev, int row_base, int slot,
     const RowStat* __restrict__ stats, int32_t* __restrict__ out) {
-  __shared__ u128 scratch[16];
+  __shared__ uint64_t wt64[SP_THREADS / 64];
+  __shared__ int32_t found;
   const int r = blockIdx.x;
   const uint64_t offset = offset_dev ? *offset_dev : offset_arg;
   const RowStat sp = stats[r];
   const float c = inv_temp * 1.44269504088896341f;
-  int32_t tok;
-  if (sp.greedy) {
-    tok = sp.argmax;
-  } else {
-    const uint16_t* xp = logits + (size_t)r * V;
-    const uint32_t U = philox_u24(seed, offset, (uint32_t)(row_base + r), (uint32_t)slot);
-    const u128 tgt = ((u128)U * sp.Z) >> 24;
-    tok = block_draw<u128>(V, tgt, [&](int t) { return (u128)token_weight(sp, c, xp[t], t); },
-                           scratch);
-  }
+  const uint32_t U = philox_u24(seed, offset, (uint32_t)(row_base + r), (uint32_t)slot);
+  const int32_t tok = draw_plain(logits + (size_t)r * V, sp, c, U, V, wt64, &found);
   if (threadIdx.x == 0) out[r] = tok;
 }
 
@@ -460,9 +620,35 @@ static bool sampler_args_ok(int V, float top_p, float inv_temp) {
   return true;
 }
 
+// Row statistics for `rows` rows: the histogram kernel, or for greedy rows the split
+// argmax (partials at `part`).
+static int launch_row_stats(const uint16_t* x, int rows, int V, float inv_temp, int top_k,
+                            float top_p, RowStat* st, uint64_t* part, hipStream_t s) {
+  if (inv_temp > 0.0f) {
+    hipLaunchKernelGGL(row_stats_kernel, dim3(rows), dim3(SP_THREADS), 0, s, x, V, inv_temp,
+                       top_k, top_p, st);
+    return launch_status();
+  }
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(SP_NSPLIT, rows), dim3(256), 0, s, x, V, part);
+  int rc = launch_status();
+  if (rc) return rc;
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, s, (const uint64_t*)part, st,
+                     (int32_t*)nullptr);
+  return launch_status();
+}
+
+static long long stats_bytes(long long rows) {
+  return rows * (long long)(sizeof(RowStat) + SP_NSPLIT * sizeof(uint64_t));
+}
+
 LOLLM_API long long lollm_spec_workspace_bytes(int B, int k, int with_draft) {
   if (B <= 0 || k < 0) return -1;
-  return (long long)(B * (k + 1) + (with_draft ? B * k : 0)) * (long long)sizeof(RowStat);
+  return stats_bytes((long long)B * (k + 1) + (with_draft ? (long long)B * k : 0));
+}
+
+LOLLM_API long long lollm_sample_workspace_bytes(int rows) {
+  if (rows <= 0) return -1;
+  return stats_bytes(rows);
 }
 
 LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int32_t* drafts,
@@ -472,19 +658,21 @@ LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int
                                 long long workspace_bytes, void* stream) {
   if (!target || !n_accepted || !next_token || !workspace || B <= 0 || k < 0) return LOLLM_EINVAL;
   if (k > 0 && !drafts) return LOLLM_EINVAL;
+  if (k > 64) return LOLLM_EUNSUPPORTED;
   if (!sampler_args_ok(V, top_p, inv_temperature)) return LOLLM_EUNSUPPORTED;
   if (workspace_bytes < lollm_spec_workspace_bytes(B, k, draft != nullptr)) return LOLLM_EINVAL;
   hipStream_t st = (hipStream_t)stream;
+  const int rt = B * (k + 1), rd = draft ? B * k : 0;
   RowStat* st_t = (RowStat*)workspace;
-  RowStat* st_d = st_t + B * (k + 1);
-  hipLaunchKernelGGL(row_stats_kernel, dim3(B * (k + 1)), dim3(SP_THREADS), 0, st,
-                     (const uint16_t*)target, V, inv_temperature, top_k, top_p, st_t);
-  int rc = launch_status();
+  RowStat* st_d = st_t + rt;
+  uint64_t* part = (uint64_t*)(st_d + rd);
+  int rc = launch_row_stats((const uint16_t*)target, rt, V, inv_temperature, top_k, top_p, st_t,
+                            part, st);
   if (rc) return rc;
   if (draft && k > 0) {
-    hipLaunchKernelGGL(row_stats_kernel, dim3(B * k), dim3(SP_THREADS), 0, st,
-                       (const uint16_t*)draft, V, inv_temperature, top_k, top_p, st_d);
-    if ((rc = launch_status())) return rc;
+    rc = launch_row_stats((const uint16_t*)draft, rd, V, inv_temperature, top_k, top_p, st_d,
+                          part + (size_t)rt * SP_NSPLIT, st);
+    if (rc) return rc;
   }
   hipLaunchKernelGGL(spec_accept_kernel, dim3(B), dim3(SP_THREADS), 0, st, (const uint16_t*)target,
                      (const uint16_t*)draft, drafts, k, V, inv_temperature, seed, offset, offset_dev,
@@ -498,12 +686,21 @@ LOLLM_API int lollm_sample_rows(const void* logits, int rows, int V, float inv_t
                                 void* workspace, long long workspace_bytes, void* stream) {
   if (!logits || !out || !workspace || rows <= 0 || slot < 0) return LOLLM_EINVAL;
   if (!sampler_args_ok(V, top_p, inv_temperature)) return LOLLM_EUNSUPPORTED;
-  if (workspace_bytes < (long long)rows * (long long)sizeof(RowStat)) return LOLLM_EINVAL;
+  if (workspace_bytes < stats_bytes(rows)) return LOLLM_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   RowStat* stats = (RowStat*)workspace;
-  hipLaunchKernelGGL(row_stats_kernel, dim3(rows), dim3(SP_THREADS), 0, st,
-                     (const uint16_t*)logits, V, inv_temperature, top_k, top_p, stats);
-  int rc = launch_status();
+  uint64_t* part = (uint64_t*)(stats + rows);
+  if (!(inv_temperature > 0.0f)) {  // greedy: the split argmax writes the tokens directly
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(SP_NSPLIT, rows), dim3(256), 0, st,
+                       (const uint16_t*)logits, V, part);
+    int rc = launch_status();
+    if (rc) return rc;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, st, (const uint64_t*)part,
+                       (RowStat*)nullptr, out);
+    return launch_status();
+  }
+  int rc = launch_row_stats((const uint16_t*)logits, rows, V, inv_temperature, top_k, top_p, stats,
+                            part, st);
   if (rc) return rc;
   hipLaunchKernelGGL(sample_rows_kernel, dim3(rows), dim3(SP_THREADS), 0, st,
                      (const uint16_t*)logits, V, inv_temperature, seed, offset, offset_dev, row_base,

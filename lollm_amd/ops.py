@@ -216,13 +216,21 @@ def spec_accept(target, draft, drafts, temperature, top_k=0, top_p=1.0, seed=0, 
     return n_accepted, next_token
 
 
+def sample_workspace_bytes(rows):
+    n = _lib.lib().lollm_sample_workspace_bytes(rows)
+    if n < 0:
+        raise ValueError("rows must be positive")
+    return n
+
+
 def sample_rows(logits, temperature, top_k=0, top_p=1.0, seed=0, offset=0, row_base=0, slot=0,
                 *, offset_dev=None, workspace=None, out=None):
     """One token per row of logits (rows, V) bf16.  Returns (rows,) int32."""
     rows, V = logits.shape
     _need(logits, "logits", torch.bfloat16)
     if workspace is None:
-        workspace = torch.empty(rows * 24, dtype=torch.uint8, device=logits.device)
+        workspace = torch.empty(sample_workspace_bytes(rows), dtype=torch.uint8,
+                                device=logits.device)
     _need(workspace, "workspace")
     if out is None:
         out = torch.empty(rows, dtype=torch.int32, device=logits.device)

@@ -141,7 +141,7 @@ class SpecDecoder:
         self.accept_hist = torch.zeros(k + 1, **i32)       # accepted-length histogram
         self.spec_ws = torch.empty(max(ops._lib.lib().lollm_spec_workspace_bytes(batch, k, 1), 16),
                                    dtype=torch.uint8, device=dev)
-        self.row_ws = torch.empty(batch * 24, dtype=torch.uint8, device=dev)
+        self.row_ws = torch.empty(ops.sample_workspace_bytes(batch), dtype=torch.uint8, device=dev)
         self.mtp_ws = model.attn_workspace(batch, 1, max(k, 1))
         self.draft_logits = (torch.empty(batch, k, cfg.vocab_size, dtype=torch.bfloat16, device=dev)
                              if self.draft_mode == "sample" else None)

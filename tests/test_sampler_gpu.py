@@ -96,3 +96,45 @@ def test_offset_from_device_memory():
     a = ops.spec_accept(tgt.cuda(), drf.cuda(), drafts.cuda(), 0.7, 0, 0.95, 5, 41)
     b = ops.spec_accept(tgt.cuda(), drf.cuda(), drafts.cuda(), 0.7, 0, 0.95, 5, 0, offset_dev=off)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_spec_accept_full_vocab_late_rejections_and_bonus():
+    """Full vocabulary with drafts at a dominant logit for the first j_b positions of
+    sequence b and a flat row after: rejections at every position 0..k and all-accepted
+    bonus draws both occur (the C4 workload itself rejects almost always at 0)."""
+    from lollm_amd import ops
+    B, k, V = 16, 3, 151936
+    gen = torch.Generator().manual_seed(21)
+    x = torch.randn(B, k + 1, V, generator=gen) * 3
+    drafts = torch.randint(0, V, (B, k), generator=gen, dtype=torch.int32)
+    for b in range(B):
+        j = b % (k + 1)                       # positions < j are near-certain accepts
+        for i in range(j):
+            x[b, i, drafts[b, i]] = 60.0
+    tgt = x.bfloat16()
+    inv = S.inv_temperature(0.7)
+    seen = set()
+    for off in (0, 5):
+        na_ref, nt_ref = S.spec_accept(tgt, None, drafts.numpy(), inv, 0, 0.95, 13, off)
+        na, nt = ops.spec_accept(tgt.cuda(), None, drafts.cuda(), 0.7, 0, 0.95, 13, off)
+        assert np.array_equal(na.cpu().numpy(), na_ref)
+        assert np.array_equal(nt.cpu().numpy(), nt_ref)
+        seen.update(int(a) for a in na_ref)
+    assert seen == set(range(k + 1))
+
+
+@pytest.mark.parametrize("temp", [0.0, 0.8])
+def test_sample_rows_vocab_beyond_register_rows(temp):
+    """A vocabulary larger than the rows the statistics kernel holds in registers
+    (19 x 1024 chunks of 8 = 155648 tokens): the tail is re-read from memory."""
+    from lollm_amd import ops
+    V = 200000
+    gen = torch.Generator().manual_seed(5)
+    x = (torch.randn(3, V, generator=gen) * 3)
+    x[1, 190000] = 40.0                      # the maximum in the tail
+    rows = x.bfloat16()
+    inv = S.inv_temperature(temp)
+    for off in (0, 3):
+        ref = S.sample_rows(rows, inv, 0, 0.9, 17, off, row_base=0, slot=1)
+        got = ops.sample_rows(rows.cuda(), temp, 0, 0.9, 17, off, row_base=0, slot=1)
+        assert np.array_equal(got.cpu().numpy(), ref)
