@@ -174,8 +174,9 @@ def gdn_layer_roofline(model, dec, iters=50):
     gbs = byt / us / 1e3
     return {"kernel": "lollm::gdn_layer_verify_kernel", "shape": f"B={B} T={T} Hv=32 Hk=16 D=128",
             "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "avg_us": round(us, 2),
-            "bytes_per_launch": byt}
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": measured_traffic("lollm::gdn_layer_verify_kernel", f"B={B} T={T} Hv=32 Hk=16 D=128"),
+            "avg_us": round(us, 2), "bytes_per_launch": byt}
 
 
 # ------------------------------------------------------------------------------------
@@ -304,6 +305,62 @@ def cpu_baseline(raw, cfg, keep, dec, k, temperature, top_p, seed):
             "step_seconds": round(step_s, 3)}
 
 
+
+# ------------------------------------------------------------------------------------
+# HBM traffic of the roofline kernel: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs over
+# `python3 bench.py --pmc-probe`, calibrated by a plain copy-like kernel of known size
+# in the same process; the measured figures are committed in profiles/traffic.json
+# ------------------------------------------------------------------------------------
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+PROBE_COPY_BYTES = 256 << 20
+
+
+def pmc_probe(B=16, T=4, launches=20):
+    """Launch only the roofline kernel (the fused GDN layer at the step's shape, inputs
+    of the dense 8B-class layer) `launches` times, then torch.neg over 256 MiB (reads
+    and writes PROBE_COPY_BYTES each) 5 times as the counter calibration."""
+    import torch
+    from lollm_amd import ops
+    Hk, Hv, D, K, S = 16, 32, 128, 4, 4
+    C = 2 * Hk * D + Hv * D
+    P = -(-(C + Hv * D + 2 * Hv) // 8) * 8
+    W = K - 1 + S
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    proj = torch.randn(B, T, P, device="cuda", generator=g).bfloat16()
+    conv_w = (0.5 * torch.randn(C, K, device="cuda", generator=g)).bfloat16()
+    A_log = torch.randn(Hv, device="cuda", generator=g) * 0.5
+    dt_bias = torch.randn(Hv, device="cuda", generator=g) * 0.5
+    norm_w = torch.ones(D, device="cuda").bfloat16()
+    win = torch.zeros(B, 2 * W, C, device="cuda").bfloat16()
+    rec = 0.02 * torch.randn(B, 2 * S, Hv, D, D, device="cuda", generator=g)
+    conv_off = torch.zeros(B, dtype=torch.int32, device="cuda")
+    rec_slot = torch.zeros(B, dtype=torch.int32, device="cuda")
+    out = torch.empty(B, T, Hv * D, dtype=torch.bfloat16, device="cuda")
+    for _ in range(launches):
+        ops.gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, False,
+                      B, T, Hk, Hv, D, K, 1e-6, out=out)
+    x = torch.randn(PROBE_COPY_BYTES // 4, device="cuda", generator=g)
+    y = torch.empty_like(x)
+    for _ in range(5):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    log(f"pmc probe: {launches} x gdn_layer B={B} T={T}, 5 x neg over {PROBE_COPY_BYTES} bytes")
+
+
+def measured_traffic(kernel, shape):
+    """HBM bytes per launch from the committed counter runs, if they cover this kernel
+    and shape (None otherwise)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel") != kernel or t.get("shape") != shape:
+        return None
+    return t.get("traffic_bytes")
+
+
 # ------------------------------------------------------------------------------------
 def main():
     ap = argparse.ArgumentParser()
@@ -315,6 +372,8 @@ def main():
     ap.add_argument("--k", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-isolated", action="store_true", help="skip the isolated kernels")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only launch the roofline kernel and a copy calibration (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the workload; --gpus {args.gpus} is not "
@@ -323,6 +382,9 @@ def main():
     import torch
     from lollm_amd import _lib
     _lib.lib()                                    # fail loudly if the kernels are not built
+    if args.pmc_probe:
+        pmc_probe()
+        return
     temperature, top_p, seed = 0.7, 0.95, 5
     t0 = time.time()
     raw, cfg, model, mtp, keep = build_8b(seed)
