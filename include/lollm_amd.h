@@ -158,6 +158,32 @@ int lollm_attn_prologue(const void* qkv, const void* q_norm_w, const void* k_nor
                         int Hkv, int D, int rotary_dim, float eps, void* q_out, void* gate_out,
                         void* k_cache, void* v_cache, int max_len, void* stream);
 
+/* Few-row weight GEMM: y = x W^T for x with M <= 64 rows (the verify pass over
+ * B x (1 + k) positions, the draft pass over B), bf16 in / fp32 accumulate / bf16 out.
+ *
+ * Replaces: the bias-free nn.Linear projections of the decoder and MTP head when the
+ * rows are few -- in_proj_qkv|z|b|a and out_proj (src/qwen3_5/blocks.py:255-262,
+ * 309-329), q|k|v_proj and o_proj (blocks.py:199-236), gate|up and down_proj
+ * (blocks.py:332-342), lm_head (modeling_qwen3_5.py:73,99) and mtp.fc (mtp.py:61-73).
+ *
+ * lollm_gemm_tile_weights re-lays an (N, K) row-major bf16 weight once, at load, into
+ * 1 KB blocks in MFMA operand order (N * K elements): block (t, s) for rows 16 t ..
+ * 16 t + 15 and k 32 s .. 32 s + 31 at element (t * K / 32 + s) * 512, lane L = 16 g + r
+ * holding row 16 t + r, k 32 s + 8 g .. + 8.  epilogue 1 (SwiGLU) takes W = [gate;
+ * up] (N = 2F) and interleaves gate / up rows 8 by 8.
+ *
+ * lollm_gemm: A (M, lda) bf16; Wt the tiled weight; C (M, ldc) bf16 with N columns, or
+ * N / 2 = bf16(bf16(silu(bf16(x gate^T))) * bf16(x up^T)) for epilogue 1
+ * (blocks.py:341-342 with the reference's bf16 tensors); workspace: fp32 pieces of the
+ * column groups cut between workgroups, lollm_gemm_workspace_bytes(M, N, K, grid)
+ * bytes; grid: workgroups (0 = two per CU, at most 1024).
+ * Supported: 1 <= M <= 64, N % 64 == 0, K % 128 == 0, lda % 8 == 0. */
+int lollm_gemm_tile_weights(const void* W, void* Wt, int N, int K, int epilogue, void* stream);
+long long lollm_gemm_workspace_bytes(int M, int N, int K, int grid);
+int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, long long ldc, int M,
+               int N, int K, int epilogue, void* workspace, long long workspace_bytes, int grid,
+               void* stream);
+
 /* The Gated DeltaNet mixer from the in_proj outputs to the gated-norm output
  * (GatedDeltaNet.forward, blocks.py:288-329, between in_proj and out_proj):
  * causal conv + SiLU, beta / g gating, L2-normalised delta-rule scan, gated RMSNorm.

@@ -1,0 +1,327 @@
+// Weight-streaming GEMM for the few-row projections of the speculative step (gfx950):
+// C[M, N] = A[M, K] W[N, K]^T with M <= 64 (the 1 + k verify positions of B sequences,
+// or the B draft positions), bf16 in, fp32 accumulate, bf16 out.  Every weight byte is
+// read once per call, so the kernel is an HBM stream of W with 64 MACs per weight at
+// most; it replaces F.linear for in_proj / out_proj / q,k,v / o_proj / gate_up / down /
+// lm_head / MTP fc (src/qwen3_5/blocks.py:199-236,288-342, modeling_qwen3_5.py:73-99,
+// mtp.py:61-73) when the rows are few.
+//
+// Weight layout (tiled once at load by lollm_gemm_tile_weights): 1 KB blocks in the
+// order the 16x16x32 bf16 MFMA consumes them.  Block (t, s) -- n-tile t (16 rows),
+// k-step s (32 k) -- sits at element offset (t * K / 32 + s) * 512, and lane L = 16 g + r
+// of the block holds row 16 t + r, k = 32 s + 8 g .. + 8.  A wave's load of one block
+// is one coalesced 1 KB read straight into the MFMA A operand: no LDS for weights.
+// The SwiGLU layout interleaves gate and up rows 8 by 8 (tile t = gate rows 8t..8t+7,
+// then up rows 8t..8t+7) so a lane and its partner 32 lanes away hold gate and up of
+// the same output columns.
+//
+// Work decomposition: a group = 64 output columns (4 n-tiles, one per wave), a unit =
+// (group, 128-k stage).  Units are laid end to end group-major and dealt out in equal
+// contiguous ranges to a fixed grid (two workgroups per CU), so every workgroup streams
+// the same number of weight bytes whatever N is (N / 64 groups over 256 CUs would run
+// uneven rounds).  The activation tile of each stage (M x 128) is staged in LDS and
+// shared by the 4 waves; weight loads run 4 units ahead in a register ring, activation
+// loads 2 units ahead.  A group one workgroup covers whole is stored directly (with
+// the epilogue); a group cut between workgroups leaves fp32 pieces in slot w + group,
+// merged by gemm_fixup_kernel.
+#include "common.h"
+
+namespace lollm {
+
+typedef __bf16 gm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float gm_f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int GM_KC = 128;                  // k per unit
+constexpr int GM_KS = GM_KC / 32;           // MFMA k-steps per unit
+constexpr int GM_COLS = 64;                 // output columns (tiled rows) per group
+constexpr int GM_PITCH = GM_KC * 2 + 16;    // padded bytes per activation row in LDS
+constexpr int GM_P = 4;                     // weight units in flight per wave
+constexpr int GM_MAXW = 1024;               // grid limit (fixup piece table)
+
+enum { GM_EPI_NONE = 0, GM_EPI_SWIGLU = 1 };
+
+struct GemmArgs {
+  const uint16_t* A;     // (M, K) activations, row stride lda
+  const uint16_t* Wt;    // tiled weights
+  uint16_t* C;           // (M, ldc)
+  float* part;           // (nw + G) x M x 64 fp32 pieces
+  long long lda, ldc;
+  int M, N, K, G, SK, nw, epi;
+  long long U;
+};
+
+__device__ __forceinline__ void gm_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ float gm_silu_bf16(float g) {
+  // the unfused path rounds the GEMM output, silu's output and the product to bf16
+  const float gr = round_bf16(g);
+  return round_bf16(gr / (1.f + __expf(-gr)));
+}
+
+__device__ __forceinline__ long long gm_begin(long long U, int w, int nw) { return U * w / nw; }
+__device__ __forceinline__ int gm_owner(long long U, long long u, int nw) {
+  return (int)(((u + 1) * nw - 1) / U);
+}
+
+__global__ void gemm_tile_kernel(const uint16_t* __restrict__ W, uint16_t* __restrict__ Wt, int N,
+                                 int K, int mode) {
+  const size_t blk = blockIdx.x;
+  const int ks = K / 32;
+  const int t = (int)(blk / ks), s = (int)(blk % ks);
+  const int L = threadIdx.x, r = L & 15, g = L >> 4;
+  int src = 16 * t + r;
+  if (mode == GM_EPI_SWIGLU) src = (r < 8 ? 0 : N / 2) + 8 * t + (r & 7);
+  const uint4 v = *reinterpret_cast<const uint4*>(W + (size_t)src * K + 32 * s + 8 * g);
+  *reinterpret_cast<uint4*>(Wt + blk * 512 + L * 8) = v;
+}
+
+template <int MT>
+__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  constexpr int CPR = GM_KC / 8;                          // 16 B chunks per activation row
+  constexpr int ACH = (MT * 16 * CPR + 255) / 256;        // activation chunks per thread
+  __shared__ __attribute__((aligned(16))) unsigned char al[2][MT * 16 * GM_PITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int w = blockIdx.x;
+  const long long u0 = gm_begin(a.U, w, a.nw), u1 = gm_begin(a.U, w + 1, a.nw);
+  if (u0 >= u1) return;
+  const int kt = a.K / 32;
+  const uint16_t* wlane = a.Wt + (size_t)wave * kt * 512 + lane * 8;
+
+  v4u wr[GM_P][GM_KS], an[2][ACH];
+  // weights of unit u for this wave: n-tile 4 g + wave, k-steps 4 st .. 4 st + 3
+  auto wload = [&](v4u* dst, long long u) {
+    const int g = (int)(u / a.SK), st = (int)(u % a.SK);
+    const uint16_t* p = wlane + ((size_t)4 * g * kt + (size_t)st * GM_KS) * 512;
+#pragma unroll
+    for (int q = 0; q < GM_KS; ++q)
+      dst[q] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p + q * 512));
+  };
+  auto aload = [&](v4u* dst, long long u) {
+    const int k0 = (int)(u % a.SK) * GM_KC;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = i * 256 + tid, row = c / CPR, col = c % CPR;
+      if (row < MT * 16) {
+        const int rr = row < a.M ? row : a.M - 1;
+        dst[i] = *reinterpret_cast<const v4u*>(a.A + (size_t)rr * a.lda + k0 + col * 8);
+      }
+    }
+  };
+
+  gm_f32x4 acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int p = 0; p < GM_P; ++p)
+    if (u0 + p < u1) wload(wr[p], u0 + p);
+  aload(an[0], u0);
+  if (u0 + 1 < u1) aload(an[1], u0 + 1);
+  bool whole_from_start = (u0 % a.SK) == 0;
+
+  // One unit: stage activations, 4 k-steps of MFMA, refill the rings; at a group's
+  // last unit (or the range's end) write the group's result or piece.
+#define GM_UNIT(J)                                                                            \
+  {                                                                                           \
+    const long long u = ub + (J);                                                             \
+    if (u < u1) {                                                                             \
+      constexpr int set = (J) & 1, slot = (J) % GM_P;                                         \
+      _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                       \
+        const int c = i * 256 + tid, row = c / CPR, col = c % CPR;                            \
+        if (row < MT * 16) *reinterpret_cast<v4u*>(&al[set][row * GM_PITCH + col * 16]) = an[set][i]; \
+      }                                                                                       \
+      gm_lds_barrier();                                                                       \
+      if (u + 2 < u1) aload(an[set], u + 2);                                                  \
+      _Pragma("unroll") for (int q = 0; q < GM_KS; ++q) {                                     \
+        _Pragma("unroll") for (int i = 0; i < MT; ++i) {                                      \
+          const gm_bf16x8 ab = *reinterpret_cast<const gm_bf16x8*>(                           \
+              &al[set][(16 * i + l16) * GM_PITCH + q * 64 + g4 * 16]);                        \
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                                   \
+              __builtin_bit_cast(gm_bf16x8, wr[slot][q]), ab, acc[i], 0, 0, 0);               \
+        }                                                                                     \
+      }                                                                                       \
+      if (u + GM_P < u1) wload(wr[slot], u + GM_P);                                           \
+      const int st = (int)(u % a.SK);                                                         \
+      if (st == a.SK - 1 || u == u1 - 1) {                                                    \
+        finish((int)(u / a.SK), whole_from_start && st == a.SK - 1);                          \
+        whole_from_start = true;                                                              \
+      }                                                                                       \
+    }                                                                                         \
+  }
+
+  // lane holds, for m-tile i, rows m = 16 i + l16 and tiled columns 4 g4 .. 4 g4 + 3 of
+  // n-tile 4 g + wave
+  auto finish = [&](int g, bool whole) {
+    if (whole) {
+      if (a.epi == GM_EPI_SWIGLU) {
+        // partner lane (g4 ^ 2) holds the other half of the same output columns
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          float other[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) other[j] = __shfl_xor(acc[i][j], 32, 64);
+          const int m = 16 * i + l16;
+          if (g4 < 2 && m < a.M) {
+            float y[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y[j] = round_bf16(gm_silu_bf16(acc[i][j]) * round_bf16(other[j]));
+            const int col = 8 * (4 * g + wave) + 4 * g4;
+            *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+                make_uint2((uint32_t)f32_to_bf16(y[0]) | ((uint32_t)f32_to_bf16(y[1]) << 16),
+                           (uint32_t)f32_to_bf16(y[2]) | ((uint32_t)f32_to_bf16(y[3]) << 16));
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const int m = 16 * i + l16;
+          if (m < a.M) {
+            const int col = GM_COLS * g + 16 * wave + 4 * g4;
+            *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+                make_uint2((uint32_t)f32_to_bf16(acc[i][0]) | ((uint32_t)f32_to_bf16(acc[i][1]) << 16),
+                           (uint32_t)f32_to_bf16(acc[i][2]) | ((uint32_t)f32_to_bf16(acc[i][3]) << 16));
+          }
+        }
+      }
+    } else {
+      // a piece: raw fp32 sums of the group's 64 tiled columns, slot w + g (pieces are
+      // ordered in both w and g, so the slot is unique)
+      float* pp = a.part + ((size_t)w + g) * ((size_t)a.M * GM_COLS);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = 16 * i + l16;
+        if (m < a.M)
+          *reinterpret_cast<float4*>(pp + (size_t)m * GM_COLS + 16 * wave + 4 * g4) =
+              make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+
+  static_assert(GM_P == 4, "the unit loop is unrolled by 4");
+  for (long long ub = u0; ub < u1; ub += 4) {
+    GM_UNIT(0) GM_UNIT(1) GM_UNIT(2) GM_UNIT(3)
+  }
+#undef GM_UNIT
+}
+
+// Merge the pieces of group blockIdx.x: sum the live pieces' fp32 columns, apply the
+// epilogue, store bf16.  Groups one workgroup finished are skipped.
+__global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
+  const int g = blockIdx.x;
+  const long long first = (long long)g * a.SK, last = first + a.SK - 1;
+  const int wf = gm_owner(a.U, first, a.nw), wl = gm_owner(a.U, last, a.nw);
+  if (wf == wl) return;
+  const size_t piece = (size_t)a.M * GM_COLS;
+  if (a.epi == GM_EPI_SWIGLU) {
+    // item = (m, tile, half): gate raw columns 16 tile + 4 half .. +4, up 8 further
+    for (int it = threadIdx.x; it < a.M * 8; it += 256) {
+      const int m = it / 8, tile = (it % 8) / 2, h = it % 2;
+      const int cg = 16 * tile + 4 * h;
+      float4 sg = make_float4(0.f, 0.f, 0.f, 0.f), su = sg;
+      for (int w = wf; w <= wl; ++w) {
+        if (gm_begin(a.U, w, a.nw) >= gm_begin(a.U, w + 1, a.nw)) continue;
+        const float* pp = a.part + ((size_t)w + g) * piece + (size_t)m * GM_COLS;
+        const float4 x = *reinterpret_cast<const float4*>(pp + cg);
+        const float4 y = *reinterpret_cast<const float4*>(pp + cg + 8);
+        sg.x += x.x; sg.y += x.y; sg.z += x.z; sg.w += x.w;
+        su.x += y.x; su.y += y.y; su.z += y.z; su.w += y.w;
+      }
+      const float gv[4] = {sg.x, sg.y, sg.z, sg.w}, uv[4] = {su.x, su.y, su.z, su.w};
+      float yv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) yv[j] = round_bf16(gm_silu_bf16(gv[j]) * round_bf16(uv[j]));
+      const int col = 8 * (4 * g + tile) + 4 * h;
+      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+          make_uint2((uint32_t)f32_to_bf16(yv[0]) | ((uint32_t)f32_to_bf16(yv[1]) << 16),
+                     (uint32_t)f32_to_bf16(yv[2]) | ((uint32_t)f32_to_bf16(yv[3]) << 16));
+    }
+  } else {
+    for (int it = threadIdx.x; it < a.M * (GM_COLS / 4); it += 256) {
+      const int m = it / (GM_COLS / 4), c4 = (it % (GM_COLS / 4)) * 4;
+      float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int w = wf; w <= wl; ++w) {
+        if (gm_begin(a.U, w, a.nw) >= gm_begin(a.U, w + 1, a.nw)) continue;
+        const float4 x = *reinterpret_cast<const float4*>(a.part + ((size_t)w + g) * piece +
+                                                          (size_t)m * GM_COLS + c4);
+        s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
+      }
+      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + GM_COLS * g + c4) =
+          make_uint2((uint32_t)f32_to_bf16(s.x) | ((uint32_t)f32_to_bf16(s.y) << 16),
+                     (uint32_t)f32_to_bf16(s.z) | ((uint32_t)f32_to_bf16(s.w) << 16));
+    }
+  }
+}
+
+}  // namespace lollm
+
+using namespace lollm;
+
+static int gemm_grid(int grid) {
+  if (grid > 0) return grid;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return -1;
+  return cus > 0 ? 2 * cus : -1;
+}
+
+static bool gemm_shape_ok(int M, int N, int K, int epi) {
+  if (M <= 0 || M > 64 || N <= 0 || K <= 0) return false;
+  if (N % GM_COLS || K % GM_KC) return false;
+  if (epi != GM_EPI_NONE && epi != GM_EPI_SWIGLU) return false;
+  return true;
+}
+
+LOLLM_API int lollm_gemm_tile_weights(const void* W, void* Wt, int N, int K, int epilogue,
+                                      void* stream) {
+  if (!W || !Wt || N <= 0 || K <= 0 || N % GM_COLS || K % GM_KC) return LOLLM_EINVAL;
+  if (epilogue != GM_EPI_NONE && epilogue != GM_EPI_SWIGLU) return LOLLM_EINVAL;
+  hipLaunchKernelGGL(gemm_tile_kernel, dim3((unsigned)((size_t)(N / 16) * (K / 32))), dim3(64), 0,
+                     (hipStream_t)stream, (const uint16_t*)W, (uint16_t*)Wt, N, K, epilogue);
+  return launch_status();
+}
+
+LOLLM_API long long lollm_gemm_workspace_bytes(int M, int N, int K, int grid) {
+  if (!gemm_shape_ok(M, N, K, GM_EPI_NONE)) return -1;
+  const int nw = gemm_grid(grid);
+  if (nw <= 0 || nw > GM_MAXW) return -1;
+  return ((long long)nw + N / GM_COLS) * M * GM_COLS * (long long)sizeof(float);
+}
+
+LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, long long ldc,
+                         int M, int N, int K, int epilogue, void* workspace,
+                         long long workspace_bytes, int grid, void* stream) {
+  if (!A || !Wt || !C || !workspace) return LOLLM_EINVAL;
+  if (!gemm_shape_ok(M, N, K, epilogue)) return LOLLM_EUNSUPPORTED;
+  const long long outc = epilogue == GM_EPI_SWIGLU ? N / 2 : N;
+  if (lda < K || ldc < outc || lda % 8 || ldc % 4) return LOLLM_EINVAL;
+  if (grid < 0 || grid > GM_MAXW) return LOLLM_EINVAL;
+  const int nw = gemm_grid(grid);
+  if (nw <= 0 || nw > GM_MAXW) return LOLLM_EUNSUPPORTED;
+  if (workspace_bytes < ((long long)nw + N / GM_COLS) * M * GM_COLS * (long long)sizeof(float))
+    return LOLLM_EINVAL;
+  GemmArgs a;
+  a.A = (const uint16_t*)A; a.Wt = (const uint16_t*)Wt; a.C = (uint16_t*)C;
+  a.part = (float*)workspace; a.lda = lda; a.ldc = ldc;
+  a.M = M; a.N = N; a.K = K; a.G = N / GM_COLS; a.SK = K / GM_KC; a.nw = nw; a.epi = epilogue;
+  a.U = (long long)a.G * a.SK;
+  hipStream_t st = (hipStream_t)stream;
+  const int mt = (M + 15) / 16;
+  switch (mt) {
+    case 1: hipLaunchKernelGGL(gemm_kernel<1>, dim3(nw), dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(gemm_kernel<2>, dim3(nw), dim3(256), 0, st, a); break;
+    case 3: hipLaunchKernelGGL(gemm_kernel<3>, dim3(nw), dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(gemm_kernel<4>, dim3(nw), dim3(256), 0, st, a); break;
+  }
+  int rc = launch_status();
+  if (rc) return rc;
+  hipLaunchKernelGGL(gemm_fixup_kernel, dim3(a.G), dim3(256), 0, st, a);
+  return launch_status();
+}

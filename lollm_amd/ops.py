@@ -179,6 +179,71 @@ def attn_verify(q, k_cache, v_cache, kv_len, gate=None, *, grid=0, scale=None,
 
 
 # ------------------------------------------------------------------------------------
+# few-row weight-streaming GEMM
+# ------------------------------------------------------------------------------------
+GEMM_NONE, GEMM_SWIGLU = 0, 1
+GEMM_MAX_ROWS = 64
+_gemm_ws = {}
+
+
+def gemm_supported(N, K, epilogue=GEMM_NONE):
+    return N % 64 == 0 and K % 128 == 0 and (epilogue == GEMM_NONE or (N // 2) % 32 == 0)
+
+
+def gemm_tile_weights(weight, epilogue=GEMM_NONE):
+    """The (N, K) bf16 weight re-laid in the 1 KB MFMA-operand blocks lollm_gemm streams
+    (for GEMM_SWIGLU, weight = [gate; up] and gate/up rows are interleaved 8 by 8)."""
+    N, K = weight.shape
+    _need(weight, "weight", torch.bfloat16)
+    out = torch.empty(N * K, dtype=torch.bfloat16, device=weight.device)
+    rc = _lib.lib().lollm_gemm_tile_weights(_ptr(weight), _ptr(out), N, K, epilogue, _stream())
+    _lib.check(rc, "lollm_gemm_tile_weights")
+    return out
+
+
+def gemm_workspace_bytes(M, N, K, grid=0):
+    n = _lib.lib().lollm_gemm_workspace_bytes(M, N, K, grid)
+    if n < 0:
+        raise ValueError("unsupported GEMM shape")
+    return n
+
+
+def gemm_workspace(nbytes, device):
+    """The shared fp32 piece buffer of lollm_gemm (one per device, grown on demand;
+    reserve the largest size before capturing a graph)."""
+    key = torch.device(device)
+    ws = _gemm_ws.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=key)
+        _gemm_ws[key] = ws
+    return ws
+
+
+def gemm(x, tiled, N, K, epilogue=GEMM_NONE, out=None, grid=0):
+    """y = x W^T for x (..., K) bf16 with at most 64 rows; `tiled` from
+    gemm_tile_weights.  Returns (..., N), or (..., N / 2) = silu(gate) * up for
+    GEMM_SWIGLU."""
+    lead = x.shape[:-1]
+    M = x.numel() // K
+    if x.shape[-1] != K:
+        raise ValueError(f"x has {x.shape[-1]} features, expected {K}")
+    if M > GEMM_MAX_ROWS or M <= 0:
+        raise ValueError(f"lollm_gemm takes 1..{GEMM_MAX_ROWS} rows, got {M}")
+    x = x.contiguous()
+    _need(x, "x", torch.bfloat16)
+    _need(tiled, "tiled", torch.bfloat16, (N * K,))
+    oc = N // 2 if epilogue == GEMM_SWIGLU else N
+    if out is None:
+        out = torch.empty(*lead, oc, dtype=torch.bfloat16, device=x.device)
+    _need(out, "out", torch.bfloat16, (*lead, oc))
+    ws = gemm_workspace(gemm_workspace_bytes(M, N, K, grid), x.device)
+    rc = _lib.lib().lollm_gemm(_ptr(x), K, _ptr(tiled), _ptr(out), oc, M, N, K, epilogue, _ptr(ws),
+                               ws.numel(), grid, _stream())
+    _lib.check(rc, "lollm_gemm")
+    return out
+
+
+# ------------------------------------------------------------------------------------
 # speculative sampling
 # ------------------------------------------------------------------------------------
 def inv_temperature(temperature: float) -> float:

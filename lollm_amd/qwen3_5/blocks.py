@@ -3,8 +3,10 @@
 Each block keeps the reference block's parameters (src/qwen3_5/blocks.py:186-342) but
 stores them the way the verify step consumes them: projections that read the same
 input are concatenated into one GEMM weight (GDN in_proj_qkv|z|b|a, attention
-q|k|v, MLP gate|up), so a layer issues 4 GEMMs (hipBLASLt via torch) plus fused HIP
-kernels for everything between them.
+q|k|v, MLP gate|up), so a layer issues 4 GEMMs plus fused HIP kernels for everything
+between them.  A GEMM over at most 64 rows (the verify and draft passes) streams a
+tiled copy of its weight through lollm_gemm, with SiLU(gate) * up fused into the
+gate|up GEMM; longer calls (the prefill) use hipBLASLt on the row-major weight.
 """
 
 from __future__ import annotations
@@ -18,6 +20,60 @@ from .config import Qwen3_5Config
 
 def _cat_rows(*ws):
     return torch.cat([w.reshape(w.shape[0], -1) for w in ws], 0).contiguous()
+
+
+class Projection:
+    """y = x W^T (blocks.py's nn.Linear layers, no bias).  Keeps the row-major weight
+    for hipBLASLt (F.linear) and a tiled copy for lollm_gemm (<= 64 rows).
+    epilogue=GEMM_SWIGLU: W = [gate; up], y = silu(x gate^T) * x up^T (blocks.py:341-342).
+
+    For a row count lollm_gemm supports, the first eager call times both paths (three
+    runs each, HIP events) and keeps the faster one for that row count; later calls --
+    and HIP-graph captures -- reuse the choice.  A call under capture with no choice
+    recorded yet takes lollm_gemm."""
+
+    def __init__(self, weight, epilogue=ops.GEMM_NONE):
+        self.weight = weight.to(torch.bfloat16).contiguous()
+        self.N, self.K = self.weight.shape
+        self.epilogue = epilogue
+        self.tiled = (ops.gemm_tile_weights(self.weight, epilogue)
+                      if self.weight.is_cuda and ops.gemm_supported(self.N, self.K, epilogue)
+                      else None)
+        self.choice = {}            # rows -> "gemm" | "blas"
+
+    def workspace_bytes(self, rows=ops.GEMM_MAX_ROWS):
+        return ops.gemm_workspace_bytes(rows, self.N, self.K) if self.tiled is not None else 0
+
+    def _blas(self, x):
+        y = F.linear(x, self.weight)
+        return ops.swiglu(y) if self.epilogue == ops.GEMM_SWIGLU else y
+
+    def _gemm(self, x):
+        return ops.gemm(x, self.tiled, self.N, self.K, self.epilogue)
+
+    def _pick(self, x, rows):
+        if torch.cuda.is_current_stream_capturing():
+            return "gemm"
+        times = {}
+        for name, fn in (("gemm", self._gemm), ("blas", self._blas)):
+            fn(x)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(3):
+                fn(x)
+            e1.record()
+            e1.synchronize()
+            times[name] = e0.elapsed_time(e1)
+        choice = min(times, key=times.get)
+        self.choice[rows] = choice
+        return choice
+
+    def __call__(self, x):
+        rows = x.numel() // self.K
+        if self.tiled is None or rows > ops.GEMM_MAX_ROWS:
+            return self._blas(x)
+        choice = self.choice.get(rows) or self._pick(x, rows)
+        return self._gemm(x) if choice == "gemm" else self._blas(x)
 
 
 class RMSNorm:
@@ -36,14 +92,17 @@ class RMSNorm:
 
 
 class MLP:
-    """SwiGLU (blocks.py:332-342): gate|up as one GEMM, fused silu*up, down."""
+    """SwiGLU (blocks.py:332-342): gate|up as one GEMM with silu*up fused, down."""
 
     def __init__(self, gate, up, down):
-        self.w_gu = _cat_rows(gate, up)
-        self.w_down = down.contiguous()
+        self.gate_up = Projection(_cat_rows(gate, up), ops.GEMM_SWIGLU)
+        self.down = Projection(down)
+
+    def projections(self):
+        return [self.gate_up, self.down]
 
     def __call__(self, x):
-        return F.linear(ops.swiglu(F.linear(x, self.w_gu)), self.w_down)
+        return self.down(self.gate_up(x))
 
 
 class GatedDeltaNet:
@@ -56,27 +115,34 @@ class GatedDeltaNet:
         w = [W[p + "in_proj_qkv.weight"], W[p + "in_proj_z.weight"], W[p + "in_proj_b.weight"],
              W[p + "in_proj_a.weight"]]
         rows = cfg.conv_dim + cfg.value_dim + 2 * Hv
-        pad = (-rows) % 8                      # keep the projection row 16-byte aligned
+        pad = (-rows) % 64                     # whole 64-column GEMM groups (16-byte rows)
         if pad:
             w.append(torch.zeros(pad, cfg.hidden_size, dtype=w[0].dtype, device=w[0].device))
-        self.w_in = _cat_rows(*w)
+        self.in_proj = Projection(_cat_rows(*w))
         self.conv_w = W[p + "conv1d.weight"].reshape(cfg.conv_dim, -1).to(torch.bfloat16).contiguous()
         self.A_log = W[p + "A_log"].float().contiguous()
         self.dt_bias = W[p + "dt_bias"].float().contiguous()
         self.norm_w = W[p + "norm.weight"].to(torch.bfloat16).contiguous()
-        self.out_proj = W[p + "out_proj.weight"].contiguous()
+        self.out_proj = Projection(W[p + "out_proj.weight"])
+
+    @property
+    def w_in(self):
+        return self.in_proj.weight
+
+    def projections(self):
+        return [self.in_proj, self.out_proj]
 
     def __call__(self, x, cache, layer):
         B, T, _ = x.shape
         cfg = self.cfg
-        proj = F.linear(x, self.w_in)
+        proj = self.in_proj(x)
         s = cache.layers[layer]
         core = ops.gdn_layer(proj, self.conv_w, self.A_log, self.dt_bias, self.norm_w, s["win"],
                              cache.conv_off, s["rec"], cache.rec_slot, cache.fresh, B, T,
                              cfg.linear_num_key_heads, cfg.linear_num_value_heads,
                              cfg.linear_key_head_dim, cfg.linear_conv_kernel_dim,
                              cfg.rms_norm_eps)
-        return F.linear(core, self.out_proj)
+        return self.out_proj(core)
 
 
 def rope_inv_freq(rotary_dim, theta, device):
@@ -92,20 +158,24 @@ class GatedAttention:
 
     def __init__(self, cfg: Qwen3_5Config, W: dict, p: str, inv_freq):
         self.cfg = cfg
-        self.w_qkv = _cat_rows(W[p + "q_proj.weight"], W[p + "k_proj.weight"], W[p + "v_proj.weight"])
+        self.qkv = Projection(_cat_rows(W[p + "q_proj.weight"], W[p + "k_proj.weight"],
+                                        W[p + "v_proj.weight"]))
         self.q_norm = W[p + "q_norm.weight"].to(torch.bfloat16).contiguous()
         self.k_norm = W[p + "k_norm.weight"].to(torch.bfloat16).contiguous()
-        self.o_proj = W[p + "o_proj.weight"].contiguous()
+        self.o_proj = Projection(W[p + "o_proj.weight"])
         self.inv_freq = inv_freq
+
+    def projections(self):
+        return [self.qkv, self.o_proj]
 
     def __call__(self, x, k_cache, v_cache, lengths, kv_len, rope_pos=None, grid=0,
                  workspace=None):
         B, T, _ = x.shape
         cfg = self.cfg
-        qkv = F.linear(x, self.w_qkv)
+        qkv = self.qkv(x)
         q, gate = ops.attn_prologue(qkv, self.q_norm, self.k_norm, self.inv_freq, lengths, B, T,
                                     cfg.num_attention_heads, cfg.num_key_value_heads,
                                     cfg.head_dim, cfg.rotary_dim, cfg.rms_norm_eps, k_cache,
                                     v_cache, rope_pos=rope_pos)
         o = ops.attn_verify(q, k_cache, v_cache, kv_len, gate, grid=grid, workspace=workspace)
-        return F.linear(o, self.o_proj)
+        return self.o_proj(o)

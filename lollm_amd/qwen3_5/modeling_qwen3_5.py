@@ -17,7 +17,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import ops
-from .blocks import MLP, GatedAttention, GatedDeltaNet, RMSNorm, rope_inv_freq
+from .blocks import MLP, GatedAttention, GatedDeltaNet, Projection, RMSNorm, rope_inv_freq
 from .config import Qwen3_5Config
 from .kv import Qwen3_5Cache
 
@@ -49,14 +49,6 @@ class _Embedding:
         return F.embedding(ids, self.weight)
 
 
-class _Linear:
-    def __init__(self, weight):
-        self.weight = weight
-
-    def __call__(self, x):
-        return F.linear(x, self.weight)
-
-
 class _Inner:
     pass
 
@@ -73,10 +65,19 @@ class Qwen3_5Model:
                                           self.inv_freq)
                              for i in range(cfg.num_hidden_layers)]
         self.model.norm = RMSNorm(W["model.norm.weight"], cfg.rms_norm_eps)
-        self.lm_head = _Linear(W["lm_head.weight"])
+        self.lm_head = Projection(W["lm_head.weight"])
         self.attn_grid = 0          # attention workgroups (0: two per CU)
+        ops.gemm_workspace(max(p.workspace_bytes() for p in self.projections()), self.device)
         self._ws = {}
         self.default_extra_capacity = 4096
+
+    def projections(self):
+        """Every weight GEMM of the decoder (for workspace sizing)."""
+        out = [self.lm_head]
+        for layer in self.model.layers:
+            mixer = layer.self_attn if layer.layer_type == "full_attention" else layer.linear_attn
+            out += mixer.projections() + layer.mlp.projections()
+        return out
 
     # ---------------------------------------------------------------------------------
     def new_cache(self, batch, max_len, spec_slots=4):

@@ -25,10 +25,9 @@ three host syncs per step.  Here:
 from __future__ import annotations
 
 import torch
-import torch.nn.functional as F
 
 from .. import ops
-from .blocks import RMSNorm
+from .blocks import Projection, RMSNorm
 from .modeling_qwen3_5 import DecoderLayer, Qwen3_5Model
 from .random_init import weight_shapes
 from .weights import take_weights, to_raw
@@ -41,14 +40,18 @@ class MTP:
         eps = cfg.rms_norm_eps
         self.pre_fc_norm_embedding = RMSNorm(W["mtp.pre_fc_norm_embedding.weight"], eps)
         self.pre_fc_norm_hidden = RMSNorm(W["mtp.pre_fc_norm_hidden.weight"], eps)
-        self.fc = W["mtp.fc.weight"].contiguous()
+        self.fc = Projection(W["mtp.fc.weight"])
         self.layers = [DecoderLayer(cfg, W, "mtp.layers.0.", "full_attention", model.inv_freq)]
         self.norm = RMSNorm(W["mtp.norm.weight"], eps)
+        layer = self.layers[0]
+        ops.gemm_workspace(max(p.workspace_bytes() for p in
+                               [self.fc] + layer.self_attn.projections() + layer.mlp.projections()),
+                           model.device)
 
     def _block(self, hidden, next_emb, k_cache, v_cache, lengths, kv_len, rope_pos, ws):
         """Returns (MTP layer output before the final norm, normed output)."""
-        x = F.linear(torch.cat([self.pre_fc_norm_embedding(next_emb),
-                                self.pre_fc_norm_hidden(hidden)], -1), self.fc)
+        x = self.fc(torch.cat([self.pre_fc_norm_embedding(next_emb),
+                               self.pre_fc_norm_hidden(hidden)], -1))
         layer = self.layers[0]
         h_in = layer.input_layernorm(x)
         h = layer.self_attn(h_in, k_cache, v_cache, lengths, kv_len, rope_pos=rope_pos,

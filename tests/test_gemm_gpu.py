@@ -1,0 +1,101 @@
+"""The few-row weight-streaming GEMM (lollm_gemm) vs the oracle's `linear` (x W^T in
+fp32 on the CPU, oracle/qwen3_5_ref.py), which restates the reference's bias-free
+nn.Linear projections (src/qwen3_5/blocks.py:199-236,288-342).  The kernel accumulates
+in fp32 and rounds once to bf16, so it must sit within one bf16 rounding of the fp32
+product (rtol 1e-2 on the row scale).  Pieces merged across workgroups must give the
+same numbers as a single workgroup covering every group whole."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import qwen3_5_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def case(M, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).bfloat16()
+    return x, W
+
+
+def close(got, ref):
+    scale = ref.abs().max().item()
+    torch.testing.assert_close(got.float().cpu(), ref, rtol=1e-2, atol=1e-2 * scale)
+
+
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 33, 64])
+@pytest.mark.parametrize("N,K", [(64, 128), (192, 256), (1024, 1024), (4096, 512)])
+@pytest.mark.parametrize("grid", [0, 1, 7, 1024])
+def test_gemm_matches_oracle(M, N, K, grid):
+    from lollm_amd import ops
+    print(f"case gemm M={M} N={N} K={K} grid={grid}", flush=True)
+    x, W = case(M, N, K, seed=M * 7 + N + K)
+    ref = R.linear(x.float(), W.float())
+    Wt = ops.gemm_tile_weights(W.cuda())
+    y = ops.gemm(x.cuda(), Wt, N, K, grid=grid)
+    torch.cuda.synchronize()
+    close(y, ref)
+
+
+def test_gemm_pieces_equal_whole_groups():
+    """grid=1: every group finished by one workgroup; grid=1024: every group cut into
+    pieces and merged by the fixup kernel; both sum the same fp32 terms in k order
+    within a workgroup, so they agree to fp32 reassociation (checked at 1 bf16 ulp)."""
+    from lollm_amd import ops
+    x, W = case(64, 1024, 2048, seed=3)
+    Wt = ops.gemm_tile_weights(W.cuda())
+    a = ops.gemm(x.cuda(), Wt, 1024, 2048, grid=1).float()
+    b = ops.gemm(x.cuda(), Wt, 1024, 2048, grid=1024).float()
+    torch.testing.assert_close(a, b, rtol=8e-3, atol=8e-3 * a.abs().max().item())
+
+
+@pytest.mark.parametrize("M,grid", [(64, 0), (16, 0), (5, 1), (64, 1024)])
+def test_gemm_swiglu_epilogue(M, grid):
+    """[gate; up] with silu(gate) * up fused (blocks.py:341-342), against the oracle's
+    mlp dtype flow: bf16 GEMM outputs, silu in bf16, product in bf16."""
+    from lollm_amd import ops
+    F_ = 512
+    x, W = case(M, 2 * F_, 1024, seed=11 + M)
+    gu = R.linear(x.float(), W.float()).bfloat16()
+    ref = (F.silu(gu[:, :F_]) * gu[:, F_:]).float()
+    Wt = ops.gemm_tile_weights(W.cuda(), ops.GEMM_SWIGLU)
+    y = ops.gemm(x.cuda(), Wt, 2 * F_, 1024, ops.GEMM_SWIGLU, grid=grid)
+    torch.cuda.synchronize()
+    assert y.shape == (M, F_)
+    close(y, ref)
+
+
+def test_gemm_rejects_bad_shapes_and_workspace():
+    from lollm_amd import ops
+    x, W = case(65, 64, 128, seed=1)
+    Wt = ops.gemm_tile_weights(W.cuda())
+    with pytest.raises(ValueError):
+        ops.gemm(x.cuda(), Wt, 64, 128)                          # 65 rows
+    with pytest.raises(ValueError):
+        ops.gemm_workspace_bytes(16, 96, 128)                     # N not a multiple of 64
+    lib = ops._lib.lib()
+    y = torch.empty(16, 64, dtype=torch.bfloat16, device="cuda")
+    need = ops.gemm_workspace_bytes(16, 64, 128, 4)
+    small = torch.empty(need - 4, dtype=torch.uint8, device="cuda")
+    rc = lib.lollm_gemm(x[:16].cuda().data_ptr(), 128, Wt.data_ptr(), y.data_ptr(), 64, 16, 64, 128,
+                        0, small.data_ptr(), small.numel(), 4,
+                        torch.cuda.current_stream().cuda_stream)
+    assert rc != 0
+
+
+def test_projection_paths_agree():
+    """Projection: both paths for <= 64 rows (the timed choice and the forced other
+    one) and hipBLASLt for more rows all match the oracle."""
+    from lollm_amd.qwen3_5.blocks import Projection
+    x, W = case(80, 256, 512, seed=5)
+    p = Projection(W.cuda())
+    assert p.tiled is not None
+    ref = R.linear(x.float(), W.float())
+    close(p(x[:64].cuda()), ref[:64])
+    assert p.choice[64] in ("gemm", "blas")
+    close(p._gemm(x[:64].cuda()), ref[:64])
+    close(p._blas(x[:64].cuda()), ref[:64])
+    close(p(x.cuda()), ref)
