@@ -175,8 +175,9 @@ int lollm_attn_prologue(const void* qkv, const void* q_norm_w, const void* k_nor
  * lollm_gemm: A (M, lda) bf16; Wt the tiled weight; C (M, ldc) bf16 with N columns, or
  * N / 2 = bf16(bf16(silu(bf16(x gate^T))) * bf16(x up^T)) for epilogue 1
  * (blocks.py:341-342 with the reference's bf16 tensors); workspace: fp32 pieces of the
- * column groups cut between workgroups, lollm_gemm_workspace_bytes(M, N, K, grid)
- * bytes; grid: workgroups (0 = two per CU, at most 1024).
+ * column groups cut between workgroups, merged by a second kernel of the same call,
+ * lollm_gemm_workspace_bytes(M, N, K, grid) bytes (calls sharing one workspace must
+ * not overlap in time); grid: workgroups (0 = two per CU, at most 1024).
  * Supported: 1 <= M <= 64, N % 64 == 0, K % 128 == 0, lda % 8 == 0. */
 int lollm_gemm_tile_weights(const void* W, void* Wt, int N, int K, int epilogue, void* stream);
 long long lollm_gemm_workspace_bytes(int M, int N, int K, int grid);

@@ -23,7 +23,9 @@
 // shared by the 4 waves; weight loads run 4 units ahead in a register ring, activation
 // loads 2 units ahead.  A group one workgroup covers whole is stored directly (with
 // the epilogue); a group cut between workgroups leaves fp32 pieces in slot w + group,
-// merged by gemm_fixup_kernel.
+// merged by gemm_fixup_kernel.  (Merging in the last-arriving workgroup instead would
+// need device-scope release / acquire fences, which write back and invalidate the
+// XCD's L2 -- measured 3-10x slower here than the second launch.)
 #include "common.h"
 
 namespace lollm {
@@ -36,7 +38,7 @@ constexpr int GM_KS = GM_KC / 32;           // MFMA k-steps per unit
 constexpr int GM_COLS = 64;                 // output columns (tiled rows) per group
 constexpr int GM_PITCH = GM_KC * 2 + 16;    // padded bytes per activation row in LDS
 constexpr int GM_P = 4;                     // weight units in flight per wave
-constexpr int GM_MAXW = 1024;               // grid limit (fixup piece table)
+constexpr int GM_MAXW = 1024;               // grid limit (piece table)
 
 enum { GM_EPI_NONE = 0, GM_EPI_SWIGLU = 1 };
 
@@ -46,8 +48,7 @@ struct GemmArgs {
   uint16_t* C;           // (M, ldc)
   float* part;           // (nw + G) x M x 64 fp32 pieces
   long long lda, ldc;
-  int M, N, K, G, SK, nw, epi;
-  long long U;
+  int M, N, K, G, SK, nw, epi, U;
 };
 
 __device__ __forceinline__ void gm_lds_barrier() {
@@ -62,9 +63,9 @@ __device__ __forceinline__ float gm_silu_bf16(float g) {
   return round_bf16(gr / (1.f + __expf(-gr)));
 }
 
-__device__ __forceinline__ long long gm_begin(long long U, int w, int nw) { return U * w / nw; }
-__device__ __forceinline__ int gm_owner(long long U, long long u, int nw) {
-  return (int)(((u + 1) * nw - 1) / U);
+__device__ __forceinline__ int gm_begin(int U, int w, int nw) { return (int)((long long)U * w / nw); }
+__device__ __forceinline__ int gm_owner(int U, int u, int nw) {
+  return (int)(((long long)(u + 1) * nw - 1) / U);
 }
 
 __global__ void gemm_tile_kernel(const uint16_t* __restrict__ W, uint16_t* __restrict__ Wt, int N,
@@ -79,6 +80,49 @@ __global__ void gemm_tile_kernel(const uint16_t* __restrict__ W, uint16_t* __res
   *reinterpret_cast<uint4*>(Wt + blk * 512 + L * 8) = v;
 }
 
+// Sum the live pieces of group g (all threads of the workgroup), apply the epilogue
+// and store bf16.
+__device__ void gemm_merge(const GemmArgs& a, int g, const int* live, int np) {
+  const size_t piece = (size_t)a.M * GM_COLS;
+  const int per_row = a.epi == GM_EPI_SWIGLU ? 8 : GM_COLS / 4;   // items per row
+  for (int it = threadIdx.x; it < a.M * per_row; it += 256) {
+    const int m = it / per_row, sub = it % per_row;
+    if (a.epi == GM_EPI_SWIGLU) {
+      // item = (tile, half): gate raw columns 16 tile + 4 half .. +4, up 8 further
+      const int tile = sub / 2, h = sub % 2, cg = 16 * tile + 4 * h;
+      float4 sg = make_float4(0.f, 0.f, 0.f, 0.f), su = sg;
+#pragma unroll 4
+      for (int k = 0; k < np; ++k) {
+        const float* pp = a.part + (size_t)live[k] * piece + (size_t)m * GM_COLS;
+        const float4 x = *reinterpret_cast<const float4*>(pp + cg);
+        const float4 y = *reinterpret_cast<const float4*>(pp + cg + 8);
+        sg.x += x.x; sg.y += x.y; sg.z += x.z; sg.w += x.w;
+        su.x += y.x; su.y += y.y; su.z += y.z; su.w += y.w;
+      }
+      const float gv[4] = {sg.x, sg.y, sg.z, sg.w}, uv[4] = {su.x, su.y, su.z, su.w};
+      float yv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) yv[j] = round_bf16(gm_silu_bf16(gv[j]) * round_bf16(uv[j]));
+      const int col = 8 * (4 * g + tile) + 4 * h;
+      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+          make_uint2((uint32_t)f32_to_bf16(yv[0]) | ((uint32_t)f32_to_bf16(yv[1]) << 16),
+                     (uint32_t)f32_to_bf16(yv[2]) | ((uint32_t)f32_to_bf16(yv[3]) << 16));
+    } else {
+      const int c4 = sub * 4;
+      float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+      for (int k = 0; k < np; ++k) {
+        const float4 x = *reinterpret_cast<const float4*>(a.part + (size_t)live[k] * piece +
+                                                          (size_t)m * GM_COLS + c4);
+        t.x += x.x; t.y += x.y; t.z += x.z; t.w += x.w;
+      }
+      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + GM_COLS * g + c4) =
+          make_uint2((uint32_t)f32_to_bf16(t.x) | ((uint32_t)f32_to_bf16(t.y) << 16),
+                     (uint32_t)f32_to_bf16(t.z) | ((uint32_t)f32_to_bf16(t.w) << 16));
+    }
+  }
+}
+
 template <int MT>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   typedef unsigned int v4u __attribute__((ext_vector_type(4)));
@@ -88,22 +132,22 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
   const int w = blockIdx.x;
-  const long long u0 = gm_begin(a.U, w, a.nw), u1 = gm_begin(a.U, w + 1, a.nw);
+  const int u0 = gm_begin(a.U, w, a.nw), u1 = gm_begin(a.U, w + 1, a.nw);
   if (u0 >= u1) return;
   const int kt = a.K / 32;
   const uint16_t* wlane = a.Wt + (size_t)wave * kt * 512 + lane * 8;
 
   v4u wr[GM_P][GM_KS], an[2][ACH];
   // weights of unit u for this wave: n-tile 4 g + wave, k-steps 4 st .. 4 st + 3
-  auto wload = [&](v4u* dst, long long u) {
-    const int g = (int)(u / a.SK), st = (int)(u % a.SK);
+  auto wload = [&](v4u* dst, int u) {
+    const int g = u / a.SK, st = u - g * a.SK;
     const uint16_t* p = wlane + ((size_t)4 * g * kt + (size_t)st * GM_KS) * 512;
 #pragma unroll
     for (int q = 0; q < GM_KS; ++q)
       dst[q] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p + q * 512));
   };
-  auto aload = [&](v4u* dst, long long u) {
-    const int k0 = (int)(u % a.SK) * GM_KC;
+  auto aload = [&](v4u* dst, int u) {
+    const int k0 = (u % a.SK) * GM_KC;
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
       const int c = i * 256 + tid, row = c / CPR, col = c % CPR;
@@ -117,42 +161,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   gm_f32x4 acc[MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i) acc[i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+  // Every load is issued unconditionally (units past the range re-read the last one),
+  // so the compiler can count the loads in flight exactly and each staging waits only
+  // for its own unit, never for the ring ahead of it.
+  const int ulast = u1 - 1;
 #pragma unroll
-  for (int p = 0; p < GM_P; ++p)
-    if (u0 + p < u1) wload(wr[p], u0 + p);
+  for (int p = 0; p < GM_P; ++p) wload(wr[p], u0 + p < u1 ? u0 + p : ulast);
   aload(an[0], u0);
-  if (u0 + 1 < u1) aload(an[1], u0 + 1);
+  aload(an[1], u0 + 1 < u1 ? u0 + 1 : ulast);
   bool whole_from_start = (u0 % a.SK) == 0;
-
-  // One unit: stage activations, 4 k-steps of MFMA, refill the rings; at a group's
-  // last unit (or the range's end) write the group's result or piece.
-#define GM_UNIT(J)                                                                            \
-  {                                                                                           \
-    const long long u = ub + (J);                                                             \
-    if (u < u1) {                                                                             \
-      constexpr int set = (J) & 1, slot = (J) % GM_P;                                         \
-      _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                       \
-        const int c = i * 256 + tid, row = c / CPR, col = c % CPR;                            \
-        if (row < MT * 16) *reinterpret_cast<v4u*>(&al[set][row * GM_PITCH + col * 16]) = an[set][i]; \
-      }                                                                                       \
-      gm_lds_barrier();                                                                       \
-      if (u + 2 < u1) aload(an[set], u + 2);                                                  \
-      _Pragma("unroll") for (int q = 0; q < GM_KS; ++q) {                                     \
-        _Pragma("unroll") for (int i = 0; i < MT; ++i) {                                      \
-          const gm_bf16x8 ab = *reinterpret_cast<const gm_bf16x8*>(                           \
-              &al[set][(16 * i + l16) * GM_PITCH + q * 64 + g4 * 16]);                        \
-          acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                                   \
-              __builtin_bit_cast(gm_bf16x8, wr[slot][q]), ab, acc[i], 0, 0, 0);               \
-        }                                                                                     \
-      }                                                                                       \
-      if (u + GM_P < u1) wload(wr[slot], u + GM_P);                                           \
-      const int st = (int)(u % a.SK);                                                         \
-      if (st == a.SK - 1 || u == u1 - 1) {                                                    \
-        finish((int)(u / a.SK), whole_from_start && st == a.SK - 1);                          \
-        whole_from_start = true;                                                              \
-      }                                                                                       \
-    }                                                                                         \
-  }
 
   // lane holds, for m-tile i, rows m = 16 i + l16 and tiled columns 4 g4 .. 4 g4 + 3 of
   // n-tile 4 g + wave
@@ -204,59 +221,64 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     for (int i = 0; i < MT; ++i) acc[i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
   };
 
+  // One unit: stage activations, 4 k-steps of MFMA, refill the rings; at a group's
+  // last unit (or the range's end) write the group's result or piece.
+#define GM_UNIT(J)                                                                            \
+  {                                                                                           \
+    const int u = ub + (J);                                                                   \
+    const bool livej = u < u1;                                                                \
+    constexpr int set = (J) & 1, slot = (J) % GM_P;                                           \
+    _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                         \
+      const int c = i * 256 + tid, row = c / CPR, col = c % CPR;                              \
+      if (row < MT * 16) *reinterpret_cast<v4u*>(&al[set][row * GM_PITCH + col * 16]) = an[set][i]; \
+    }                                                                                         \
+    gm_lds_barrier();                                                                         \
+    aload(an[set], u + 2 < u1 ? u + 2 : ulast);                                               \
+    if (livej) {                                                                              \
+      _Pragma("unroll") for (int q = 0; q < GM_KS; ++q) {                                     \
+        _Pragma("unroll") for (int i = 0; i < MT; ++i) {                                      \
+          const gm_bf16x8 ab = *reinterpret_cast<const gm_bf16x8*>(                           \
+              &al[set][(16 * i + l16) * GM_PITCH + q * 64 + g4 * 16]);                        \
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                                   \
+              __builtin_bit_cast(gm_bf16x8, wr[slot][q]), ab, acc[i], 0, 0, 0);               \
+        }                                                                                     \
+      }                                                                                       \
+    }                                                                                         \
+    wload(wr[slot], u + GM_P < u1 ? u + GM_P : ulast);                                        \
+    if (livej) {                                                                              \
+      const int st = u % a.SK;                                                                \
+      if (st == a.SK - 1 || u == ulast) {                                                     \
+        finish(u / a.SK, whole_from_start && st == a.SK - 1);                                 \
+        whole_from_start = true;                                                              \
+      }                                                                                       \
+    }                                                                                         \
+  }
+
   static_assert(GM_P == 4, "the unit loop is unrolled by 4");
-  for (long long ub = u0; ub < u1; ub += 4) {
+  for (int ub = u0; ub < u1; ub += 4) {
     GM_UNIT(0) GM_UNIT(1) GM_UNIT(2) GM_UNIT(3)
   }
 #undef GM_UNIT
 }
 
-// Merge the pieces of group blockIdx.x: sum the live pieces' fp32 columns, apply the
-// epilogue, store bf16.  Groups one workgroup finished are skipped.
+
+// Merge the pieces of group blockIdx.x: the live piece slots are listed in LDS once,
+// then every element's piece loads are independent and issued back to back; groups
+// one workgroup finished are skipped.
 __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
+  __shared__ int live[GM_MAXW];
+  __shared__ int nlive;
   const int g = blockIdx.x;
-  const long long first = (long long)g * a.SK, last = first + a.SK - 1;
-  const int wf = gm_owner(a.U, first, a.nw), wl = gm_owner(a.U, last, a.nw);
+  const int wf = gm_owner(a.U, g * a.SK, a.nw), wl = gm_owner(a.U, g * a.SK + a.SK - 1, a.nw);
   if (wf == wl) return;
-  const size_t piece = (size_t)a.M * GM_COLS;
-  if (a.epi == GM_EPI_SWIGLU) {
-    // item = (m, tile, half): gate raw columns 16 tile + 4 half .. +4, up 8 further
-    for (int it = threadIdx.x; it < a.M * 8; it += 256) {
-      const int m = it / 8, tile = (it % 8) / 2, h = it % 2;
-      const int cg = 16 * tile + 4 * h;
-      float4 sg = make_float4(0.f, 0.f, 0.f, 0.f), su = sg;
-      for (int w = wf; w <= wl; ++w) {
-        if (gm_begin(a.U, w, a.nw) >= gm_begin(a.U, w + 1, a.nw)) continue;
-        const float* pp = a.part + ((size_t)w + g) * piece + (size_t)m * GM_COLS;
-        const float4 x = *reinterpret_cast<const float4*>(pp + cg);
-        const float4 y = *reinterpret_cast<const float4*>(pp + cg + 8);
-        sg.x += x.x; sg.y += x.y; sg.z += x.z; sg.w += x.w;
-        su.x += y.x; su.y += y.y; su.z += y.z; su.w += y.w;
-      }
-      const float gv[4] = {sg.x, sg.y, sg.z, sg.w}, uv[4] = {su.x, su.y, su.z, su.w};
-      float yv[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) yv[j] = round_bf16(gm_silu_bf16(gv[j]) * round_bf16(uv[j]));
-      const int col = 8 * (4 * g + tile) + 4 * h;
-      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
-          make_uint2((uint32_t)f32_to_bf16(yv[0]) | ((uint32_t)f32_to_bf16(yv[1]) << 16),
-                     (uint32_t)f32_to_bf16(yv[2]) | ((uint32_t)f32_to_bf16(yv[3]) << 16));
-    }
-  } else {
-    for (int it = threadIdx.x; it < a.M * (GM_COLS / 4); it += 256) {
-      const int m = it / (GM_COLS / 4), c4 = (it % (GM_COLS / 4)) * 4;
-      float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int w = wf; w <= wl; ++w) {
-        if (gm_begin(a.U, w, a.nw) >= gm_begin(a.U, w + 1, a.nw)) continue;
-        const float4 x = *reinterpret_cast<const float4*>(a.part + ((size_t)w + g) * piece +
-                                                          (size_t)m * GM_COLS + c4);
-        s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
-      }
-      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + GM_COLS * g + c4) =
-          make_uint2((uint32_t)f32_to_bf16(s.x) | ((uint32_t)f32_to_bf16(s.y) << 16),
-                     (uint32_t)f32_to_bf16(s.z) | ((uint32_t)f32_to_bf16(s.w) << 16));
-    }
+  if (threadIdx.x == 0) {
+    int n = 0;
+    for (int x = wf; x <= wl; ++x)
+      if (gm_begin(a.U, x, a.nw) < gm_begin(a.U, x + 1, a.nw)) live[n++] = x + g;
+    nlive = n;
   }
+  __syncthreads();
+  gemm_merge(a, g, live, nlive);
 }
 
 }  // namespace lollm
@@ -288,11 +310,16 @@ LOLLM_API int lollm_gemm_tile_weights(const void* W, void* Wt, int N, int K, int
   return launch_status();
 }
 
+// Workspace: the fp32 pieces, slot w + group.
+static long long gemm_ws_bytes(int M, int N, int nw) {
+  return ((long long)nw + N / GM_COLS) * M * GM_COLS * (long long)sizeof(float);
+}
+
 LOLLM_API long long lollm_gemm_workspace_bytes(int M, int N, int K, int grid) {
   if (!gemm_shape_ok(M, N, K, GM_EPI_NONE)) return -1;
   const int nw = gemm_grid(grid);
   if (nw <= 0 || nw > GM_MAXW) return -1;
-  return ((long long)nw + N / GM_COLS) * M * GM_COLS * (long long)sizeof(float);
+  return gemm_ws_bytes(M, N, nw);
 }
 
 LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, long long ldc,
@@ -305,13 +332,14 @@ LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, 
   if (grid < 0 || grid > GM_MAXW) return LOLLM_EINVAL;
   const int nw = gemm_grid(grid);
   if (nw <= 0 || nw > GM_MAXW) return LOLLM_EUNSUPPORTED;
-  if (workspace_bytes < ((long long)nw + N / GM_COLS) * M * GM_COLS * (long long)sizeof(float))
-    return LOLLM_EINVAL;
+  if (workspace_bytes < gemm_ws_bytes(M, N, nw)) return LOLLM_EINVAL;
+  if ((long long)(N / GM_COLS) * (K / GM_KC) >= (1LL << 31)) return LOLLM_EUNSUPPORTED;
   GemmArgs a;
   a.A = (const uint16_t*)A; a.Wt = (const uint16_t*)Wt; a.C = (uint16_t*)C;
-  a.part = (float*)workspace; a.lda = lda; a.ldc = ldc;
+  a.part = (float*)workspace;
+  a.lda = lda; a.ldc = ldc;
   a.M = M; a.N = N; a.K = K; a.G = N / GM_COLS; a.SK = K / GM_KC; a.nw = nw; a.epi = epilogue;
-  a.U = (long long)a.G * a.SK;
+  a.U = a.G * a.SK;
   hipStream_t st = (hipStream_t)stream;
   const int mt = (M + 15) / 16;
   switch (mt) {

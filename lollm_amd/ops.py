@@ -209,8 +209,8 @@ def gemm_workspace_bytes(M, N, K, grid=0):
 
 
 def gemm_workspace(nbytes, device):
-    """The shared fp32 piece buffer of lollm_gemm (one per device, grown on demand;
-    reserve the largest size before capturing a graph)."""
+    """The shared piece buffer of lollm_gemm (one per device, grown on demand; reserve
+    the largest size before capturing a graph)."""
     key = torch.device(device)
     ws = _gemm_ws.get(key)
     if ws is None or ws.numel() < nbytes:

@@ -99,3 +99,4 @@ def test_projection_paths_agree():
     close(p._gemm(x[:64].cuda()), ref[:64])
     close(p._blas(x[:64].cuda()), ref[:64])
     close(p(x.cuda()), ref)
+
