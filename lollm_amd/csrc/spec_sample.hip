@@ -22,9 +22,10 @@
 // Kernels:
 //   row_stats    one 1024-thread workgroup per row, ONE pass over HBM: the row is
 //                held in registers (19 x 16 B per thread covers V <= 155648; larger
-//                rows re-read the tail), giving the max key / argmax, then a per-key
-//                count histogram over the NBINS keys below the max in LDS and block
-//                scans for the top-k / top-p cut points and the kept mass Z;
+//                rows re-read the tail), giving the max key (packed 16-bit order keys,
+//                two tokens per max), then a per-key count histogram over the NBINS
+//                keys below the max in LDS and block scans for the top-k / top-p cut
+//                points and the kept mass Z;
 //   argmax_*     greedy rows: the row split over 16 workgroups, partial maxima
 //                merged by a second tiny kernel (a greedy row needs no histogram);
 //   spec_accept  one workgroup per sequence: the k accept tests in parallel, then
@@ -33,8 +34,10 @@
 // A draw is an inverse CDF over token ids in two steps: every wave of the block
 // sums the weights of its own contiguous sixteenth of the row (coalesced, one pass,
 // exact integers), then the one wave whose segment holds the target walks it again
-// with wave-level scans.  Residual masses are 64-bit when q is one-hot (argmax
-// drafts) and 128-bit when q is a sampled distribution.
+// with wave-level scans.  A token's weight depends only on its key's distance below
+// the row maximum, so each draw first fills an LDS table of the NBINS weights (the
+// same weight_of) and then reads one entry per token.  Residual masses are 64-bit
+// when q is one-hot (argmax drafts) and 128-bit when q is a sampled distribution.
 #include "common.h"
 
 namespace lollm {
@@ -117,7 +120,37 @@ __device__ __forceinline__ uint64_t token_weight(const RowStat& s, float c, uint
   return weight_of(key_value(k), key_value(s.kmax), c);
 }
 
-__device__ __forceinline__ uint32_t bf16_at(const uint16_t* x, int i) { return x[i]; }
+// Weight table of a row's distribution: tab[d] = the weight of a token whose key is d
+// below the row's maximum key (zero past the cut) -- token_weight as a lookup.
+__device__ void build_table(const RowStat& s, float c, uint64_t* tab) {
+  const float xmax = key_value(s.kmax);
+  for (int d = threadIdx.x; d < SP_NBINS; d += blockDim.x)
+    tab[d] = (!s.greedy && d <= s.cut) ? weight_of(key_value(s.kmax - d), xmax, c) : 0;
+}
+
+__device__ __forceinline__ uint64_t table_weight(const RowStat& s, const uint64_t* tab,
+                                                 uint32_t b, int32_t tok) {
+  if (s.greedy) return tok == s.argmax ? 1u : 0u;
+  const uint32_t d = (uint32_t)(s.kmax - skey(b));   // >= 0: kmax is the row maximum
+  return d < (uint32_t)SP_NBINS ? tab[d] : 0;
+}
+
+// Order keys of the two bf16 in a word, packed (ord16 per half).
+__device__ __forceinline__ uint32_t ord_pair(uint32_t w) {
+  const uint32_t sgn = (w >> 15) & 0x00010001u;
+  return w ^ ((sgn * 0x7FFFu) | 0x80008000u);
+}
+
+typedef unsigned short sp_us2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(sp_us2, a),
+                                                                __builtin_bit_cast(sp_us2, b)));
+}
+
+// bf16 bits of an order key (inverse of ord16)
+__device__ __forceinline__ uint32_t ord_bits(uint32_t o) {
+  return (o & 0x8000u) ? (o ^ 0x8000u) : (~o & 0xFFFFu);
+}
 
 // ---------------------------------------------------------------- block primitives
 template <typename T>
@@ -243,6 +276,7 @@ __device__ __forceinline__ void hist_chunk(uint4 u, int32_t km, uint32_t* hist) 
   }
 }
 
+// Sampled rows only (inv_temp > 0); greedy rows take the split argmax below.
 __global__ __launch_bounds__(SP_THREADS) void row_stats_kernel(const uint16_t* __restrict__ logits,
                                                                int V, float inv_temp, int top_k,
                                                                float top_p, RowStat* stats) {
@@ -254,7 +288,6 @@ __global__ __launch_bounds__(SP_THREADS) void row_stats_kernel(const uint16_t* _
   const int row = blockIdx.x;
   const int nch = V >> 3;
   const uint4* x4 = reinterpret_cast<const uint4*>(logits + (size_t)row * V);
-  const bool greedy = !(inv_temp > 0.0f);
   // ---- the row into registers (one HBM pass); zero the histogram meanwhile ----
   uint4 reg[SP_REG];
 #pragma unroll
@@ -262,28 +295,28 @@ __global__ __launch_bounds__(SP_THREADS) void row_stats_kernel(const uint16_t* _
     const int c = i * SP_THREADS + tid;
     reg[i] = c < nch ? x4[c] : make_uint4(0, 0, 0, 0);
   }
-  if (!greedy)
-    for (int i = tid; i < SP_NBINS; i += SP_THREADS) hist[i] = 0;
-  uint64_t best = 0;
-  int32_t km = INT32_MIN;
+  for (int i = tid; i < SP_NBINS; i += SP_THREADS) hist[i] = 0;
+  // ---- the maximum order key, two bf16 at a time ----
+  uint32_t m2 = 0;
 #pragma unroll
   for (int i = 0; i < SP_REG; ++i) {
     const int c = i * SP_THREADS + tid;
-    if (c < nch) scan_chunk(reg[i], c, best, km);
+    if (c < nch) {
+      m2 = max_u16x2(m2, ord_pair(reg[i].x));
+      m2 = max_u16x2(m2, ord_pair(reg[i].y));
+      m2 = max_u16x2(m2, ord_pair(reg[i].z));
+      m2 = max_u16x2(m2, ord_pair(reg[i].w));
+    }
   }
-  for (int c = SP_REG * SP_THREADS + tid; c < nch; c += SP_THREADS) scan_chunk(x4[c], c, best, km);
-  best = block_max<uint64_t>(best, s64);
+  for (int c = SP_REG * SP_THREADS + tid; c < nch; c += SP_THREADS) {
+    const uint4 u = x4[c];
+    m2 = max_u16x2(max_u16x2(m2, ord_pair(u.x)), max_u16x2(ord_pair(u.y), max_u16x2(ord_pair(u.z), ord_pair(u.w))));
+  }
+  const uint32_t omax = (uint32_t)block_max<uint64_t>((uint64_t)max((m2 & 0xFFFFu), (m2 >> 16)), s64);
   RowStat st;
-  st.argmax = (int32_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu));
-  st.greedy = greedy;
-  if (greedy) {
-    st.kmax = 0;
-    st.cut = 0;
-    st.Z = 1;
-    if (tid == 0) stats[row] = st;
-    return;
-  }
-  km = (int32_t)block_max<int64_t>((int64_t)km, reinterpret_cast<int64_t*>(s64));
+  st.greedy = 0;
+  st.argmax = -1;   // only greedy rows use it
+  const int32_t km = skey(ord_bits(omax));   // skey is monotone in the order key
   st.kmax = km;
   // ---- per-key counts below the max (from registers) ----
 #pragma unroll
@@ -478,9 +511,10 @@ __device__ __forceinline__ u128 scaled_target(uint32_t U, u128 M) {
   return (u128)U * (M >> 24) + (((u128)U * (uint64_t)(M & 0xFFFFFFu)) >> 24);
 }
 
-// Plain draw from a row's own distribution p (u64 masses, target floor(U Z / 2^24)).
-__device__ int32_t draw_plain(const uint16_t* xp, const RowStat& sp, float c, uint32_t U, int V,
-                              uint64_t* wtot, int32_t* found) {
+// Plain draw from a row's own distribution p (u64 masses, target floor(U Z / 2^24));
+// tab is p's weight table (build_table), complete before the call.
+__device__ int32_t draw_plain(const uint16_t* xp, const RowStat& sp, const uint64_t* tab, uint32_t U,
+                              int V, uint64_t* wtot, int32_t* found) {
   if (sp.greedy) return sp.argmax;
   const int nch = V >> 3, seg = (nch + SP_THREADS / 64 - 1) / (SP_THREADS / 64);
   const uint4* x4 = reinterpret_cast<const uint4*>(xp);
@@ -489,7 +523,7 @@ __device__ int32_t draw_plain(const uint16_t* xp, const RowStat& sp, float c, ui
     const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      w[e] = token_weight(sp, c, (wd[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, ch * 8 + e);
+      w[e] = table_weight(sp, tab, (wd[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, ch * 8 + e);
   };
   draw_totals<uint64_t>(nch, seg, w8, wtot);
   const uint64_t tgt = (uint64_t)(((u128)U * sp.Z) >> 24);
@@ -506,6 +540,7 @@ __global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
   __shared__ uint64_t wt64[SP_THREADS / 64];
   __shared__ int32_t found;
   __shared__ int32_t ok[64];
+  __shared__ uint64_t tab_p[SP_NBINS], tab_q[SP_NBINS];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const uint64_t offset = offset_dev ? *offset_dev : offset_arg;
@@ -536,7 +571,9 @@ __global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
   int32_t tok;
   if (!rej) {
     const RowStat sp = st_t[b * (k + 1) + k];
-    tok = draw_plain(target + ((size_t)b * (k + 1) + k) * V, sp, c, U, V, wt64, &found);
+    build_table(sp, c, tab_p);
+    __syncthreads();
+    tok = draw_plain(target + ((size_t)b * (k + 1) + k) * V, sp, tab_p, U, V, wt64, &found);
   } else {
     const RowStat sp = st_t[b * (k + 1) + a];
     const uint16_t* xp = target + ((size_t)b * (k + 1) + a) * V;
@@ -544,41 +581,45 @@ __global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
     d = d < 0 ? 0 : (d >= V ? V - 1 : d);
     const int nch = V >> 3, seg = (nch + SP_THREADS / 64 - 1) / (SP_THREADS / 64);
     const uint4* xp4 = reinterpret_cast<const uint4*>(xp);
+    build_table(sp, c, tab_p);
     if (draft) {
       // q a sampled distribution: residual wp Zq - wq Zp in 128 bits
       const RowStat sq = st_d[b * k + a];
       const uint4* xq4 = reinterpret_cast<const uint4*>(draft + ((size_t)b * k + a) * V);
       const uint64_t Zq = sq.Z;
+      build_table(sq, c, tab_q);
+      __syncthreads();
       auto w8 = [&](int ch, u128* w) {
         const uint4 up = xp4[ch], uq = xq4[ch];
         const uint32_t pw[4] = {up.x, up.y, up.z, up.w}, qw[4] = {uq.x, uq.y, uq.z, uq.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int t = ch * 8 + e;
-          const uint64_t wpt = token_weight(sp, c, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
-          const uint64_t wqt = token_weight(sq, c, (qw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
+          const uint64_t wpt = table_weight(sp, tab_p, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
+          const uint64_t wqt = table_weight(sq, tab_q, (qw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
           const u128 l = (u128)wpt * Zq, r = (u128)wqt * sp.Z;
           w[e] = l > r ? l - r : (u128)0;
         }
       };
       const u128 R = draw_totals<u128>(nch, seg, w8, wt128);
-      tok = R == 0 ? draw_plain(xp, sp, c, U, V, wt64, &found)
+      tok = R == 0 ? draw_plain(xp, sp, tab_p, U, V, wt64, &found)
                    : draw_find<u128>(nch, seg, w8, wt128, scaled_target(U, R), V, &found);
     } else {
       // q one-hot at d: residual wp - [t == d] Zp fits 64 bits
+      __syncthreads();
       auto w8 = [&](int ch, uint64_t* w) {
         const uint4 up = xp4[ch];
         const uint32_t pw[4] = {up.x, up.y, up.z, up.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int t = ch * 8 + e;
-          const uint64_t wpt = token_weight(sp, c, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
+          const uint64_t wpt = table_weight(sp, tab_p, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
           const uint64_t r = t == d ? sp.Z : 0;
           w[e] = wpt > r ? wpt - r : 0;
         }
       };
       const uint64_t R = draw_totals<uint64_t>(nch, seg, w8, wt64);
-      tok = R == 0 ? draw_plain(xp, sp, c, U, V, wt64, &found)
+      tok = R == 0 ? draw_plain(xp, sp, tab_p, U, V, wt64, &found)
                    : draw_find<uint64_t>(nch, seg, w8, wt64,
                                          (uint64_t)scaled_target(U, (u128)R), V, &found);
     }
@@ -595,12 +636,15 @@ __global__ __launch_bounds__(SP_THREADS) void sample_rows_kernel(
     const RowStat* __restrict__ stats, int32_t* __restrict__ out) {
   __shared__ uint64_t wt64[SP_THREADS / 64];
   __shared__ int32_t found;
+  __shared__ uint64_t tab[SP_NBINS];
   const int r = blockIdx.x;
   const uint64_t offset = offset_dev ? *offset_dev : offset_arg;
   const RowStat sp = stats[r];
   const float c = inv_temp * 1.44269504088896341f;
   const uint32_t U = philox_u24(seed, offset, (uint32_t)(row_base + r), (uint32_t)slot);
-  const int32_t tok = draw_plain(logits + (size_t)r * V, sp, c, U, V, wt64, &found);
+  build_table(sp, c, tab);
+  __syncthreads();
+  const int32_t tok = draw_plain(logits + (size_t)r * V, sp, tab, U, V, wt64, &found);
   if (threadIdx.x == 0) out[r] = tok;
 }
 
