@@ -22,10 +22,12 @@
 // uneven rounds).  The activation tile of each stage (M x 128) is staged in LDS and
 // shared by the 4 waves; weight loads run 4 units ahead in a register ring, activation
 // loads 2 units ahead.  A group one workgroup covers whole is stored directly (with
-// the epilogue); a group cut between workgroups leaves fp32 pieces in slot w + group,
-// merged by gemm_fixup_kernel.  (Merging in the last-arriving workgroup instead would
-// need device-scope release / acquire fences, which write back and invalidate the
-// XCD's L2 -- measured 3-10x slower here than the second launch.)
+// the epilogue); a group cut between workgroups leaves an fp32 piece in slot w + group,
+// stored in accumulator order (each wave's store is one contiguous 1 KB), merged by
+// gemm_fixup_kernel with one float4 per thread over a (group, m-tile) grid.  (Merging
+// in the last-arriving workgroup instead would need device-scope release / acquire
+// fences, which write back and invalidate the XCD's L2 -- measured 3-10x slower here
+// than the second launch.)
 #include "common.h"
 
 namespace lollm {
@@ -46,7 +48,7 @@ struct GemmArgs {
   const uint16_t* A;     // (M, K) activations, row stride lda
   const uint16_t* Wt;    // tiled weights
   uint16_t* C;           // (M, ldc)
-  float* part;           // (nw + G) x M x 64 fp32 pieces
+  float* part;           // (nw + G) pieces of MT x 4 x 64 float4 (accumulator order)
   long long lda, ldc;
   int M, N, K, G, SK, nw, epi, U;
 };
@@ -78,49 +80,6 @@ __global__ void gemm_tile_kernel(const uint16_t* __restrict__ W, uint16_t* __res
   if (mode == GM_EPI_SWIGLU) src = (r < 8 ? 0 : N / 2) + 8 * t + (r & 7);
   const uint4 v = *reinterpret_cast<const uint4*>(W + (size_t)src * K + 32 * s + 8 * g);
   *reinterpret_cast<uint4*>(Wt + blk * 512 + L * 8) = v;
-}
-
-// Sum the live pieces of group g (all threads of the workgroup), apply the epilogue
-// and store bf16.
-__device__ void gemm_merge(const GemmArgs& a, int g, const int* live, int np) {
-  const size_t piece = (size_t)a.M * GM_COLS;
-  const int per_row = a.epi == GM_EPI_SWIGLU ? 8 : GM_COLS / 4;   // items per row
-  for (int it = threadIdx.x; it < a.M * per_row; it += 256) {
-    const int m = it / per_row, sub = it % per_row;
-    if (a.epi == GM_EPI_SWIGLU) {
-      // item = (tile, half): gate raw columns 16 tile + 4 half .. +4, up 8 further
-      const int tile = sub / 2, h = sub % 2, cg = 16 * tile + 4 * h;
-      float4 sg = make_float4(0.f, 0.f, 0.f, 0.f), su = sg;
-#pragma unroll 4
-      for (int k = 0; k < np; ++k) {
-        const float* pp = a.part + (size_t)live[k] * piece + (size_t)m * GM_COLS;
-        const float4 x = *reinterpret_cast<const float4*>(pp + cg);
-        const float4 y = *reinterpret_cast<const float4*>(pp + cg + 8);
-        sg.x += x.x; sg.y += x.y; sg.z += x.z; sg.w += x.w;
-        su.x += y.x; su.y += y.y; su.z += y.z; su.w += y.w;
-      }
-      const float gv[4] = {sg.x, sg.y, sg.z, sg.w}, uv[4] = {su.x, su.y, su.z, su.w};
-      float yv[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) yv[j] = round_bf16(gm_silu_bf16(gv[j]) * round_bf16(uv[j]));
-      const int col = 8 * (4 * g + tile) + 4 * h;
-      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
-          make_uint2((uint32_t)f32_to_bf16(yv[0]) | ((uint32_t)f32_to_bf16(yv[1]) << 16),
-                     (uint32_t)f32_to_bf16(yv[2]) | ((uint32_t)f32_to_bf16(yv[3]) << 16));
-    } else {
-      const int c4 = sub * 4;
-      float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-      for (int k = 0; k < np; ++k) {
-        const float4 x = *reinterpret_cast<const float4*>(a.part + (size_t)live[k] * piece +
-                                                          (size_t)m * GM_COLS + c4);
-        t.x += x.x; t.y += x.y; t.z += x.z; t.w += x.w;
-      }
-      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + GM_COLS * g + c4) =
-          make_uint2((uint32_t)f32_to_bf16(t.x) | ((uint32_t)f32_to_bf16(t.y) << 16),
-                     (uint32_t)f32_to_bf16(t.z) | ((uint32_t)f32_to_bf16(t.w) << 16));
-    }
-  }
 }
 
 template <int MT>
@@ -206,16 +165,13 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         }
       }
     } else {
-      // a piece: raw fp32 sums of the group's 64 tiled columns, slot w + g (pieces are
-      // ordered in both w and g, so the slot is unique)
-      float* pp = a.part + ((size_t)w + g) * ((size_t)a.M * GM_COLS);
+      // a piece: the raw fp32 accumulators of the group, slot w + g (pieces are ordered
+      // in both w and g, so the slot is unique), float4 (i, wave, lane)
+      float* pp = a.part + ((size_t)w + g) * ((size_t)MT * 16 * GM_COLS);
 #pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const int m = 16 * i + l16;
-        if (m < a.M)
-          *reinterpret_cast<float4*>(pp + (size_t)m * GM_COLS + 16 * wave + 4 * g4) =
-              make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
-      }
+      for (int i = 0; i < MT; ++i)
+        *reinterpret_cast<float4*>(pp + (((size_t)i * 4 + wave) * 64 + lane) * 4) =
+            make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
     }
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -262,23 +218,62 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 }
 
 
-// Merge the pieces of group blockIdx.x: the live piece slots are listed in LDS once,
-// then every element's piece loads are independent and issued back to back; groups
-// one workgroup finished are skipped.
+// Merge the pieces of m-tile blockIdx.y of group blockIdx.x: the live piece slots are
+// listed in LDS by one wave (ballots over the workgroups whose ranges touch the group;
+// empty ranges leave no piece), then each thread sums one float4 of the accumulator
+// layout over the pieces in slot order and applies the epilogue.  Groups one workgroup
+// finished are skipped.
 __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
   __shared__ int live[GM_MAXW];
   __shared__ int nlive;
-  const int g = blockIdx.x;
+  const int g = blockIdx.x, i = blockIdx.y;
   const int wf = gm_owner(a.U, g * a.SK, a.nw), wl = gm_owner(a.U, g * a.SK + a.SK - 1, a.nw);
   if (wf == wl) return;
-  if (threadIdx.x == 0) {
-    int n = 0;
-    for (int x = wf; x <= wl; ++x)
-      if (gm_begin(a.U, x, a.nw) < gm_begin(a.U, x + 1, a.nw)) live[n++] = x + g;
-    nlive = n;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (wave == 0) {
+    int cnt = 0;
+    for (int base = wf; base <= wl; base += 64) {
+      const int x = base + lane;
+      const bool ok = x <= wl && gm_begin(a.U, x, a.nw) < gm_begin(a.U, x + 1, a.nw);
+      const unsigned long long m = __ballot(ok);
+      if (ok) live[cnt + __popcll(m & ((1ull << lane) - 1))] = x + g;
+      cnt += __popcll(m);
+    }
+    if (lane == 0) nlive = cnt;
   }
   __syncthreads();
-  gemm_merge(a, g, live, nlive);
+  const int np = nlive;
+  const int mt = (a.M + 15) / 16;
+  const size_t piece = (size_t)mt * 16 * GM_COLS;
+  const size_t off = (((size_t)i * 4 + wave) * 64 + lane) * 4;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+  for (int k = 0; k < np; ++k) {
+    const float4 x = *reinterpret_cast<const float4*>(a.part + (size_t)live[k] * piece + off);
+    s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
+  }
+  // lane holds rows 16 i + (lane & 15), tiled columns 4 (lane >> 4) .. + 3 of n-tile 4 g + wave
+  const int m = 16 * i + (lane & 15), g4 = lane >> 4;
+  if (a.epi == GM_EPI_SWIGLU) {
+    // partner lane (g4 ^ 2) holds the up half of the same output columns
+    const float o[4] = {__shfl_xor(s.x, 32, 64), __shfl_xor(s.y, 32, 64), __shfl_xor(s.z, 32, 64),
+                        __shfl_xor(s.w, 32, 64)};
+    const float gv[4] = {s.x, s.y, s.z, s.w};
+    if (g4 < 2 && m < a.M) {
+      float y[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[j] = round_bf16(gm_silu_bf16(gv[j]) * round_bf16(o[j]));
+      const int col = 8 * (4 * g + wave) + 4 * g4;
+      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+          make_uint2((uint32_t)f32_to_bf16(y[0]) | ((uint32_t)f32_to_bf16(y[1]) << 16),
+                     (uint32_t)f32_to_bf16(y[2]) | ((uint32_t)f32_to_bf16(y[3]) << 16));
+    }
+  } else if (m < a.M) {
+    const int col = GM_COLS * g + 16 * wave + 4 * g4;
+    *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+        make_uint2((uint32_t)f32_to_bf16(s.x) | ((uint32_t)f32_to_bf16(s.y) << 16),
+                   (uint32_t)f32_to_bf16(s.z) | ((uint32_t)f32_to_bf16(s.w) << 16));
+  }
 }
 
 }  // namespace lollm
@@ -310,9 +305,9 @@ LOLLM_API int lollm_gemm_tile_weights(const void* W, void* Wt, int N, int K, int
   return launch_status();
 }
 
-// Workspace: the fp32 pieces, slot w + group.
+// Workspace: the fp32 pieces, slot w + group, each (M rounded up to 16) x 64.
 static long long gemm_ws_bytes(int M, int N, int nw) {
-  return ((long long)nw + N / GM_COLS) * M * GM_COLS * (long long)sizeof(float);
+  return ((long long)nw + N / GM_COLS) * ((M + 15) / 16 * 16) * GM_COLS * (long long)sizeof(float);
 }
 
 LOLLM_API long long lollm_gemm_workspace_bytes(int M, int N, int K, int grid) {
@@ -350,6 +345,6 @@ LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, 
   }
   int rc = launch_status();
   if (rc) return rc;
-  hipLaunchKernelGGL(gemm_fixup_kernel, dim3(a.G), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(gemm_fixup_kernel, dim3(a.G, mt), dim3(256), 0, st, a);
   return launch_status();
 }

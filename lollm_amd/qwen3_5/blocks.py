@@ -22,15 +22,28 @@ def _cat_rows(*ws):
     return torch.cat([w.reshape(w.shape[0], -1) for w in ws], 0).contiguous()
 
 
+_FLUSH = {}
+
+
+def _flush_caches(device):
+    """Read a 512 MiB buffer: evicts earlier data from L2 and the 256 MiB last-level
+    cache, so the next kernel's weight reads go to HBM."""
+    buf = _FLUSH.get(device)
+    if buf is None:
+        buf = _FLUSH[device] = torch.ones(1 << 27, dtype=torch.float32, device=device)
+    buf.sum()
+
+
 class Projection:
     """y = x W^T (blocks.py's nn.Linear layers, no bias).  Keeps the row-major weight
     for hipBLASLt (F.linear) and a tiled copy for lollm_gemm (<= 64 rows).
     epilogue=GEMM_SWIGLU: W = [gate; up], y = silu(x gate^T) * x up^T (blocks.py:341-342).
 
     For a row count lollm_gemm supports, the first eager call times both paths (three
-    runs each, HIP events) and keeps the faster one for that row count; later calls --
-    and HIP-graph captures -- reuse the choice.  A call under capture with no choice
-    recorded yet takes lollm_gemm."""
+    runs each, HIP events, each run after the caches were flushed so the weight streams
+    from HBM as it does in a step that walks every layer) and keeps the faster one for
+    that row count; later calls -- and HIP-graph captures -- reuse the choice.  A call
+    under capture with no choice recorded yet takes lollm_gemm."""
 
     def __init__(self, weight, epilogue=ops.GEMM_NONE):
         self.weight = weight.to(torch.bfloat16).contiguous()
@@ -57,13 +70,16 @@ class Projection:
         times = {}
         for name, fn in (("gemm", self._gemm), ("blas", self._blas)):
             fn(x)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
+            total = 0.0
             for _ in range(3):
+                _flush_caches(x.device)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
                 fn(x)
-            e1.record()
-            e1.synchronize()
-            times[name] = e0.elapsed_time(e1)
+                e1.record()
+                e1.synchronize()
+                total += e0.elapsed_time(e1)
+            times[name] = total
         choice = min(times, key=times.get)
         self.choice[rows] = choice
         return choice
