@@ -112,6 +112,18 @@ def run_e2e(model, mtp, cfg, B, prompt_len, k, steps, warmup, temperature, top_p
                  "final_context_mean": ctx}
 
 
+def projection_paths():
+    """The path each projection shape took ("gemm" = lollm_gemm, "blas" = hipBLASLt),
+    keyed "NxK rows" (+ " +norm" for the residual add / RMSNorm fused form)."""
+    from lollm_amd.qwen3_5 import blocks
+    out = {}
+    for (N, K, epi, key), choice in sorted(blocks._SHAPE_CHOICE.items(), key=str):
+        rows = key[1] if isinstance(key, tuple) else key
+        tag = f"{N}x{K}{' swiglu' if epi else ''} M={rows}{' +norm' if isinstance(key, tuple) else ''}"
+        out[tag] = choice
+    return out
+
+
 def verify_breakdown(dec, iters=20):
     """Eager timing of the step's parts (µs): draft chain, verify forward, acceptance."""
     import torch
@@ -424,6 +436,7 @@ def main():
             {k_: round(v, 1) for k_, v in parts.items()},
         "roofline": {k_: roof[k_] for k_ in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
         "roofline_kernel": roof["kernel"],
+        "projection_paths": projection_paths(),
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

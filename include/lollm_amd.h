@@ -185,6 +185,22 @@ int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, long long 
                int N, int K, int epilogue, void* workspace, long long workspace_bytes, int grid,
                void* stream);
 
+/* A projection that feeds the residual stream, with the residual add and the next
+ * RMSNorm fused into the GEMM's second kernel: C = A W^T (as lollm_gemm, epilogue 0),
+ * x_out = bf16(C + residual), y = RMSNorm_{1+w}(x_out) (lollm_rmsnorm's arithmetic).
+ *
+ * Replaces: o_proj (src/qwen3_5/blocks.py:236), out_proj (blocks.py:326) and down_proj
+ * (blocks.py:342) followed by the residual adds and norms of the decoder layer
+ * (modeling_qwen3_5.py:59-60) -- `x = x + h; y = post_attention_layernorm(x)` and
+ * `x = x + mlp(...)` feeding the next layer's input_layernorm or the final norm.
+ *
+ * C (M, N) bf16 scratch; residual, x_out, y (M, N) bf16 contiguous (x_out may alias
+ * residual); norm_w (N) bf16; workspace as lollm_gemm.  Supported: N <= 8192 and at
+ * least as many (64-column, 128-k) units as workgroups, else LOLLM_EUNSUPPORTED. */
+int lollm_gemm_rmsnorm(const void* A, long long lda, const void* Wt, int M, int N, int K,
+                       const void* residual, const void* norm_w, float eps, void* C, void* x_out,
+                       void* y, void* workspace, long long workspace_bytes, int grid, void* stream);
+
 /* The Gated DeltaNet mixer from the in_proj outputs to the gated-norm output
  * (GatedDeltaNet.forward, blocks.py:288-329, between in_proj and out_proj):
  * causal conv + SiLU, beta / g gating, L2-normalised delta-rule scan, gated RMSNorm.

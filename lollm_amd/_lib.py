@@ -49,6 +49,8 @@ SIGNATURES = {
     "lollm_gemm_workspace_bytes": ([_I, _I, _I, _I], ctypes.c_longlong),
     "lollm_gemm": ([_P, ctypes.c_longlong, _P, _P, ctypes.c_longlong, _I, _I, _I, _I, _P,
                     ctypes.c_longlong, _I, _P], _I),
+    "lollm_gemm_rmsnorm": ([_P, ctypes.c_longlong, _P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P,
+                            ctypes.c_longlong, _I, _P], _I),
     "lollm_spec_commit": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P,
                            _P, _P], _I),
 }

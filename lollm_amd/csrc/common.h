@@ -49,6 +49,36 @@ __device__ __forceinline__ void store_nt(void* p, uint4 v) {
   __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(p));
 }
 
+// Sum over a workgroup of THREADS threads (wave64); red holds THREADS / 64 floats.
+template <int THREADS>
+__device__ __forceinline__ float block_sum_f(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < THREADS / 64; ++w) t += red[w];
+  return t;
+}
+
+// RMSNorm arithmetic shared by every kernel that normalises a hidden row, so fused and
+// stand-alone paths give the same bits: a RMS_THREADS-thread workgroup per row, thread t
+// owns the 8-value chunks t and t + RMS_THREADS (rows of up to 8192), accumulates the
+// squares in chunk order, then rstd = rsqrt(block sum / H + eps) and
+// y = bf16(v * rstd * (1 + w)).
+constexpr int RMS_THREADS = 512;
+constexpr int RMS_CHUNKS = 2;
+__device__ __forceinline__ float rms_rstd(float ss, float* red, int H, float eps) {
+  return rsqrtf(block_sum_f<RMS_THREADS>(ss, red) / (float)H + eps);
+}
+__device__ __forceinline__ uint32_t rms_out2(float v0, float v1, float r, uint32_t w2) {
+  const float w0 = __uint_as_float(w2 << 16), w1 = __uint_as_float(w2 & 0xffff0000u);
+  return f32_to_bf16(v0 * r * (1.f + w0)) | ((uint32_t)f32_to_bf16(v1 * r * (1.f + w1)) << 16);
+}
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LOLLM_OK : LOLLM_EHIP_BASE + (int)e;

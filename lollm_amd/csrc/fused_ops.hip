@@ -14,37 +14,24 @@
 
 namespace lollm {
 
-template <int THREADS>
-__device__ __forceinline__ float block_sum_f(float v, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float t = 0.f;
-#pragma unroll
-  for (int w = 0; w < THREADS / 64; ++w) t += red[w];
-  return t;
-}
-
-// One 256-thread workgroup per row; H % 8 == 0, vector loads of 8 bf16.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
-                                                      const uint16_t* __restrict__ h,
-                                                      uint16_t* __restrict__ x_out,
-                                                      const uint16_t* __restrict__ w,
-                                                      uint16_t* __restrict__ y, int H, float eps) {
-  __shared__ float red[4];
+// One RMS_THREADS-thread workgroup per row; H % 8 == 0, vector loads of 8 bf16.
+__global__ __launch_bounds__(RMS_THREADS) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                              const uint16_t* __restrict__ h,
+                                                              uint16_t* __restrict__ x_out,
+                                                              const uint16_t* __restrict__ w,
+                                                              uint16_t* __restrict__ y, int H,
+                                                              float eps) {
+  __shared__ float red[RMS_THREADS / 64];
   const size_t row = blockIdx.x;
   const uint4* x4 = reinterpret_cast<const uint4*>(x + row * H);
   const uint4* h4 = h ? reinterpret_cast<const uint4*>(h + row * H) : nullptr;
   const int n8 = H / 8;
-  constexpr int MAXV = 4;  // H <= 8192
+  constexpr int MAXV = RMS_CHUNKS;  // H <= 8192
   float v[MAXV][8];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
-    const int c = threadIdx.x + i * 256;
+    const int c = threadIdx.x + i * RMS_THREADS;
     if (c < n8) {
       uint4 u = x4[c];
       uint32_t wd[4] = {u.x, u.y, u.z, u.w};
@@ -67,20 +54,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
       }
     }
   }
-  const float r = rsqrtf(block_sum_f<256>(ss, red) / (float)H + eps);
+  const float r = rms_rstd(ss, red, H, eps);
   const uint4* w4 = reinterpret_cast<const uint4*>(w);
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
-    const int c = threadIdx.x + i * 256;
+    const int c = threadIdx.x + i * RMS_THREADS;
     if (c < n8) {
       uint4 wu = w4[c];
       uint32_t wd[4] = {wu.x, wu.y, wu.z, wu.w};
       uint32_t od[4];
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float w0 = __uint_as_float(wd[e >> 1] << 16), w1 = __uint_as_float(wd[e >> 1] & 0xffff0000u);
-        od[e >> 1] = f32_to_bf16(v[i][e] * r * (1.f + w0)) | ((uint32_t)f32_to_bf16(v[i][e + 1] * r * (1.f + w1)) << 16);
-      }
+      for (int e = 0; e < 8; e += 2) od[e >> 1] = rms_out2(v[i][e], v[i][e + 1], r, wd[e >> 1]);
       reinterpret_cast<uint4*>(y + row * H)[c] = make_uint4(od[0], od[1], od[2], od[3]);
     }
   }
@@ -194,7 +178,7 @@ LOLLM_API int lollm_rmsnorm(const void* x, const void* residual, void* x_out, co
                             void* y, int rows, int H, float eps, void* stream) {
   if (!x || !w || !y || rows <= 0 || H <= 0) return LOLLM_EINVAL;
   if (H % 8 || H > 8192) return LOLLM_EUNSUPPORTED;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(RMS_THREADS), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)residual, (uint16_t*)x_out,
                      (const uint16_t*)w, (uint16_t*)y, H, eps);
   return launch_status();

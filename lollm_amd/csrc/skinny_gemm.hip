@@ -22,9 +22,9 @@
 // uneven rounds).  The activation tile of each stage (M x 128) is staged in LDS and
 // shared by the 4 waves; weight loads run 4 units ahead in a register ring, activation
 // loads 2 units ahead.  A group one workgroup covers whole is stored directly (with
-// the epilogue); a group cut between workgroups leaves an fp32 piece in slot w + group,
-// stored in accumulator order (each wave's store is one contiguous 1 KB), merged by
-// gemm_fixup_kernel with one float4 per thread over a (group, m-tile) grid.  (Merging
+// the epilogue); a group cut between workgroups leaves an fp32 piece (rows x 64, row
+// major) in slot w + group, merged by gemm_fixup_kernel with one float4 per thread
+// over a (group, m-tile) grid, or by gemm_norm_kernel row by row.  (Merging
 // in the last-arriving workgroup instead would need device-scope release / acquire
 // fences, which write back and invalidate the XCD's L2 -- measured 3-10x slower here
 // than the second launch.)
@@ -41,6 +41,7 @@ constexpr int GM_COLS = 64;                 // output columns (tiled rows) per g
 constexpr int GM_PITCH = GM_KC * 2 + 16;    // padded bytes per activation row in LDS
 constexpr int GM_P = 4;                     // weight units in flight per wave
 constexpr int GM_MAXW = 1024;               // grid limit (piece table)
+constexpr int GM_PB = 8;                    // piece loads a merge issues together
 
 enum { GM_EPI_NONE = 0, GM_EPI_SWIGLU = 1 };
 
@@ -48,7 +49,7 @@ struct GemmArgs {
   const uint16_t* A;     // (M, K) activations, row stride lda
   const uint16_t* Wt;    // tiled weights
   uint16_t* C;           // (M, ldc)
-  float* part;           // (nw + G) pieces of MT x 4 x 64 float4 (accumulator order)
+  float* part;           // (nw + G) pieces of (16 MT) x 64 fp32, row major
   long long lda, ldc;
   int M, N, K, G, SK, nw, epi, U;
 };
@@ -165,12 +166,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         }
       }
     } else {
-      // a piece: the raw fp32 accumulators of the group, slot w + g (pieces are ordered
-      // in both w and g, so the slot is unique), float4 (i, wave, lane)
+      // a piece: the raw fp32 sums of the group's 64 tiled columns, slot w + g (pieces
+      // are ordered in both w and g, so the slot is unique); padding rows included
       float* pp = a.part + ((size_t)w + g) * ((size_t)MT * 16 * GM_COLS);
 #pragma unroll
       for (int i = 0; i < MT; ++i)
-        *reinterpret_cast<float4*>(pp + (((size_t)i * 4 + wave) * 64 + lane) * 4) =
+        *reinterpret_cast<float4*>(pp + (size_t)(16 * i + l16) * GM_COLS + 16 * wave + 4 * g4) =
             make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
     }
 #pragma unroll
@@ -220,9 +221,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 
 // Merge the pieces of m-tile blockIdx.y of group blockIdx.x: the live piece slots are
 // listed in LDS by one wave (ballots over the workgroups whose ranges touch the group;
-// empty ranges leave no piece), then each thread sums one float4 of the accumulator
-// layout over the pieces in slot order and applies the epilogue.  Groups one workgroup
-// finished are skipped.
+// empty ranges leave no piece), then each thread sums one float4 (the one its lane
+// held in the main kernel) over the pieces in slot order and applies the epilogue.
+// Groups one workgroup finished are skipped.
 __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
   __shared__ int live[GM_MAXW];
   __shared__ int nlive;
@@ -245,15 +246,20 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
   const int np = nlive;
   const int mt = (a.M + 15) / 16;
   const size_t piece = (size_t)mt * 16 * GM_COLS;
-  const size_t off = (((size_t)i * 4 + wave) * 64 + lane) * 4;
-  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-  for (int k = 0; k < np; ++k) {
-    const float4 x = *reinterpret_cast<const float4*>(a.part + (size_t)live[k] * piece + off);
-    s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
-  }
-  // lane holds rows 16 i + (lane & 15), tiled columns 4 (lane >> 4) .. + 3 of n-tile 4 g + wave
   const int m = 16 * i + (lane & 15), g4 = lane >> 4;
+  const size_t off = (size_t)m * GM_COLS + 16 * wave + 4 * g4;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int k0 = 0; k0 < np; k0 += GM_PB) {
+    // GM_PB pieces' loads in flight together (indices past np re-read the last, unused)
+    float4 p[GM_PB];
+#pragma unroll
+    for (int j = 0; j < GM_PB; ++j)
+      p[j] = *reinterpret_cast<const float4*>(a.part + (size_t)live[min(k0 + j, np - 1)] * piece + off);
+#pragma unroll
+    for (int j = 0; j < GM_PB; ++j)
+      if (k0 + j < np) { s.x += p[j].x; s.y += p[j].y; s.z += p[j].z; s.w += p[j].w; }
+  }
+  // lane holds row m, tiled columns 4 g4 .. + 3 of n-tile 4 g + wave
   if (a.epi == GM_EPI_SWIGLU) {
     // partner lane (g4 ^ 2) holds the up half of the same output columns
     const float o[4] = {__shfl_xor(s.x, 32, 64), __shfl_xor(s.y, 32, 64), __shfl_xor(s.z, 32, 64),
@@ -273,6 +279,105 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
     *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
         make_uint2((uint32_t)f32_to_bf16(s.x) | ((uint32_t)f32_to_bf16(s.y) << 16),
                    (uint32_t)f32_to_bf16(s.z) | ((uint32_t)f32_to_bf16(s.w) << 16));
+  }
+}
+
+// The GEMM output completed, the residual added and the row normalised, for a
+// projection that feeds the decoder's residual stream (o_proj / out_proj / down, then
+// modeling_qwen3_5.py:59-60): x_out = bf16(C + residual), y = RMSNorm_{1+w}(x_out).
+// One workgroup per row; thread t owns the 8-column chunks of lollm_rmsnorm's
+// chunking, and first forms each C value the way gemm_fixup_kernel does (groups
+// one workgroup finished come from C, the others are the fp32 sum of their pieces in
+// slot order, rounded to bf16), so the result has the same bits as lollm_gemm
+// followed by lollm_rmsnorm.  Every workgroup range is non-empty (U >= nw, checked on
+// the host), so the owners of a group are exactly wf .. wl.
+constexpr int GM_NORM_MAXG = 128;   // N <= 8192
+
+__global__ __launch_bounds__(RMS_THREADS) void gemm_norm_kernel(GemmArgs a,
+                                                                const uint16_t* __restrict__ res,
+                                                                const uint16_t* __restrict__ w,
+                                                                uint16_t* __restrict__ x_out,
+                                                                uint16_t* __restrict__ y,
+                                                                float eps) {
+  __shared__ int own[2 * GM_NORM_MAXG];
+  __shared__ float red[RMS_THREADS / 64];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  for (int g = tid; g < a.G; g += RMS_THREADS) {
+    own[2 * g] = gm_owner(a.U, g * a.SK, a.nw);
+    own[2 * g + 1] = gm_owner(a.U, g * a.SK + a.SK - 1, a.nw);
+  }
+  __syncthreads();
+  const int n8 = a.N / 8;
+  const size_t piece = (size_t)((a.M + 15) / 16) * 16 * GM_COLS;
+  const size_t row = (size_t)m * a.N;
+  constexpr int MAXV = RMS_CHUNKS;
+  float v[MAXV][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int ci = 0; ci < MAXV; ++ci) {
+    const int c = tid + RMS_THREADS * ci;
+    if (c < n8) {
+      const int g = c / 8;
+      const int wf = own[2 * g], wl = own[2 * g + 1];
+      float cv[8];
+      if (wf == wl) {
+        const uint4 u = *reinterpret_cast<const uint4*>(a.C + (size_t)m * a.ldc + 8 * c);
+        const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cv[e] = __uint_as_float(e & 1 ? wd[e >> 1] & 0xffff0000u : wd[e >> 1] << 16);
+      } else {
+        // columns 8c .. 8c + 7 = columns 8 (c % 8) .. + 7 of the group's piece row m
+        const size_t off0 = (size_t)m * GM_COLS + 8 * (c % 8);
+        float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0;
+        for (int x0 = wf; x0 <= wl; x0 += GM_PB) {
+          // GM_PB pieces' loads in flight together (indices past wl re-read wl, unused)
+          float4 p0[GM_PB], p1[GM_PB];
+#pragma unroll
+          for (int j = 0; j < GM_PB; ++j) {
+            const float* pp = a.part + (size_t)(min(x0 + j, wl) + g) * piece + off0;
+            p0[j] = *reinterpret_cast<const float4*>(pp);
+            p1[j] = *reinterpret_cast<const float4*>(pp + 4);
+          }
+#pragma unroll
+          for (int j = 0; j < GM_PB; ++j) {
+            if (x0 + j <= wl) {
+              s0.x += p0[j].x; s0.y += p0[j].y; s0.z += p0[j].z; s0.w += p0[j].w;
+              s1.x += p1[j].x; s1.y += p1[j].y; s1.z += p1[j].z; s1.w += p1[j].w;
+            }
+          }
+        }
+        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cv[e] = round_bf16(sv[e]);
+      }
+      const uint4 h = *reinterpret_cast<const uint4*>(res + row + 8 * c);
+      const uint32_t hd[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = round_bf16(cv[e] + __uint_as_float(e & 1 ? hd[e >> 1] & 0xffff0000u : hd[e >> 1] << 16));
+        v[ci][e] = f;
+        ss += f * f;
+      }
+      uint4 o;
+      o.x = f32_to_bf16(v[ci][0]) | ((uint32_t)f32_to_bf16(v[ci][1]) << 16);
+      o.y = f32_to_bf16(v[ci][2]) | ((uint32_t)f32_to_bf16(v[ci][3]) << 16);
+      o.z = f32_to_bf16(v[ci][4]) | ((uint32_t)f32_to_bf16(v[ci][5]) << 16);
+      o.w = f32_to_bf16(v[ci][6]) | ((uint32_t)f32_to_bf16(v[ci][7]) << 16);
+      *reinterpret_cast<uint4*>(x_out + row + 8 * c) = o;
+    }
+  }
+  const float r = rms_rstd(ss, red, a.N, eps);
+#pragma unroll
+  for (int ci = 0; ci < MAXV; ++ci) {
+    const int c = tid + RMS_THREADS * ci;
+    if (c < n8) {
+      const uint4 wu = *reinterpret_cast<const uint4*>(w + 8 * c);
+      const uint32_t wd[4] = {wu.x, wu.y, wu.z, wu.w};
+      uint32_t od[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) od[e >> 1] = rms_out2(v[ci][e], v[ci][e + 1], r, wd[e >> 1]);
+      *reinterpret_cast<uint4*>(y + row + 8 * c) = make_uint4(od[0], od[1], od[2], od[3]);
+    }
   }
 }
 
@@ -317,9 +422,10 @@ LOLLM_API long long lollm_gemm_workspace_bytes(int M, int N, int K, int grid) {
   return gemm_ws_bytes(M, N, nw);
 }
 
-LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, long long ldc,
-                         int M, int N, int K, int epilogue, void* workspace,
-                         long long workspace_bytes, int grid, void* stream) {
+// Validates the arguments common to the GEMM entry points and launches the main kernel.
+static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, void* C,
+                     long long ldc, int M, int N, int K, int epilogue, void* workspace,
+                     long long workspace_bytes, int grid, hipStream_t st) {
   if (!A || !Wt || !C || !workspace) return LOLLM_EINVAL;
   if (!gemm_shape_ok(M, N, K, epilogue)) return LOLLM_EUNSUPPORTED;
   const long long outc = epilogue == GM_EPI_SWIGLU ? N / 2 : N;
@@ -329,22 +435,45 @@ LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, 
   if (nw <= 0 || nw > GM_MAXW) return LOLLM_EUNSUPPORTED;
   if (workspace_bytes < gemm_ws_bytes(M, N, nw)) return LOLLM_EINVAL;
   if ((long long)(N / GM_COLS) * (K / GM_KC) >= (1LL << 31)) return LOLLM_EUNSUPPORTED;
-  GemmArgs a;
   a.A = (const uint16_t*)A; a.Wt = (const uint16_t*)Wt; a.C = (uint16_t*)C;
   a.part = (float*)workspace;
   a.lda = lda; a.ldc = ldc;
   a.M = M; a.N = N; a.K = K; a.G = N / GM_COLS; a.SK = K / GM_KC; a.nw = nw; a.epi = epilogue;
   a.U = a.G * a.SK;
-  hipStream_t st = (hipStream_t)stream;
-  const int mt = (M + 15) / 16;
-  switch (mt) {
+  switch ((M + 15) / 16) {
     case 1: hipLaunchKernelGGL(gemm_kernel<1>, dim3(nw), dim3(256), 0, st, a); break;
     case 2: hipLaunchKernelGGL(gemm_kernel<2>, dim3(nw), dim3(256), 0, st, a); break;
     case 3: hipLaunchKernelGGL(gemm_kernel<3>, dim3(nw), dim3(256), 0, st, a); break;
     default: hipLaunchKernelGGL(gemm_kernel<4>, dim3(nw), dim3(256), 0, st, a); break;
   }
-  int rc = launch_status();
+  return launch_status();
+}
+
+LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, long long ldc,
+                         int M, int N, int K, int epilogue, void* workspace,
+                         long long workspace_bytes, int grid, void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  GemmArgs a;
+  int rc = gemm_main(a, A, lda, Wt, C, ldc, M, N, K, epilogue, workspace, workspace_bytes, grid, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(gemm_fixup_kernel, dim3(a.G, mt), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(gemm_fixup_kernel, dim3(a.G, (M + 15) / 16), dim3(256), 0, st, a);
+  return launch_status();
+}
+
+LOLLM_API int lollm_gemm_rmsnorm(const void* A, long long lda, const void* Wt, int M, int N, int K,
+                                 const void* residual, const void* norm_w, float eps, void* C,
+                                 void* x_out, void* y, void* workspace, long long workspace_bytes,
+                                 int grid, void* stream) {
+  if (!residual || !norm_w || !x_out || !y) return LOLLM_EINVAL;
+  if (N > 8 * RMS_THREADS * RMS_CHUNKS) return LOLLM_EUNSUPPORTED;
+  if (M <= 0 || N <= 0 || K <= 0 || N % GM_COLS || K % GM_KC) return LOLLM_EUNSUPPORTED;
+  const int nw = gemm_grid(grid);
+  if (nw <= 0 || (long long)(N / GM_COLS) * (K / GM_KC) < nw) return LOLLM_EUNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  GemmArgs a;
+  int rc = gemm_main(a, A, lda, Wt, C, N, M, N, K, GM_EPI_NONE, workspace, workspace_bytes, grid, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(gemm_norm_kernel, dim3(M), dim3(RMS_THREADS), 0, st, a, (const uint16_t*)residual,
+                     (const uint16_t*)norm_w, (uint16_t*)x_out, (uint16_t*)y, eps);
   return launch_status();
 }

@@ -243,6 +243,49 @@ def gemm(x, tiled, N, K, epilogue=GEMM_NONE, out=None, grid=0):
     return out
 
 
+def gemm_rmsnorm_supported(M, N, K, grid=0):
+    """Whether lollm_gemm_rmsnorm takes this shape (N <= 8192 and at least one
+    (64-column, 128-k) unit per workgroup)."""
+    if not gemm_supported(N, K) or N > 8192 or not 0 < M <= GEMM_MAX_ROWS:
+        return False
+    if grid <= 0:
+        dev = torch.cuda.current_device()
+        if dev not in _cu_count:
+            _cu_count[dev] = torch.cuda.get_device_properties(dev).multi_processor_count
+        grid = 2 * _cu_count[dev]
+    return (N // 64) * (K // 128) >= grid
+
+
+_cu_count = {}
+
+
+def gemm_rmsnorm(x, tiled, N, K, residual, w, eps, grid=0):
+    """h = x W^T completed with the residual add and RMSNorm of the decoder layer:
+    x_out = bf16(h + residual), y = RMSNorm_{1+w}(x_out).  Returns (y, x_out), the same
+    bits as gemm() followed by rmsnorm(h, w, eps, residual=residual)."""
+    lead = x.shape[:-1]
+    M = x.numel() // K
+    if x.shape[-1] != K:
+        raise ValueError(f"x has {x.shape[-1]} features, expected {K}")
+    if M > GEMM_MAX_ROWS or M <= 0:
+        raise ValueError(f"lollm_gemm takes 1..{GEMM_MAX_ROWS} rows, got {M}")
+    x = x.contiguous()
+    _need(x, "x", torch.bfloat16)
+    _need(tiled, "tiled", torch.bfloat16, (N * K,))
+    residual = residual.contiguous()
+    _need(residual, "residual", torch.bfloat16, (*lead, N))
+    _need(w, "w", torch.bfloat16, (N,))
+    c = torch.empty(*lead, N, dtype=torch.bfloat16, device=x.device)
+    x_out = torch.empty_like(c)
+    y = torch.empty_like(c)
+    ws = gemm_workspace(gemm_workspace_bytes(M, N, K, grid), x.device)
+    rc = _lib.lib().lollm_gemm_rmsnorm(_ptr(x), K, _ptr(tiled), M, N, K, _ptr(residual), _ptr(w),
+                                       float(eps), _ptr(c), _ptr(x_out), _ptr(y), _ptr(ws),
+                                       ws.numel(), grid, _stream())
+    _lib.check(rc, "lollm_gemm_rmsnorm")
+    return y, x_out
+
+
 # ------------------------------------------------------------------------------------
 # speculative sampling
 # ------------------------------------------------------------------------------------

@@ -23,6 +23,7 @@ def _cat_rows(*ws):
 
 
 _FLUSH = {}
+_SHAPE_CHOICE = {}   # (N, K, epilogue, rows or ("norm", rows)) -> "gemm" | "blas"
 
 
 def _flush_caches(device):
@@ -39,11 +40,12 @@ class Projection:
     for hipBLASLt (F.linear) and a tiled copy for lollm_gemm (<= 64 rows).
     epilogue=GEMM_SWIGLU: W = [gate; up], y = silu(x gate^T) * x up^T (blocks.py:341-342).
 
-    For a row count lollm_gemm supports, the first eager call times both paths (three
-    runs each, HIP events, each run after the caches were flushed so the weight streams
-    from HBM as it does in a step that walks every layer) and keeps the faster one for
-    that row count; later calls -- and HIP-graph captures -- reuse the choice.  A call
-    under capture with no choice recorded yet takes lollm_gemm."""
+    For a row count lollm_gemm supports, the first eager call of a weight shape times
+    both paths (five runs each, alternating, HIP events, each run after the caches were
+    flushed so the weight streams from HBM as it does in a step that walks every layer)
+    and keeps the faster median for that (shape, row count); every projection of that
+    shape -- and later calls and HIP-graph captures -- reuse the choice.  A call under
+    capture with no choice recorded yet takes lollm_gemm."""
 
     def __init__(self, weight, epilogue=ops.GEMM_NONE):
         self.weight = weight.to(torch.bfloat16).contiguous()
@@ -64,32 +66,56 @@ class Projection:
     def _gemm(self, x):
         return ops.gemm(x, self.tiled, self.N, self.K, self.epilogue)
 
-    def _pick(self, x, rows):
+    def _pick(self, key, paths):
+        shape = (self.N, self.K, self.epilogue, key)
+        if shape in _SHAPE_CHOICE:
+            self.choice[key] = _SHAPE_CHOICE[shape]
+            return self.choice[key]
         if torch.cuda.is_current_stream_capturing():
             return "gemm"
-        times = {}
-        for name, fn in (("gemm", self._gemm), ("blas", self._blas)):
-            fn(x)
-            total = 0.0
-            for _ in range(3):
-                _flush_caches(x.device)
+        times = {name: [] for name in paths}
+        for fn in paths.values():
+            fn()
+        for _ in range(5):
+            for name, fn in paths.items():
+                _flush_caches(torch.cuda.current_device())
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
-                fn(x)
+                fn()
                 e1.record()
                 e1.synchronize()
-                total += e0.elapsed_time(e1)
-            times[name] = total
-        choice = min(times, key=times.get)
-        self.choice[rows] = choice
+                times[name].append(e0.elapsed_time(e1))
+        choice = min(times, key=lambda n: sorted(times[n])[len(times[n]) // 2])
+        _SHAPE_CHOICE[shape] = self.choice[key] = choice
         return choice
 
     def __call__(self, x):
         rows = x.numel() // self.K
         if self.tiled is None or rows > ops.GEMM_MAX_ROWS:
             return self._blas(x)
-        choice = self.choice.get(rows) or self._pick(x, rows)
+        choice = self.choice.get(rows) or self._pick(
+            rows, {"gemm": lambda: self._gemm(x), "blas": lambda: self._blas(x)})
         return self._gemm(x) if choice == "gemm" else self._blas(x)
+
+    def add_norm(self, x, residual, norm):
+        """The projection feeding the residual stream with the add and the next RMSNorm
+        (modeling_qwen3_5.py:59-60): x_out = residual + x W^T, y = norm(x_out); returns
+        (y, x_out).  lollm_gemm_rmsnorm (one GEMM call, the norm fused into its second
+        kernel) or F.linear + lollm_rmsnorm, chosen per row count as in __call__."""
+        rows = x.numel() // self.K
+        if (self.tiled is None or self.epilogue != ops.GEMM_NONE
+                or not ops.gemm_rmsnorm_supported(rows, self.N, self.K)):
+            return norm(self._blas(x), residual=residual)
+
+        def fused():
+            return ops.gemm_rmsnorm(x, self.tiled, self.N, self.K, residual, norm.weight, norm.eps)
+
+        def unfused():
+            return norm(self._blas(x), residual=residual)
+
+        key = ("norm", rows)
+        choice = self.choice.get(key) or self._pick(key, {"gemm": fused, "blas": unfused})
+        return fused() if choice == "gemm" else unfused()
 
 
 class RMSNorm:
@@ -148,17 +174,24 @@ class GatedDeltaNet:
     def projections(self):
         return [self.in_proj, self.out_proj]
 
-    def __call__(self, x, cache, layer):
+    def core(self, x, cache, layer):
+        """Everything before out_proj (blocks.py:288-325)."""
         B, T, _ = x.shape
         cfg = self.cfg
         proj = self.in_proj(x)
         s = cache.layers[layer]
-        core = ops.gdn_layer(proj, self.conv_w, self.A_log, self.dt_bias, self.norm_w, s["win"],
+        return ops.gdn_layer(proj, self.conv_w, self.A_log, self.dt_bias, self.norm_w, s["win"],
                              cache.conv_off, s["rec"], cache.rec_slot, cache.fresh, B, T,
                              cfg.linear_num_key_heads, cfg.linear_num_value_heads,
                              cfg.linear_key_head_dim, cfg.linear_conv_kernel_dim,
                              cfg.rms_norm_eps)
-        return self.out_proj(core)
+
+    @property
+    def out(self):
+        return self.out_proj
+
+    def __call__(self, x, cache, layer):
+        return self.out_proj(self.core(x, cache, layer))
 
 
 def rope_inv_freq(rotary_dim, theta, device):
@@ -184,8 +217,9 @@ class GatedAttention:
     def projections(self):
         return [self.qkv, self.o_proj]
 
-    def __call__(self, x, k_cache, v_cache, lengths, kv_len, rope_pos=None, grid=0,
-                 workspace=None):
+    def core(self, x, k_cache, v_cache, lengths, kv_len, rope_pos=None, grid=0,
+             workspace=None):
+        """Everything before o_proj (blocks.py:208-235)."""
         B, T, _ = x.shape
         cfg = self.cfg
         qkv = self.qkv(x)
@@ -193,5 +227,13 @@ class GatedAttention:
                                     cfg.num_attention_heads, cfg.num_key_value_heads,
                                     cfg.head_dim, cfg.rotary_dim, cfg.rms_norm_eps, k_cache,
                                     v_cache, rope_pos=rope_pos)
-        o = ops.attn_verify(q, k_cache, v_cache, kv_len, gate, grid=grid, workspace=workspace)
-        return self.o_proj(o)
+        return ops.attn_verify(q, k_cache, v_cache, kv_len, gate, grid=grid, workspace=workspace)
+
+    @property
+    def out(self):
+        return self.o_proj
+
+    def __call__(self, x, k_cache, v_cache, lengths, kv_len, rope_pos=None, grid=0,
+                 workspace=None):
+        return self.o_proj(self.core(x, k_cache, v_cache, lengths, kv_len, rope_pos=rope_pos,
+                                     grid=grid, workspace=workspace))

@@ -117,19 +117,23 @@ class Qwen3_5Model:
         lengths = cache.lengths
         kv_len = lengths + T
         ws = self.attn_workspace(B, T, cache.max_len)
-        m = None
+        # each residual-stream projection (o_proj / out_proj / down_proj) is issued with
+        # the residual add and the norm that follows it (modeling_qwen3_5.py:59-60)
+        pending = None   # (down_proj, its input): opens the next layer
         for i, layer in enumerate(self.model.layers):
-            if m is None:
+            if pending is None:
                 h_in = layer.input_layernorm(x)
             else:
-                h_in, x = layer.input_layernorm(m, residual=x)
+                h_in, x = pending[0].add_norm(pending[1], x, layer.input_layernorm)
             if layer.layer_type == "full_attention":
                 s = cache.layers[i]
-                h = layer.self_attn(h_in, s["k"], s["v"], lengths, kv_len,
-                                    grid=self.attn_grid, workspace=ws)
+                mixer = layer.self_attn
+                core = mixer.core(h_in, s["k"], s["v"], lengths, kv_len,
+                                  grid=self.attn_grid, workspace=ws)
             else:
-                h = layer.linear_attn(h_in, cache, i)
-            y, x = layer.post_attention_layernorm(h, residual=x)
-            m = layer.mlp(y)
-        normed, x = self.model.norm(m, residual=x)
+                mixer = layer.linear_attn
+                core = mixer.core(h_in, cache, i)
+            y, x = mixer.out.add_norm(core, x, layer.post_attention_layernorm)
+            pending = (layer.mlp.down, layer.mlp.gate_up(y))
+        normed, x = pending[0].add_norm(pending[1], x, self.model.norm)
         return x, normed

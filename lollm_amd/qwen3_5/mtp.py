@@ -54,11 +54,10 @@ class MTP:
                                self.pre_fc_norm_hidden(hidden)], -1))
         layer = self.layers[0]
         h_in = layer.input_layernorm(x)
-        h = layer.self_attn(h_in, k_cache, v_cache, lengths, kv_len, rope_pos=rope_pos,
-                            grid=self.model.attn_grid, workspace=ws)
-        y, x = layer.post_attention_layernorm(h, residual=x)
-        m = layer.mlp(y)
-        normed, x = self.norm(m, residual=x)
+        core = layer.self_attn.core(h_in, k_cache, v_cache, lengths, kv_len, rope_pos=rope_pos,
+                                    grid=self.model.attn_grid, workspace=ws)
+        y, x = layer.self_attn.out.add_norm(core, x, layer.post_attention_layernorm)
+        normed, x = layer.mlp.down.add_norm(layer.mlp.gate_up(y), x, self.norm)
         return x, normed
 
     def scratch_cache(self, B, L):

@@ -100,3 +100,46 @@ def test_projection_paths_agree():
     close(p._blas(x[:64].cuda()), ref[:64])
     close(p(x.cuda()), ref)
 
+
+
+@pytest.mark.parametrize("M,N,K,grid", [(64, 4096, 4096, 0), (16, 4096, 12288, 0), (5, 512, 128, 4),
+                                        (33, 1024, 256, 12), (64, 2048, 1024, 200),
+                                        (1, 8192, 128, 64)])
+def test_gemm_rmsnorm_equals_gemm_then_rmsnorm(M, N, K, grid):
+    """lollm_gemm_rmsnorm (the residual add and RMSNorm of modeling_qwen3_5.py:59-60
+    fused into the GEMM's second kernel) gives the same bits as lollm_gemm followed by
+    lollm_rmsnorm with the residual -- groups finished whole (grid 4 over 8 one-stage
+    groups), cut into pieces (grid 0) and mixed (grid 12, 200) -- and both match the
+    oracle's x + h then rmsnorm_plus1 (blocks.py:23-35)."""
+    from lollm_amd import ops
+    print(f"case gemm_rmsnorm M={M} N={N} K={K} grid={grid}", flush=True)
+    x, W = case(M, N, K, seed=M + N + K)
+    g = torch.Generator().manual_seed(N + 1)
+    res = torch.randn(M, N, generator=g).bfloat16()
+    w = (torch.randn(N, generator=g) * 0.1).bfloat16()
+    eps = 1e-6
+    assert ops.gemm_rmsnorm_supported(M, N, K, grid)
+    Wt = ops.gemm_tile_weights(W.cuda())
+    y, xo = ops.gemm_rmsnorm(x.cuda(), Wt, N, K, res.cuda(), w.cuda(), eps, grid=grid)
+    h = ops.gemm(x.cuda(), Wt, N, K, grid=grid)
+    y2, xo2 = ops.rmsnorm(h, w.cuda(), eps, residual=res.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(xo, xo2) and torch.equal(y, y2)
+    href = R.linear(x.float(), W.float()).bfloat16()
+    xref = (href.float() + res.float()).bfloat16()
+    close(xo, xref.float())
+    close(y, R.rmsnorm_plus1(xref, w, eps).float())
+
+
+def test_gemm_rmsnorm_rejects_unsupported():
+    """Rows wider than 8192, or fewer (64-column, 128-k) units than workgroups."""
+    from lollm_amd import ops
+    lib = ops._lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    p = buf.data_ptr()
+    assert not ops.gemm_rmsnorm_supported(16, 64, 128)            # 1 unit < 512 workgroups
+    assert lib.lollm_gemm_rmsnorm(p, 128, p, 16, 64, 128, p, p, 1e-6, p, p, p, p, buf.numel(), 0,
+                                  st) == 2
+    assert lib.lollm_gemm_rmsnorm(p, 128, p, 1, 8256, 128, p, p, 1e-6, p, p, p, p, buf.numel(), 1,
+                                  st) == 2
