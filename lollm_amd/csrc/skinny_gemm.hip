@@ -22,9 +22,10 @@
 // uneven rounds).  The activation tile of each stage (M x 128) is staged in LDS and
 // shared by the 4 waves; weight loads run 4 units ahead in a register ring, activation
 // loads 2 units ahead.  A group one workgroup covers whole is stored directly (with
-// the epilogue); a group cut between workgroups leaves an fp32 piece (rows x 64, row
-// major) in slot w + group, merged by gemm_fixup_kernel with one float4 per thread
-// over a (group, m-tile) grid, or by gemm_norm_kernel row by row.  (Merging
+// the epilogue); a group cut between workgroups leaves an fp32 piece in slot
+// w + group: in accumulator order (each wave's store one contiguous 1 KB) when
+// gemm_fixup_kernel merges it with one float4 per thread over a (group, m-tile) grid,
+// row major when gemm_norm_kernel merges it row by row.  (Merging
 // in the last-arriving workgroup instead would need device-scope release / acquire
 // fences, which write back and invalidate the XCD's L2 -- measured 3-10x slower here
 // than the second launch.)
@@ -49,9 +50,10 @@ struct GemmArgs {
   const uint16_t* A;     // (M, K) activations, row stride lda
   const uint16_t* Wt;    // tiled weights
   uint16_t* C;           // (M, ldc)
-  float* part;           // (nw + G) pieces of (16 MT) x 64 fp32, row major
+  float* part;           // (nw + G) pieces of (16 MT) x 64 fp32
   long long lda, ldc;
   int M, N, K, G, SK, nw, epi, U;
+  int rowmajor;          // piece layout: 0 = accumulator order (float4 (i, wave, lane)), 1 = row major
 };
 
 __device__ __forceinline__ void gm_lds_barrier() {
@@ -170,9 +172,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
       // are ordered in both w and g, so the slot is unique); padding rows included
       float* pp = a.part + ((size_t)w + g) * ((size_t)MT * 16 * GM_COLS);
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
-        *reinterpret_cast<float4*>(pp + (size_t)(16 * i + l16) * GM_COLS + 16 * wave + 4 * g4) =
-            make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+      for (int i = 0; i < MT; ++i) {
+        const size_t off = a.rowmajor ? (size_t)(16 * i + l16) * GM_COLS + 16 * wave + 4 * g4
+                                      : (((size_t)i * 4 + wave) * 64 + lane) * 4;
+        *reinterpret_cast<float4*>(pp + off) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+      }
     }
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -247,7 +251,7 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
   const int mt = (a.M + 15) / 16;
   const size_t piece = (size_t)mt * 16 * GM_COLS;
   const int m = 16 * i + (lane & 15), g4 = lane >> 4;
-  const size_t off = (size_t)m * GM_COLS + 16 * wave + 4 * g4;
+  const size_t off = (((size_t)i * 4 + wave) * 64 + lane) * 4;   // accumulator order
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int k0 = 0; k0 < np; k0 += GM_PB) {
     // GM_PB pieces' loads in flight together (indices past np re-read the last, unused)
@@ -425,7 +429,7 @@ LOLLM_API long long lollm_gemm_workspace_bytes(int M, int N, int K, int grid) {
 // Validates the arguments common to the GEMM entry points and launches the main kernel.
 static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, void* C,
                      long long ldc, int M, int N, int K, int epilogue, void* workspace,
-                     long long workspace_bytes, int grid, hipStream_t st) {
+                     long long workspace_bytes, int grid, int rowmajor, hipStream_t st) {
   if (!A || !Wt || !C || !workspace) return LOLLM_EINVAL;
   if (!gemm_shape_ok(M, N, K, epilogue)) return LOLLM_EUNSUPPORTED;
   const long long outc = epilogue == GM_EPI_SWIGLU ? N / 2 : N;
@@ -440,6 +444,7 @@ static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, 
   a.lda = lda; a.ldc = ldc;
   a.M = M; a.N = N; a.K = K; a.G = N / GM_COLS; a.SK = K / GM_KC; a.nw = nw; a.epi = epilogue;
   a.U = a.G * a.SK;
+  a.rowmajor = rowmajor;
   switch ((M + 15) / 16) {
     case 1: hipLaunchKernelGGL(gemm_kernel<1>, dim3(nw), dim3(256), 0, st, a); break;
     case 2: hipLaunchKernelGGL(gemm_kernel<2>, dim3(nw), dim3(256), 0, st, a); break;
@@ -454,8 +459,10 @@ LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, 
                          long long workspace_bytes, int grid, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   GemmArgs a;
-  int rc = gemm_main(a, A, lda, Wt, C, ldc, M, N, K, epilogue, workspace, workspace_bytes, grid, st);
+  int rc = gemm_main(a, A, lda, Wt, C, ldc, M, N, K, epilogue, workspace, workspace_bytes, grid, 0, st);
   if (rc) return rc;
+  // every range a whole number of whole groups (grid divides the groups): nothing to merge
+  if (a.G % a.nw == 0) return LOLLM_OK;
   hipLaunchKernelGGL(gemm_fixup_kernel, dim3(a.G, (M + 15) / 16), dim3(256), 0, st, a);
   return launch_status();
 }
@@ -471,7 +478,7 @@ LOLLM_API int lollm_gemm_rmsnorm(const void* A, long long lda, const void* Wt, i
   if (nw <= 0 || (long long)(N / GM_COLS) * (K / GM_KC) < nw) return LOLLM_EUNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
   GemmArgs a;
-  int rc = gemm_main(a, A, lda, Wt, C, N, M, N, K, GM_EPI_NONE, workspace, workspace_bytes, grid, st);
+  int rc = gemm_main(a, A, lda, Wt, C, N, M, N, K, GM_EPI_NONE, workspace, workspace_bytes, grid, 1, st);
   if (rc) return rc;
   hipLaunchKernelGGL(gemm_norm_kernel, dim3(M), dim3(RMS_THREADS), 0, st, a, (const uint16_t*)residual,
                      (const uint16_t*)norm_w, (uint16_t*)x_out, (uint16_t*)y, eps);
