@@ -434,19 +434,28 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* __rest
 }
 
 // ---------------------------------------------------------------- inverse-CDF draw
-// Wave w of the 16 owns chunks [w * seg, min((w + 1) * seg, nch)).  W8(c, w[8]) gives
-// the weights of the 8 tokens of chunk c.
-template <typename Acc, typename W8>
-__device__ Acc draw_totals(int nch, int seg, W8 w8, Acc* wtot) {
+// Wave w of the 16 owns chunks [w * seg, min((w + 1) * seg, nch)).  ld(c) loads chunk c
+// (8 tokens; addresses clamped in range by the callers here), wt(raw, c, w[8]) turns it
+// into the 8 token weights.  The totals pass keeps UN chunks per lane in flight.
+template <typename Acc, int UN, typename LD, typename WT>
+__device__ Acc draw_totals(int nch, int seg, LD ld, WT wt, Acc* wtot) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __syncthreads();  // wtot may still be read by a previous draw's waves
   const int c0 = wave * seg, c1 = min(c0 + seg, nch);
   Acc acc = 0;
-  for (int c = c0 + lane; c < c1; c += 64) {
-    Acc w[8];
-    w8(c, w);
+  for (int c = c0 + lane; c < c1; c += 64 * UN) {
+    decltype(ld(0)) r[UN];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += w[e];
+    for (int u = 0; u < UN; ++u) r[u] = ld(min(c + 64 * u, c1 - 1));
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      if (c + 64 * u < c1) {
+        Acc w[8];
+        wt(r[u], c + 64 * u, w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += w[e];
+      }
+    }
   }
   acc = wave_sum_any(acc);
   if (lane == 0) wtot[wave] = acc;
@@ -458,8 +467,8 @@ __device__ Acc draw_totals(int nch, int seg, W8 w8, Acc* wtot) {
 }
 
 // The first token whose inclusive prefix exceeds target (< the row total).
-template <typename Acc, typename W8>
-__device__ int32_t draw_find(int nch, int seg, W8 w8, const Acc* wtot, Acc target, int V,
+template <typename Acc, typename LD, typename WT>
+__device__ int32_t draw_find(int nch, int seg, LD ld, WT wt, const Acc* wtot, Acc target, int V,
                              int32_t* found) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   Acc before = 0;
@@ -470,15 +479,17 @@ __device__ int32_t draw_find(int nch, int seg, W8 w8, const Acc* wtot, Acc targe
   }
   if (threadIdx.x == 0) *found = -1;
   __syncthreads();
-  if (wave == ow) {
-    const int c0 = ow * seg, c1 = min(c0 + seg, nch);
+  const int c0 = ow * seg, c1 = min(c0 + seg, nch);
+  if (wave == ow && c0 < c1) {
     Acc run = before;
+    auto cur = ld(min(c0 + lane, c1 - 1));
     for (int cb = c0; cb < c1; cb += 64) {
       const int c = cb + lane;
+      const auto nxt = ld(min(cb + 64 + lane, c1 - 1));   // next step's chunk, in flight
       Acc w[8];
       Acc sum = 0;
       if (c < c1) {
-        w8(c, w);
+        wt(cur, c, w);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) w[e] = 0;
@@ -500,12 +511,15 @@ __device__ int32_t draw_find(int nch, int seg, W8 w8, const Acc* wtot, Acc targe
         break;
       }
       run += tot;
+      cur = nxt;
     }
   }
   __syncthreads();
   const int32_t f = *found;
   return f < 0 ? V - 1 : f;
 }
+
+struct ChunkPair { u32x4_t p, q; };   // vector members: copies stay in registers
 
 __device__ __forceinline__ u128 scaled_target(uint32_t U, u128 M) {
   return (u128)U * (M >> 24) + (((u128)U * (uint64_t)(M & 0xFFFFFFu)) >> 24);
@@ -517,17 +531,17 @@ __device__ int32_t draw_plain(const uint16_t* xp, const RowStat& sp, const uint6
                               int V, uint64_t* wtot, int32_t* found) {
   if (sp.greedy) return sp.argmax;
   const int nch = V >> 3, seg = (nch + SP_THREADS / 64 - 1) / (SP_THREADS / 64);
-  const uint4* x4 = reinterpret_cast<const uint4*>(xp);
-  auto w8 = [&](int ch, uint64_t* w) {
-    const uint4 u = x4[ch];
+  const u32x4_t* v4 = reinterpret_cast<const u32x4_t*>(xp);
+  auto ld = [=](int ch) { return v4[ch]; };
+  auto wt = [=](const u32x4_t& u, int ch, uint64_t* w) {
     const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       w[e] = table_weight(sp, tab, (wd[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, ch * 8 + e);
   };
-  draw_totals<uint64_t>(nch, seg, w8, wtot);
+  draw_totals<uint64_t, 4>(nch, seg, ld, wt, wtot);
   const uint64_t tgt = (uint64_t)(((u128)U * sp.Z) >> 24);
-  return draw_find<uint64_t>(nch, seg, w8, wtot, tgt, V, found);
+  return draw_find<uint64_t>(nch, seg, ld, wt, wtot, tgt, V, found);
 }
 
 __global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
@@ -589,8 +603,11 @@ __global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
       const uint64_t Zq = sq.Z;
       build_table(sq, c, tab_q);
       __syncthreads();
-      auto w8 = [&](int ch, u128* w) {
-        const uint4 up = xp4[ch], uq = xq4[ch];
+      const u32x4_t* vp = reinterpret_cast<const u32x4_t*>(xp4);
+      const u32x4_t* vq = reinterpret_cast<const u32x4_t*>(xq4);
+      auto ld = [=](int ch) { return ChunkPair{vp[ch], vq[ch]}; };
+      auto wt = [=](const ChunkPair& r, int ch, u128* w) {
+        const u32x4_t up = r.p, uq = r.q;
         const uint32_t pw[4] = {up.x, up.y, up.z, up.w}, qw[4] = {uq.x, uq.y, uq.z, uq.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -601,14 +618,15 @@ __global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
           w[e] = l > r ? l - r : (u128)0;
         }
       };
-      const u128 R = draw_totals<u128>(nch, seg, w8, wt128);
+      const u128 R = draw_totals<u128, 2>(nch, seg, ld, wt, wt128);
       tok = R == 0 ? draw_plain(xp, sp, tab_p, U, V, wt64, &found)
-                   : draw_find<u128>(nch, seg, w8, wt128, scaled_target(U, R), V, &found);
+                   : draw_find<u128>(nch, seg, ld, wt, wt128, scaled_target(U, R), V, &found);
     } else {
       // q one-hot at d: residual wp - [t == d] Zp fits 64 bits
       __syncthreads();
-      auto w8 = [&](int ch, uint64_t* w) {
-        const uint4 up = xp4[ch];
+      const u32x4_t* vp = reinterpret_cast<const u32x4_t*>(xp4);
+      auto ld = [=](int ch) { return vp[ch]; };
+      auto wt = [=](const u32x4_t& up, int ch, uint64_t* w) {
         const uint32_t pw[4] = {up.x, up.y, up.z, up.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -618,9 +636,9 @@ __global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
           w[e] = wpt > r ? wpt - r : 0;
         }
       };
-      const uint64_t R = draw_totals<uint64_t>(nch, seg, w8, wt64);
+      const uint64_t R = draw_totals<uint64_t, 4>(nch, seg, ld, wt, wt64);
       tok = R == 0 ? draw_plain(xp, sp, tab_p, U, V, wt64, &found)
-                   : draw_find<uint64_t>(nch, seg, w8, wt64,
+                   : draw_find<uint64_t>(nch, seg, ld, wt, wt64,
                                          (uint64_t)scaled_target(U, (u128)R), V, &found);
     }
   }
