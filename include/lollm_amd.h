@@ -226,6 +226,22 @@ int lollm_gdn_layer(const void* proj, long long proj_stride, const void* conv_w,
                     int slots, int fresh, void* out, int B, int T, int Hk, int Hv, int Dk, int Dv,
                     int conv_kernel, float eps, void* stream);
 
+/* The same layer for long calls (prefill) with the delta rule in its chunked parallel
+ * form: torch_chunk_gated_delta_rule (src/qwen3_5/blocks.py:59-113), which the reference
+ * runs for every T > 1 call (blocks.py:316-322), fused with the conv / gating / norm of
+ * lollm_gdn_layer.  Chunks of 64 tokens, all products fp32 MFMA; the L2 norm of q and
+ * k (blocks.py:124-127) is applied as fp32 scales, as the recurrent kernels do.  Same
+ * arguments and the same long-call placement as lollm_gdn_layer: the final state in
+ * slot 0 of the half not holding rec_slot[b], the final K-1 raw inputs in rows 0 .. K-2
+ * of the window half not holding conv_off[b].  Supported: conv_kernel 4, T > slots,
+ * K - 1 + T > win_rows (the call does not fit a window half), else LOLLM_EUNSUPPORTED. */
+int lollm_gdn_layer_chunked(const void* proj, long long proj_stride, const void* conv_w,
+                            const float* A_log, const float* dt_bias, const void* norm_w,
+                            void* win, const int32_t* conv_off, int win_rows, float* rec,
+                            const int32_t* rec_slot, int slots, int fresh, void* out, int B, int T,
+                            int Hk, int Hv, int Dk, int Dv, int conv_kernel, float eps,
+                            void* stream);
+
 /* End of one speculative step, per sequence b with a = n_accepted[b] (of T - 1
  * drafts): keep a + 1 of the T verified positions (lengths += a + 1, GDN snapshot
  * slot = written half + a, conv window offset = written half + a + 1, with the halves

@@ -413,10 +413,20 @@ def attn_prologue(qkv, q_norm_w, k_norm_w, inv_freq, lengths, B, T, Hq, Hkv, D, 
     return q_out, gate_out
 
 
+GDN_CHUNK_MIN_T = 64
+
+
+def gdn_chunked_ok(T, slots, win_rows, conv_kernel):
+    """Whether a call can take the chunked long-call kernel (lollm_gdn_layer_chunked)."""
+    return conv_kernel == 4 and T > slots and conv_kernel - 1 + T > win_rows
+
+
 def gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, fresh, B, T,
-              Hk, Hv, D, conv_kernel, eps, out=None):
+              Hk, Hv, D, conv_kernel, eps, out=None, chunked=None):
     """Fused GDN mixer (include/lollm_amd.h).  proj (B, T, P) bf16; win (B, 2W,
-    conv_dim) bf16; rec (B, 2S, Hv, D, D) fp32; conv_off / rec_slot (B,) int32."""
+    conv_dim) bf16; rec (B, 2S, Hv, D, D) fp32; conv_off / rec_slot (B,) int32.
+    chunked: None = the chunked kernel for long calls of at least GDN_CHUNK_MIN_T tokens
+    that it supports, the recurrent kernel otherwise; True / False force one."""
     P = proj.shape[-1]
     _need(proj, "proj", torch.bfloat16)
     _need(win, "win", torch.bfloat16)
@@ -428,11 +438,15 @@ def gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot
     value_dim = Hv * D
     if out is None:
         out = torch.empty(B, T, value_dim, dtype=torch.bfloat16, device=proj.device)
-    rc = _lib.lib().lollm_gdn_layer(
+    W, S = win.shape[1] // 2, rec.shape[1] // 2
+    if chunked is None:
+        chunked = T >= GDN_CHUNK_MIN_T and gdn_chunked_ok(T, S, W, conv_kernel)
+    fn = "lollm_gdn_layer_chunked" if chunked else "lollm_gdn_layer"
+    rc = getattr(_lib.lib(), fn)(
         _ptr(proj), P, _ptr(conv_w), _ptr(A_log), _ptr(dt_bias), _ptr(norm_w), _ptr(win),
-        _ptr(conv_off), win.shape[1] // 2, _ptr(rec), _ptr(rec_slot), rec.shape[1] // 2,
-        int(bool(fresh)), _ptr(out), B, T, Hk, Hv, D, D, conv_kernel, float(eps), _stream())
-    _lib.check(rc, "lollm_gdn_layer")
+        _ptr(conv_off), W, _ptr(rec), _ptr(rec_slot), S, int(bool(fresh)), _ptr(out), B, T, Hk,
+        Hv, D, D, conv_kernel, float(eps), _stream())
+    _lib.check(rc, fn)
     return out
 
 

@@ -108,3 +108,71 @@ def test_gdn_layer_verify_matches_oracle(B, T, S):
         assert torch.equal(win_o[b, wbase + K - 1:wbase + K - 1 + T], proj[b, :, :C])
         other = slice(W - wbase, 2 * W - wbase)
         assert torch.equal(win_o[b, other], win[b, other])
+
+
+@pytest.mark.parametrize("B,T,S,fresh", [(2, 64, 4, False), (2, 130, 4, False), (1, 257, 8, True),
+                                         (2, 70, 4, True)])
+def test_gdn_layer_chunked_matches_oracle(B, T, S, fresh):
+    """The chunked long-call kernel (blocks.py:59-113 fused with the layer's conv, gating
+    and gated norm) against the oracle's recurrence: outputs at the model-test bar, the
+    final state (slot 0 of the written half) to rtol 2e-2 of the state scale, the final
+    K-1 raw inputs in the written window half bit for bit, the committed halves untouched."""
+    from lollm_amd import ops
+    print(f"case gdn_layer_chunked B={B} T={T} S={S} fresh={fresh}", flush=True)
+    proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, W = make(B, T, S, 7 * T + B)
+    rec_in = rec.clone()
+    if fresh:
+        for b in range(B):
+            rec_in[b, int(rec_slot[b])] = 0
+    ref_o, _ = oracle(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec_in, rec_slot, T)
+    r32_o, ref_s = oracle(proj.float(), conv_w.float(), A_log, dt_bias, norm_w.float(),
+                          win.float(), conv_off, rec_in, rec_slot, T)
+    win_d, rec_d = win.cuda(), rec.cuda()
+    assert ops.gdn_chunked_ok(T, S, W, K)
+    out = ops.gdn_layer(proj.cuda(), conv_w.cuda(), A_log.cuda(), dt_bias.cuda(), norm_w.cuda(),
+                        win_d, conv_off.cuda(), rec_d, rec_slot.cuda(), fresh, B, T, Hk, Hv, D, K,
+                        1e-6, chunked=True)
+    torch.cuda.synchronize()
+    got = out.cpu().float()
+    err = (got - r32_o).abs().max().item()
+    budget = 2 * (ref_o.float() - r32_o).abs().max().item() + 1e-3 * r32_o.abs().max().item()
+    assert err <= budget, f"max err {err:.4g} > budget {budget:.4g}"
+    bad = ~torch.isclose(got, ref_o.float(), rtol=2e-2, atol=2e-2)
+    assert bad.float().mean().item() <= 1e-3, f"{int(bad.sum())} of {bad.numel()} outside 2e-2"
+    win_o, rec_o = win_d.cpu(), rec_d.cpu()
+    for b in range(B):
+        off, slot = int(conv_off[b]), int(rec_slot[b])
+        wbase = 0 if off >= W else W
+        rbase = 0 if slot >= S else S
+        scale = ref_s[b, -1].abs().max().item()
+        torch.testing.assert_close(rec_o[b, rbase], ref_s[b, -1], rtol=2e-2, atol=2e-2 * scale)
+        keep = slice(S - rbase, 2 * S - rbase)
+        assert torch.equal(rec_o[b, keep], rec[b, keep])
+        assert torch.equal(win_o[b, wbase:wbase + K - 1], proj[b, T - K + 1:, :C])
+        other = slice(W - wbase, 2 * W - wbase)
+        assert torch.equal(win_o[b, other], win[b, other])
+
+
+def test_gdn_layer_chunked_agrees_with_recurrent():
+    """Chunked and recurrent long-call kernels on the same inputs: outputs within the
+    bf16 bar of each other, final states within 2e-2 of the state scale (they differ by
+    summation order only)."""
+    from lollm_amd import ops
+    B, T, S = 2, 192, 4
+    proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, W = make(B, T, S, 99)
+    res = []
+    for chunked in (True, False):
+        win_d, rec_d = win.cuda(), rec.cuda()
+        out = ops.gdn_layer(proj.cuda(), conv_w.cuda(), A_log.cuda(), dt_bias.cuda(),
+                            norm_w.cuda(), win_d, conv_off.cuda(), rec_d, rec_slot.cuda(), False,
+                            B, T, Hk, Hv, D, K, 1e-6, chunked=chunked)
+        torch.cuda.synchronize()
+        res.append((out.cpu().float(), rec_d.cpu(), win_d.cpu()))
+    (oc, rc, wc), (orr, rr, wr) = res
+    bad = ~torch.isclose(oc, orr, rtol=2e-2, atol=2e-2)
+    assert bad.float().mean().item() <= 1e-3
+    assert torch.equal(wc, wr)
+    for b in range(B):
+        rbase = 0 if int(rec_slot[b]) >= S else S
+        scale = rr[b, rbase].abs().max().item()
+        torch.testing.assert_close(rc[b, rbase], rr[b, rbase], rtol=2e-2, atol=2e-2 * scale)
