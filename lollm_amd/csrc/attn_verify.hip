@@ -548,12 +548,14 @@ LOLLM_API int lollm_attn_verify(const void* q, const void* k_cache, const void* 
   a.max_len = max_len; a.nw = nw;
   a.cl2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
-  static bool lds_set = false;
-  if (!lds_set) {
+  static bool lds_set[64] = {};   // per device: the attribute is set on the current device
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return LOLLM_EUNSUPPORTED;
+  if (!lds_set[dev]) {
     hipError_t e = hipFuncSetAttribute((const void*)attn_verify_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, AT_LDS_BYTES);
     if (e != hipSuccess) return LOLLM_EHIP_BASE + (int)e;
-    lds_set = true;
+    lds_set[dev] = true;
   }
   hipLaunchKernelGGL(attn_verify_kernel, dim3(nw), dim3(256), AT_LDS_BYTES, st, a);
   if ((rc = launch_status())) return rc;

@@ -28,8 +28,10 @@
 //                points and the kept mass Z;
 //   argmax_*     greedy rows: the row split over 16 workgroups, partial maxima
 //                merged by a second tiny kernel (a greedy row needs no histogram);
-//   spec_accept  one workgroup per sequence: the k accept tests in parallel, then
-//                the residual or bonus draw;
+//   spec_partial / spec_final  the k accept tests in parallel, then the residual or
+//                bonus draw in two passes: ns workgroups per sequence sum the draw's
+//                weights over ns contiguous vocabulary slices, then one workgroup per
+//                sequence locates the slice holding the target and the token in it;
 //   sample_rows  one draw per row.
 // A draw is an inverse CDF over token ids in two steps: every wave of the block
 // sums the weights of its own contiguous sixteenth of the row (coalesced, one pass,
@@ -39,6 +41,8 @@
 // same weight_of) and then reads one entry per token.  Residual masses are 64-bit
 // when q is one-hot (argmax drafts) and 128-bit when q is a sampled distribution.
 #include "common.h"
+
+#include <algorithm>
 
 namespace lollm {
 
@@ -434,14 +438,20 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* __rest
 }
 
 // ---------------------------------------------------------------- inverse-CDF draw
-// Wave w of the 16 owns chunks [w * seg, min((w + 1) * seg, nch)).  ld(c) loads chunk c
-// (8 tokens; addresses clamped in range by the callers here), wt(raw, c, w[8]) turns it
-// into the 8 token weights.  The totals pass keeps UN chunks per lane in flight.
+// Over the chunk range [lo, hi), wave w of the 16 owns [lo + w seg, min(lo + (w + 1) seg,
+// hi)) with seg = ceil((hi - lo) / 16).  ld(c) loads chunk c (8 tokens; addresses stay in
+// [lo, hi)), wt(raw, c, w[8]) turns it into the 8 token weights.  The totals pass keeps
+// UN chunks per lane in flight.
+__device__ __forceinline__ int range_seg(int lo, int hi) {
+  return (hi - lo + SP_THREADS / 64 - 1) / (SP_THREADS / 64);
+}
+
 template <typename Acc, int UN, typename LD, typename WT>
-__device__ Acc draw_totals(int nch, int seg, LD ld, WT wt, Acc* wtot) {
+__device__ Acc draw_totals(int lo, int hi, LD ld, WT wt, Acc* wtot) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __syncthreads();  // wtot may still be read by a previous draw's waves
-  const int c0 = wave * seg, c1 = min(c0 + seg, nch);
+  const int seg = range_seg(lo, hi);
+  const int c0 = lo + wave * seg, c1 = min(c0 + seg, hi);
   Acc acc = 0;
   for (int c = c0 + lane; c < c1; c += 64 * UN) {
     decltype(ld(0)) r[UN];
@@ -466,9 +476,10 @@ __device__ Acc draw_totals(int nch, int seg, LD ld, WT wt, Acc* wtot) {
   return tot;
 }
 
-// The first token whose inclusive prefix exceeds target (< the row total).
+// The first token of [lo, hi) whose inclusive prefix (from lo) exceeds target (< the
+// range total held in wtot by draw_totals).
 template <typename Acc, typename LD, typename WT>
-__device__ int32_t draw_find(int nch, int seg, LD ld, WT wt, const Acc* wtot, Acc target, int V,
+__device__ int32_t draw_find(int lo, int hi, LD ld, WT wt, const Acc* wtot, Acc target, int V,
                              int32_t* found) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   Acc before = 0;
@@ -479,7 +490,8 @@ __device__ int32_t draw_find(int nch, int seg, LD ld, WT wt, const Acc* wtot, Ac
   }
   if (threadIdx.x == 0) *found = -1;
   __syncthreads();
-  const int c0 = ow * seg, c1 = min(c0 + seg, nch);
+  const int seg = range_seg(lo, hi);
+  const int c0 = lo + ow * seg, c1 = min(c0 + seg, hi);
   if (wave == ow && c0 < c1) {
     Acc run = before;
     auto cur = ld(min(c0 + lane, c1 - 1));
@@ -530,7 +542,7 @@ __device__ __forceinline__ u128 scaled_target(uint32_t U, u128 M) {
 __device__ int32_t draw_plain(const uint16_t* xp, const RowStat& sp, const uint64_t* tab, uint32_t U,
                               int V, uint64_t* wtot, int32_t* found) {
   if (sp.greedy) return sp.argmax;
-  const int nch = V >> 3, seg = (nch + SP_THREADS / 64 - 1) / (SP_THREADS / 64);
+  const int nch = V >> 3;
   const u32x4_t* v4 = reinterpret_cast<const u32x4_t*>(xp);
   auto ld = [=](int ch) { return v4[ch]; };
   auto wt = [=](const u32x4_t& u, int ch, uint64_t* w) {
@@ -539,28 +551,27 @@ __device__ int32_t draw_plain(const uint16_t* xp, const RowStat& sp, const uint6
     for (int e = 0; e < 8; ++e)
       w[e] = table_weight(sp, tab, (wd[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, ch * 8 + e);
   };
-  draw_totals<uint64_t, 4>(nch, seg, ld, wt, wtot);
+  draw_totals<uint64_t, 4>(0, nch, ld, wt, wtot);
   const uint64_t tgt = (uint64_t)(((u128)U * sp.Z) >> 24);
-  return draw_find<uint64_t>(nch, seg, ld, wt, wtot, tgt, V, found);
+  return draw_find<uint64_t>(0, nch, ld, wt, wtot, tgt, V, found);
 }
 
-__global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
-    const uint16_t* __restrict__ target, const uint16_t* __restrict__ draft,
-    const int32_t* __restrict__ drafts, int k, int V, float inv_temp, uint64_t seed,
-    uint64_t offset_arg, const uint64_t* __restrict__ offset_dev, const RowStat* __restrict__ st_t,
-    const RowStat* __restrict__ st_d, int32_t* __restrict__ n_accepted,
-    int32_t* __restrict__ next_token) {
-  __shared__ u128 wt128[SP_THREADS / 64];
-  __shared__ uint64_t wt64[SP_THREADS / 64];
-  __shared__ int32_t found;
-  __shared__ int32_t ok[64];
-  __shared__ uint64_t tab_p[SP_NBINS], tab_q[SP_NBINS];
-  const int b = blockIdx.x;
-  const int tid = threadIdx.x;
-  const uint64_t offset = offset_dev ? *offset_dev : offset_arg;
-  const float c = inv_temp * 1.44269504088896341f;
-  // ---- the k accept tests, one thread each ----
-  for (int i = tid; i < k; i += SP_THREADS) {
+// ---------------------------------------------------------------- acceptance
+// The accept tests of sequence b (rows st_t[b (k+1) + i], st_d[b k + i]) and the
+// distribution its emitted token is drawn from; every workgroup working on b derives
+// the same plan.
+struct AcceptPlan {
+  int a;          // accepted drafts
+  int kind;       // 0: p of row a (bonus, a == k), 1: residual with sampled q, 2: residual with one-hot q
+  int d;          // the rejected draft (kinds 1, 2)
+  uint32_t U;     // the draw's uniform
+};
+
+__device__ AcceptPlan accept_plan(const uint16_t* target, const uint16_t* draft,
+                                  const int32_t* drafts, int k, int V, float c, uint64_t seed,
+                                  uint64_t offset, const RowStat* st_t, const RowStat* st_d, int b,
+                                  int32_t* ok) {
+  for (int i = threadIdx.x; i < k; i += SP_THREADS) {
     int32_t d = drafts[b * k + i];
     d = d < 0 ? 0 : (d >= V ? V - 1 : d);
     const RowStat sp = st_t[b * (k + 1) + i];
@@ -572,78 +583,170 @@ __global__ __launch_bounds__(SP_THREADS) void spec_accept_kernel(
       wq = token_weight(sq, c, draft[((size_t)b * k + i) * V + d], d);
       Zq = sq.Z;
     }
-    const uint32_t U = philox_u24(seed, offset, (uint32_t)b, (uint32_t)i);
-    const u128 lhs = (u128)U * wq * Zp;
+    const uint32_t Ui = philox_u24(seed, offset, (uint32_t)b, (uint32_t)i);
+    const u128 lhs = (u128)Ui * wq * Zp;
     const u128 rhs = ((u128)wp * Zq) << 24;
     if (i < 64) ok[i] = lhs < rhs;
   }
   __syncthreads();
-  int a = 0;
-  while (a < k && a < 64 && ok[a]) ++a;
-  const bool rej = a < k;
-  const uint32_t U = philox_u24(seed, offset, (uint32_t)b, (uint32_t)k);
+  AcceptPlan pl;
+  pl.a = 0;
+  while (pl.a < k && pl.a < 64 && ok[pl.a]) ++pl.a;
+  pl.kind = pl.a == k ? 0 : (draft ? 1 : 2);
+  int32_t d = pl.a < k ? drafts[b * k + pl.a] : 0;
+  pl.d = d < 0 ? 0 : (d >= V ? V - 1 : d);
+  pl.U = philox_u24(seed, offset, (uint32_t)b, (uint32_t)k);
+  return pl;
+}
+
+// Runs f(ld, wt, acc_tag) with the chunk loader and weight function of the plan's draw
+// (tables filled and visible on return from the setup).
+template <typename F>
+__device__ void with_draw(const AcceptPlan& pl, const uint16_t* target, const uint16_t* draft,
+                          int k, int V, float c, const RowStat* st_t, const RowStat* st_d, int b,
+                          uint64_t* tab_p, uint64_t* tab_q, F f) {
+  const RowStat sp = st_t[b * (k + 1) + pl.a];
+  const uint16_t* xp = target + ((size_t)b * (k + 1) + pl.a) * V;
+  const u32x4_t* vp = reinterpret_cast<const u32x4_t*>(xp);
+  build_table(sp, c, tab_p);
+  if (pl.kind == 1) {
+    // q a sampled distribution: residual wp Zq - wq Zp in 128 bits
+    const RowStat sq = st_d[b * k + pl.a];
+    const u32x4_t* vq = reinterpret_cast<const u32x4_t*>(draft + ((size_t)b * k + pl.a) * V);
+    const uint64_t Zq = sq.Z;
+    build_table(sq, c, tab_q);
+    __syncthreads();
+    auto ld = [=](int ch) { return ChunkPair{vp[ch], vq[ch]}; };
+    auto wt = [=](const ChunkPair& r, int ch, u128* w) {
+      const u32x4_t up = r.p, uq = r.q;
+      const uint32_t pw[4] = {up.x, up.y, up.z, up.w}, qw[4] = {uq.x, uq.y, uq.z, uq.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = ch * 8 + e;
+        const uint64_t wpt = table_weight(sp, tab_p, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
+        const uint64_t wqt = table_weight(sq, tab_q, (qw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
+        const u128 l = (u128)wpt * Zq, r = (u128)wqt * sp.Z;
+        w[e] = l > r ? l - r : (u128)0;
+      }
+    };
+    f(ld, wt, (u128)0);
+  } else if (pl.kind == 2) {
+    // q one-hot at d: residual wp - [t == d] Zp fits 64 bits
+    __syncthreads();
+    const int d = pl.d;
+    auto ld = [=](int ch) { return vp[ch]; };
+    auto wt = [=](const u32x4_t& up, int ch, uint64_t* w) {
+      const uint32_t pw[4] = {up.x, up.y, up.z, up.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = ch * 8 + e;
+        const uint64_t wpt = table_weight(sp, tab_p, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
+        const uint64_t r = t == d ? sp.Z : 0;
+        w[e] = wpt > r ? wpt - r : 0;
+      }
+    };
+    f(ld, wt, (uint64_t)0);
+  } else {
+    // the bonus: p of row k itself
+    __syncthreads();
+    auto ld = [=](int ch) { return vp[ch]; };
+    auto wt = [=](const u32x4_t& u, int ch, uint64_t* w) {
+      const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        w[e] = table_weight(sp, tab_p, (wd[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, ch * 8 + e);
+    };
+    f(ld, wt, (uint64_t)0);
+  }
+}
+
+__device__ __forceinline__ void split_range(int nch, int ns, int s, int& lo, int& hi) {
+  const int per = (nch + ns - 1) / ns;
+  lo = min(nch, s * per);
+  hi = min(nch, lo + per);
+}
+
+// Pass 1, grid (ns, B): workgroup (s, b) sums the draw's weights over the s-th of ns
+// contiguous slices of the vocabulary (exact integers, u128 in part[b ns + s]).
+__global__ __launch_bounds__(SP_THREADS) void spec_partial_kernel(
+    const uint16_t* __restrict__ target, const uint16_t* __restrict__ draft,
+    const int32_t* __restrict__ drafts, int k, int V, float inv_temp, uint64_t seed,
+    uint64_t offset_arg, const uint64_t* __restrict__ offset_dev, const RowStat* __restrict__ st_t,
+    const RowStat* __restrict__ st_d, int ns, u128* __restrict__ part) {
+  __shared__ u128 wt128[SP_THREADS / 64];
+  __shared__ uint64_t wt64[SP_THREADS / 64];
+  __shared__ int32_t ok[64];
+  extern __shared__ uint64_t sp_tabs[];   // p's table, then q's when drafts are sampled
+  uint64_t* tab_p = sp_tabs;
+  uint64_t* tab_q = sp_tabs + SP_NBINS;
+  const int s = blockIdx.x, b = blockIdx.y;
+  const uint64_t offset = offset_dev ? *offset_dev : offset_arg;
+  const float c = inv_temp * 1.44269504088896341f;
+  const AcceptPlan pl = accept_plan(target, draft, drafts, k, V, c, seed, offset, st_t, st_d, b, ok);
+  int lo, hi;
+  split_range(V >> 3, ns, s, lo, hi);
+  with_draw(pl, target, draft, k, V, c, st_t, st_d, b, tab_p, tab_q, [&](auto ld, auto wt, auto tag) {
+    using Acc = decltype(tag);
+    Acc* wtot;
+    if constexpr (sizeof(Acc) == 16) wtot = wt128; else wtot = wt64;
+    const Acc tot = draw_totals<Acc, sizeof(Acc) == 16 ? 2 : 4>(lo, hi, ld, wt, wtot);
+    if (threadIdx.x == 0) part[(size_t)b * ns + s] = (u128)tot;
+  });
+}
+
+// Pass 2, grid (B): the slice holding the target, then the token inside it.
+__global__ __launch_bounds__(SP_THREADS) void spec_final_kernel(
+    const uint16_t* __restrict__ target, const uint16_t* __restrict__ draft,
+    const int32_t* __restrict__ drafts, int k, int V, float inv_temp, uint64_t seed,
+    uint64_t offset_arg, const uint64_t* __restrict__ offset_dev, const RowStat* __restrict__ st_t,
+    const RowStat* __restrict__ st_d, int ns, const u128* __restrict__ part,
+    int32_t* __restrict__ n_accepted, int32_t* __restrict__ next_token) {
+  __shared__ u128 wt128[SP_THREADS / 64];
+  __shared__ uint64_t wt64[SP_THREADS / 64];
+  __shared__ int32_t found;
+  __shared__ int32_t ok[64];
+  extern __shared__ uint64_t sp_tabs[];
+  uint64_t* tab_p = sp_tabs;
+  uint64_t* tab_q = sp_tabs + SP_NBINS;
+  const int b = blockIdx.x;
+  const uint64_t offset = offset_dev ? *offset_dev : offset_arg;
+  const float c = inv_temp * 1.44269504088896341f;
+  const AcceptPlan pl = accept_plan(target, draft, drafts, k, V, c, seed, offset, st_t, st_d, b, ok);
+  const RowStat sp = st_t[b * (k + 1) + pl.a];
+  const int nch = V >> 3;
+  u128 R = 0;
+  for (int s = 0; s < ns; ++s) R += part[(size_t)b * ns + s];
   int32_t tok;
-  if (!rej) {
-    const RowStat sp = st_t[b * (k + 1) + k];
+  if (sp.greedy && pl.kind == 0) {
+    tok = sp.argmax;
+  } else if (pl.kind != 0 && R == 0) {
+    // the residual is empty: draw from p itself (whole row, this workgroup)
     build_table(sp, c, tab_p);
     __syncthreads();
-    tok = draw_plain(target + ((size_t)b * (k + 1) + k) * V, sp, tab_p, U, V, wt64, &found);
+    tok = draw_plain(target + ((size_t)b * (k + 1) + pl.a) * V, sp, tab_p, pl.U, V, wt64, &found);
   } else {
-    const RowStat sp = st_t[b * (k + 1) + a];
-    const uint16_t* xp = target + ((size_t)b * (k + 1) + a) * V;
-    int32_t d = drafts[b * k + a];
-    d = d < 0 ? 0 : (d >= V ? V - 1 : d);
-    const int nch = V >> 3, seg = (nch + SP_THREADS / 64 - 1) / (SP_THREADS / 64);
-    const uint4* xp4 = reinterpret_cast<const uint4*>(xp);
-    build_table(sp, c, tab_p);
-    if (draft) {
-      // q a sampled distribution: residual wp Zq - wq Zp in 128 bits
-      const RowStat sq = st_d[b * k + a];
-      const uint4* xq4 = reinterpret_cast<const uint4*>(draft + ((size_t)b * k + a) * V);
-      const uint64_t Zq = sq.Z;
-      build_table(sq, c, tab_q);
-      __syncthreads();
-      const u32x4_t* vp = reinterpret_cast<const u32x4_t*>(xp4);
-      const u32x4_t* vq = reinterpret_cast<const u32x4_t*>(xq4);
-      auto ld = [=](int ch) { return ChunkPair{vp[ch], vq[ch]}; };
-      auto wt = [=](const ChunkPair& r, int ch, u128* w) {
-        const u32x4_t up = r.p, uq = r.q;
-        const uint32_t pw[4] = {up.x, up.y, up.z, up.w}, qw[4] = {uq.x, uq.y, uq.z, uq.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int t = ch * 8 + e;
-          const uint64_t wpt = table_weight(sp, tab_p, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
-          const uint64_t wqt = table_weight(sq, tab_q, (qw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
-          const u128 l = (u128)wpt * Zq, r = (u128)wqt * sp.Z;
-          w[e] = l > r ? l - r : (u128)0;
-        }
-      };
-      const u128 R = draw_totals<u128, 2>(nch, seg, ld, wt, wt128);
-      tok = R == 0 ? draw_plain(xp, sp, tab_p, U, V, wt64, &found)
-                   : draw_find<u128>(nch, seg, ld, wt, wt128, scaled_target(U, R), V, &found);
-    } else {
-      // q one-hot at d: residual wp - [t == d] Zp fits 64 bits
-      __syncthreads();
-      const u32x4_t* vp = reinterpret_cast<const u32x4_t*>(xp4);
-      auto ld = [=](int ch) { return vp[ch]; };
-      auto wt = [=](const u32x4_t& up, int ch, uint64_t* w) {
-        const uint32_t pw[4] = {up.x, up.y, up.z, up.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int t = ch * 8 + e;
-          const uint64_t wpt = table_weight(sp, tab_p, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
-          const uint64_t r = t == d ? sp.Z : 0;
-          w[e] = wpt > r ? wpt - r : 0;
-        }
-      };
-      const uint64_t R = draw_totals<uint64_t, 4>(nch, seg, ld, wt, wt64);
-      tok = R == 0 ? draw_plain(xp, sp, tab_p, U, V, wt64, &found)
-                   : draw_find<uint64_t>(nch, seg, ld, wt, wt64,
-                                         (uint64_t)scaled_target(U, (u128)R), V, &found);
+    // target: floor(U Z / 2^24) for the bonus (Z = the kept mass of p), U R scaled for
+    // a residual; then the slice whose running total passes it
+    const u128 tgt = pl.kind == 0 ? (u128)(((u128)pl.U * sp.Z) >> 24) : scaled_target(pl.U, R);
+    u128 before = 0;
+    int s_hit = ns - 1;
+    for (int s = 0; s < ns; ++s) {
+      const u128 v = part[(size_t)b * ns + s];
+      if (before + v > tgt) { s_hit = s; break; }
+      before += v;
     }
+    int lo, hi;
+    split_range(nch, ns, s_hit, lo, hi);
+    with_draw(pl, target, draft, k, V, c, st_t, st_d, b, tab_p, tab_q, [&](auto ld, auto wt, auto tag) {
+      using Acc = decltype(tag);
+      Acc* wtot;
+      if constexpr (sizeof(Acc) == 16) wtot = wt128; else wtot = wt64;
+      draw_totals<Acc, sizeof(Acc) == 16 ? 2 : 4>(lo, hi, ld, wt, wtot);
+      tok = draw_find<Acc>(lo, hi, ld, wt, wtot, (Acc)(tgt - before), V, &found);
+    });
   }
-  if (tid == 0) {
-    n_accepted[b] = a;
+  if (threadIdx.x == 0) {
+    n_accepted[b] = pl.a;
     next_token[b] = tok;
   }
 }
@@ -703,9 +806,16 @@ static long long stats_bytes(long long rows) {
   return rows * (long long)(sizeof(RowStat) + SP_NSPLIT * sizeof(uint64_t));
 }
 
+constexpr int SP_MAXSLICE = 16;   // vocabulary slices of the acceptance draw
+
+static long long accept_part_offset(int B, int k, int with_draft) {
+  const long long st = stats_bytes((long long)B * (k + 1) + (with_draft ? (long long)B * k : 0));
+  return (st + 15) / 16 * 16;
+}
+
 LOLLM_API long long lollm_spec_workspace_bytes(int B, int k, int with_draft) {
   if (B <= 0 || k < 0) return -1;
-  return stats_bytes((long long)B * (k + 1) + (with_draft ? (long long)B * k : 0));
+  return accept_part_offset(B, k, with_draft) + (long long)B * SP_MAXSLICE * (long long)sizeof(u128);
 }
 
 LOLLM_API long long lollm_sample_workspace_bytes(int rows) {
@@ -736,9 +846,33 @@ LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int
                           part + (size_t)rt * SP_NSPLIT, st);
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(spec_accept_kernel, dim3(B), dim3(SP_THREADS), 0, st, (const uint16_t*)target,
+  // the draw: vocabulary slices summed by B x ns workgroups (about two per CU), then one
+  // workgroup per sequence finds the slice and the token
+  const int ns = std::max(1, std::min(SP_MAXSLICE, (512 + B - 1) / B));
+  u128* apart = (u128*)((char*)workspace + accept_part_offset(B, k, draft != nullptr));
+  // LDS: the weight table of p, and of q when the drafts are sampled (one-hot drafts
+  // need only p's, which leaves room for two workgroups per CU)
+  const size_t tabs = (draft ? 2 : 1) * SP_NBINS * sizeof(uint64_t);
+  static bool lds_set[64] = {};   // per device: the attribute is set on the current device
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return LOLLM_EUNSUPPORTED;
+  if (!lds_set[dev]) {
+    const int mx = 2 * SP_NBINS * (int)sizeof(uint64_t);
+    hipError_t e = hipFuncSetAttribute((const void*)spec_partial_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, mx);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)spec_final_kernel,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, mx);
+    if (e != hipSuccess) return LOLLM_EHIP_BASE + (int)e;
+    lds_set[dev] = true;
+  }
+  hipLaunchKernelGGL(spec_partial_kernel, dim3(ns, B), dim3(SP_THREADS), tabs, st,
+                     (const uint16_t*)target, (const uint16_t*)draft, drafts, k, V, inv_temperature,
+                     seed, offset, offset_dev, st_t, draft ? st_d : nullptr, ns, apart);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(spec_final_kernel, dim3(B), dim3(SP_THREADS), tabs, st, (const uint16_t*)target,
                      (const uint16_t*)draft, drafts, k, V, inv_temperature, seed, offset, offset_dev,
-                     st_t, draft ? st_d : nullptr, n_accepted, next_token);
+                     st_t, draft ? st_d : nullptr, ns, (const u128*)apart, n_accepted, next_token);
   return launch_status();
 }
 
