@@ -214,6 +214,43 @@ def isolated_gdn(B, kd):
             "GBs": round(byt / us / 1e3, 1), "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
 
 
+PEAK_FP32_MFMA_TFLOPS = 157.3
+
+
+def isolated_gdn_prefill(B=16, T=2048):
+    """The chunked GDN prefill layer (conv + gating + chunked delta rule + gated norm)
+    at the e2e prompt shape; compute-bound, so reported against the fp32 matrix peak.
+    FLOPs counted: the chunk algorithm's products per (sequence, v-head, 64-token chunk)
+    -- k.k^T and q.k^T (2 x 64x64x128), W and Tm diag(beta) V (2 x 64x128x64), W S and
+    Q S (2 x 64x128x128), intra V' (64x128x64), K^T V' (128x128x64) -- at 2 flops per
+    multiply-add."""
+    import torch
+    from lollm_amd import ops
+    Hk, Hv, D, K, S = 16, 32, 128, 4, 4
+    C = 2 * Hk * D + Hv * D
+    P = -(-(C + Hv * D + 2 * Hv) // 8) * 8
+    g = torch.Generator(device="cuda")
+    g.manual_seed(6)
+    proj = torch.randn(B, T, P, device="cuda", generator=g).bfloat16()
+    conv_w = (torch.randn(C, K, device="cuda", generator=g) * 0.5).bfloat16()
+    A_log = torch.randn(Hv, device="cuda", generator=g) * 0.5
+    dt_bias = torch.randn(Hv, device="cuda", generator=g) * 0.5
+    norm_w = (1 + 0.1 * torch.randn(D, device="cuda", generator=g)).bfloat16()
+    win = torch.zeros(B, 2 * (K - 1 + S), C, device="cuda").bfloat16()
+    rec = torch.zeros(B, 2 * S, Hv, D, D, device="cuda")
+    zero = torch.zeros(B, dtype=torch.int32, device="cuda")
+    out = torch.empty(B, T, Hv * D, dtype=torch.bfloat16, device="cuda")
+    us = time_fn(lambda: ops.gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, zero, rec, zero,
+                                       True, B, T, Hk, Hv, D, K, 1e-6, out=out, chunked=True), 5)
+    C64 = 64
+    per_chunk = 2 * (2 * C64 * C64 * D + 2 * C64 * D * C64 + 2 * C64 * D * D + C64 * D * C64 + D * D * C64)
+    flops = B * Hv * (-(-T // C64)) * per_chunk
+    tf = flops / us / 1e6
+    return {"B": B, "T": T, "us": round(us, 1), "GFLOP": round(flops / 1e9, 1),
+            "TFLOPs": round(tf, 2), "bound": "mfma", "peak": PEAK_FP32_MFMA_TFLOPS,
+            "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 3)}
+
+
 def isolated_attn():
     import torch
     from lollm_amd import ops
@@ -414,6 +451,7 @@ def main():
         kernels["gdn_verify_isolated"] = [isolated_gdn(B, kd) for B in (1, 8, 32) for kd in (1, 2, 4)]
         kernels["attn_verify_isolated"] = isolated_attn()
         kernels["spec_accept_isolated"] = isolated_sampler()
+        kernels["gdn_prefill_chunked"] = isolated_gdn_prefill()
     cpu = None
     if not args.no_cpu:
         try:
