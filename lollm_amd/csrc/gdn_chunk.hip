@@ -8,54 +8,175 @@
 // written, final K-1 raw inputs in rows 0 .. K-2 of the window half being written).
 //
 // One 256-thread workgroup per (sequence b, v-head h) walks the chunks of 64 tokens in
-// order; the 128 x 128 fp32 state S[key][value] stays in LDS.  Per chunk, with
-// gc = cumsum(g), s = Dk^-0.5 and every product an fp32 MFMA (v_mfma_f32_16x16x4f32:
-// the reference's fp32 arithmetic up to summation order):
+// order.  Per chunk, with gc = cumsum(g) and s = Dk^-0.5:
 //   A  = -(beta_i k_i.k_j) exp(gc_i - gc_j), j < i          (:99-100)
-//   Tm = (I - A)^-1, by the reference's row recurrence (:101-103): one wave, each lane a
-//        column in registers, rows broadcast with readlane
+//   Tm = (I - A)^-1                                          (:101-103)
 //   W  = Tm diag(beta e^gc) K,   V' = Tm diag(beta) V - W S   (:104-105, :113)
 //   O  = diag(s e^gc) Q S + [s (q_i.k_j) exp(gc_i - gc_j)]_{j<=i} V'   (:112-115)
 //   S <- e^gc_63 S + K^T diag(e^(gc_63 - gc)) V'              (:116-117)
+//
+// Work split.  The 128 x 128 fp32 state S[key][value] lives in registers: wave w owns
+// the value columns 32w .. 32w+31 in the 16x16 MFMA accumulator layout (lane (g, r)
+// holds S[16kb + 4g + j][32w + 16u + r]), so V', O and the state update of those
+// columns never leave the wave.  The value-independent matrices (k, k^T, q, v^T, Tm
+// scaled two ways, W, the masked q.k decay) are shared through LDS.
+//
+// Arithmetic.  Products run on the bf16 MFMA (16x16x32).  q, k, v are bf16 conv
+// outputs and enter exactly; an fp32 operand x enters as hi + lo with hi = bf16(x),
+// lo = bf16(x - hi) (16 significant bits), and a product of two fp32 operands takes
+// hi.hi + hi.lo + lo.hi, so every product carries a relative error near 2^-17 against
+// the reference's fp32 arithmetic, accumulated in fp32.  A product whose B operand
+// comes from registers (S, V') contracts in the accumulator's row order: its k slots
+// 8g .. 8g+7 hold rows 32s + 4g .. +3 and 32s + 16 + 4g .. +3, and the A operand is
+// read from LDS in that same order (two 8-byte reads).
+//
+// Tm is solved blockwise in fp32: the four 16 x 16 diagonal blocks by the reference's
+// row recurrence (one lane per column), the off-diagonal blocks by
+// T_ij = T_ii sum_{k=j}^{i-1} A_ik T_kj with fp32 MFMA (16x16x4), while the other three
+// waves form the masked q.k decay.
+//
 // q and k enter the products as their bf16 conv outputs with the L2-norm factors
-// rq_t, rk_t applied as fp32 row scales (the normalised vectors are never rounded),
-// which is the arithmetic of the recurrent kernels, so a prefill and the decode steps
-// after it agree.  Tokens past T in the last chunk enter with q = k = v = 0 and
+// rq_t, rk_t applied as fp32 scales (the normalised vectors are never rounded), which
+// is the arithmetic of the recurrent kernels, so a prefill and the decode steps after
+// it agree.  Tokens past T in the last chunk enter with q = k = v = 0 and
 // beta = g = 0 and change nothing, as the reference's zero padding (:77-80).
 #include "gdn_common.h"
 
 namespace lollm {
 
 constexpr int GC_C = 64;     // tokens per chunk
-constexpr int GC_PB = 136;   // bf16 pitch of the 64 x 128 operand tiles
-constexpr int GC_PS = 132;   // fp32 pitch of the 64 x 128 matrix
-constexpr int GC_PSS = 144;  // fp32 pitch of the state (conflict-free operand reads)
-constexpr int GC_PT = 68;    // fp32 pitch of 64-column matrices
+constexpr int GC_PW = 136;   // bf16 pitch of 128-wide rows
+constexpr int GC_PN = 72;    // bf16 pitch of 64-wide rows
+constexpr int GC_PF = 68;    // fp32 pitch of 64-wide rows
+constexpr int GC_PO = 132;   // fp32 pitch of the output rows
 
 typedef float gc_f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 gc_bf16x8 __attribute__((ext_vector_type(8)));
 
 struct GcSmem {
-  uint16_t kb[GC_C][GC_PB];    // k of the chunk (bf16 conv output)
-  uint16_t qv[GC_C][GC_PB];    // v of the chunk, then q
-  float sm[GL_DK][GC_PSS];     // the state S[key][value]
-  float tm[GC_C][GC_PT];       // raw q (bf16 view) -> A -> Tm -> masked s q.k decay
-  float wm[GC_C][GC_PS];       // W -> V' -> O
+  union {
+    uint16_t kc[GC_C][GC_PW];           // k [t][channel] (conv -> q.k products)
+    uint16_t in[2][GC_C][GC_PN];        // hi, lo of the masked s q.k decay [i][j]
+  } r1;
+  uint16_t kt[GL_DK][GC_PN];            // k^T [channel][t]
+  uint16_t qc[GC_C][GC_PW];             // q [t][channel]
+  uint16_t vt[GL_DK][GC_PN];            // v^T [channel][t]
+  union {
+    struct {
+      float am[GC_C][GC_PF];            // A (strictly lower)
+      float tf[GC_C][GC_PF];            // Tm, lower blocks
+    } s;
+    uint16_t w[2][GC_C][GC_PW];         // hi, lo of -W [t][key]
+  } r2;
+  union {
+    uint16_t tm[4][GC_C][GC_PN];        // hi, lo of Tm diag(rk beta e^gc), of Tm diag(beta)
+    float o[GC_C][GC_PO];               // O (fp32) for the gated norm
+  } r3;
   float gcv[GC_C], egv[GC_C], btv[GC_C], gv[GC_C], rqv[GC_C], rkv[GC_C];
   float fwv[GC_C], f7v[GC_C];  // rk beta e^gc (W), rk e^(gc_63 - gc) (state update)
+  uint16_t cw[GL_CH][4];       // conv weights of the head's q, k, v channels
 };
 static_assert(sizeof(GcSmem) <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ float gc_bf(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
-__device__ __forceinline__ gc_f32x4 gc_mma(float a, float b, gc_f32x4 c) {
+__device__ __forceinline__ gc_f32x4 gc_mma(gc_bf16x8 a, gc_bf16x8 b, gc_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ gc_f32x4 gc_mma4(float a, float b, gc_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ gc_bf16x8 gc_ld8(const uint16_t* p) {
+  return __builtin_bit_cast(gc_bf16x8, *reinterpret_cast<const u32x4_t*>(p));
+}
+
+// k slots 0..3 from p0, 4..7 from p1 (the accumulator row order)
+__device__ __forceinline__ gc_bf16x8 gc_ld44(const uint16_t* p0, const uint16_t* p1) {
+  const uint2 x = *reinterpret_cast<const uint2*>(p0), y = *reinterpret_cast<const uint2*>(p1);
+  return __builtin_bit_cast(gc_bf16x8, u32x4_t{x.x, x.y, y.x, y.y});
+}
+
+// hi/lo bf16 of the 8 values p[0..3], q[0..3]
+__device__ __forceinline__ void gc_split(gc_f32x4 p, gc_f32x4 q, gc_bf16x8& hi, gc_bf16x8& lo) {
+  gc_bf16x8 h, l;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const __bf16 a = (__bf16)p[j], c = (__bf16)q[j];
+    h[j] = a;
+    h[j + 4] = c;
+    l[j] = (__bf16)(p[j] - (float)a);
+    l[j + 4] = (__bf16)(q[j] - (float)c);
+  }
+  hi = h;
+  lo = l;
+}
+
+__device__ __forceinline__ uint16_t gc_bits(__bf16 x) { return __builtin_bit_cast(uint16_t, x); }
+
+__device__ __forceinline__ float gc_rbf(float x) { return (float)(__bf16)x; }   // round to bf16
+
+// 16-lane row sum in every lane of the row (DPP: quad xor 1, xor 2, half-row and row
+// mirrors)
+template <int CTRL> __device__ __forceinline__ float gc_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float gc_row16_sum(float v) {
+  v += gc_dpp<0xB1>(v);
+  v += gc_dpp<0x4E>(v);
+  v += gc_dpp<0x141>(v);
+  v += gc_dpp<0x140>(v);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t gc_pack(float lo, float hi) {
+  return (uint32_t)gc_bits((__bf16)lo) | ((uint32_t)gc_bits((__bf16)hi) << 16);
+}
+
+// projection column of local channel lc (0..127 q, 128..255 k, 256..383 v) of head h
+__device__ __forceinline__ int gc_chan(const GdnLayerArgs& a, int hk, int h, int lc) {
+  return lc < GL_DK ? hk * GL_DK + lc
+                    : (lc < 2 * GL_DK ? a.key_dim + hk * GL_DK + (lc - GL_DK)
+                                      : 2 * a.key_dim + h * GL_DK + (lc - 2 * GL_DK));
+}
+
+// Conv work of a chunk: item n of thread tid = (8-channel vector cv of the 48, 4-token
+// group tq of the 16) with it = tid + 256 n; its 7 input rows (3 history + 4) are
+// loaded ahead of use.  Every load is issued unconditionally and nothing touches the
+// loaded values before the conv uses them, so no wait is placed at the loads and a
+// later wait never drains loads issued after these.  A row past the call is read at
+// row T - 1 instead: it only feeds outputs of tokens past the call, which are zero.
+// (Chunks after the first never reach back into the conv window.)
+constexpr int GC_ITEMS = 3;
+
+__device__ __forceinline__ void gc_prefetch(const uint16_t* projb, long long P, int T, int tc, int tid,
+                                            const int (&c0n)[GC_ITEMS], u32x4_t (&raw)[GC_ITEMS][7]) {
+#pragma unroll
+  for (int n = 0; n < GC_ITEMS; ++n) {
+    const int t4 = tc + 4 * ((tid + 256 * n) / 48);
+#pragma unroll
+    for (int r = 0; r < 7; ++r) {
+      const int t = t4 - 3 + r;
+      raw[n][r] = *reinterpret_cast<const u32x4_t*>(projb + (size_t)(t < T ? t : T - 1) * P + c0n[n]);
+    }
+  }
+}
+
+// bf16 b and a (gating inputs) of token tc + (tid & 63)
+__device__ __forceinline__ void gc_prefetch_ba(const GdnLayerArgs& a, const uint16_t* projb, int h, int tc,
+                                               int tid, uint16_t& braw, uint16_t& araw) {
+  const int t = tc + (tid & (GC_C - 1));
+  const uint16_t* p = projb + (size_t)(t < a.T ? t : a.T - 1) * a.P + a.C + a.value_dim + h;
+  braw = p[0];
+  araw = p[a.Hv];
 }
 
 __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
   __shared__ GcSmem sh;
-  uint16_t (*qraw)[GC_PB] = reinterpret_cast<uint16_t (*)[GC_PB]>(&sh.tm[0][0]);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r16 = lane & 15, kq = lane >> 4;   // MFMA lane coordinates
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;   // MFMA lane coordinates
   const int b = blockIdx.x / a.Hv, h = blockIdx.x % a.Hv;
   const int vpk = a.Hv / a.Hk, hk = h / vpk;
   const bool write_qk = (h % vpk) == 0;
@@ -70,354 +191,537 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
   const size_t win_b = (size_t)b * 2 * a.W;
   const float qscale = rsqrtf((float)GL_DK);
   const float a_log = a.A_log[h], dtb = a.dt_bias[h];
+  const int vcol = 32 * wave;   // first value column of this wave
 
-  auto gchan = [&](int lc) {
-    return lc < GL_DK ? hk * GL_DK + lc
-                      : (lc < 2 * GL_DK ? a.key_dim + hk * GL_DK + (lc - GL_DK)
-                                        : 2 * a.key_dim + h * GL_DK + (lc - 2 * GL_DK));
-  };
 
-  // ---- initial state ----
+  // ---- initial state: this wave's 32 value columns, accumulator layout ----
+  gc_f32x4 st[8][2];
   {
     const float* s0 = a.rec + ((size_t)(b * 2 * a.S + slot) * a.Hv + h) * SS;
-    for (int i = tid; i < GL_DK * GL_DK / 4; i += 256) {
-      const int row = i / (GL_DK / 4), c4 = (i % (GL_DK / 4)) * 4;
-      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (!a.fresh) f = *reinterpret_cast<const float4*>(s0 + (size_t)row * GL_DK + c4);
-      sh.sm[row][c4] = f.x; sh.sm[row][c4 + 1] = f.y; sh.sm[row][c4 + 2] = f.z; sh.sm[row][c4 + 3] = f.w;
-    }
+    const float keep = a.fresh ? 0.f : 1.f;   // a fresh sequence starts from S = 0
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          st[kb][u][j] = keep * s0[(size_t)(16 * kb + 4 * g4 + j) * GL_DK + vcol + 16 * u + r16];
   }
 
-  for (int t0 = 0; t0 < a.T; t0 += GC_C) {
-    // ================= A. conv + SiLU =================
-    // thread = (8-channel vector cv of the 48, 16-token group tg of the 4); its 19 input
-    // rows (3 history + 16) are loaded as 16-byte vectors before any use
-    __syncthreads();   // chunk buffers free
-    if (tid < 48 * 4) {
-      const int cv = tid % 48, tg = tid / 48, lc0 = cv * 8, c0 = gchan(lc0);
-      const int tb = t0 + 16 * tg;            // first token of the group
-      u32x4_t raw[19];
+  int c0n[GC_ITEMS];   // projection column of each conv item's first channel
 #pragma unroll
-      for (int r = 0; r < 19; ++r) {
-        const int t = tb - 3 + r;
-        u32x4_t v = {0u, 0u, 0u, 0u};
-        if (t < 0) v = *reinterpret_cast<const u32x4_t*>(a.win + (win_b + off + 3 + t) * a.C + c0);
-        else if (t < a.T) v = *reinterpret_cast<const u32x4_t*>(a.proj + ((size_t)b * a.T + t) * a.P + c0);
-        raw[r] = v;
-      }
+  for (int n = 0; n < GC_ITEMS; ++n) c0n[n] = gc_chan(a, hk, h, 8 * ((tid + 256 * n) % 48));
+  const uint16_t* projb = a.proj + (size_t)b * a.T * a.P;   // this sequence's projection rows
+  u32x4_t raw[GC_ITEMS][7];
+  uint16_t braw, araw;
+  // the first chunk's history rows come from the committed conv window
+#pragma unroll
+  for (int n = 0; n < GC_ITEMS; ++n) {
+    const int t4 = 4 * ((tid + 256 * n) / 48);
+#pragma unroll
+    for (int r = 0; r < 7; ++r) {
+      const int t = t4 - 3 + r;
+      const uint16_t* src = t < 0 ? a.win + (win_b + off + 3 + t) * a.C + c0n[n]
+                                  : projb + (size_t)(t < a.T ? t : a.T - 1) * a.P + c0n[n];
+      raw[n][r] = *reinterpret_cast<const u32x4_t*>(src);
+    }
+  }
+  gc_prefetch_ba(a, projb, h, 0, tid, braw, araw);
+  const uint4 nwreg = *reinterpret_cast<const uint4*>(a.norm_w + (tid & 15) * 8);   // gated-norm weight
+  if (tid < GL_CH / 2)   // two channels (16 bytes) per thread
+    *reinterpret_cast<u32x4_t*>(&sh.cw[2 * tid][0]) =
+        *reinterpret_cast<const u32x4_t*>(a.conv_w + (size_t)gc_chan(a, hk, h, 2 * tid) * 4);
+  __syncthreads();
+
+  for (int t0 = 0; t0 < a.T; t0 += GC_C) {
+    // lane coordinates re-derived per chunk from an opaque copy of the thread index, so
+    // the compiler recomputes LDS addresses in the loop instead of holding (and
+    // spilling) every one of them across it
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, r16 = lane & 15, g4 = lane >> 4;
+    // ================= conv + SiLU, L2-norm factors; beta, g, cumsum(g) =================
+    // (every reader of the chunk buffers passed the barrier before the previous norm)
+#pragma unroll
+    for (int n = 0; n < GC_ITEMS; ++n) {
+      const int it = tid + 256 * n, cv = it % 48, tq = it / 48;
+      const int nvalid = a.T - (t0 + 4 * tq);   // tokens of the group inside the call
+      const u32x4_t* cwp = reinterpret_cast<const u32x4_t*>(&sh.cw[8 * cv][0]);
       float w[8][4];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const uint2 wv = *reinterpret_cast<const uint2*>(a.conv_w + (size_t)(c0 + e) * 4);
-        w[e][0] = __uint_as_float(wv.x << 16); w[e][1] = __uint_as_float(wv.x & 0xffff0000u);
-        w[e][2] = __uint_as_float(wv.y << 16); w[e][3] = __uint_as_float(wv.y & 0xffff0000u);
+        const u32x4_t cw = cwp[e >> 1];
+        const uint32_t lo = cw[(e & 1) * 2], hi = cw[(e & 1) * 2 + 1];
+        w[e][0] = __uint_as_float(lo << 16); w[e][1] = __uint_as_float(lo & 0xffff0000u);
+        w[e][2] = __uint_as_float(hi << 16); w[e][3] = __uint_as_float(hi & 0xffff0000u);
       }
-      uint16_t* dst = cv < 16 ? &qraw[0][0] : (cv < 32 ? &sh.kb[0][0] : &sh.qv[0][0]);
-      const int col = (cv % 16) * 8;
+      uint32_t pk[4][4];   // token r: bf16 pairs (channels 2p, 2p + 1)
+      float ssq[4];        // token r: sum of squares over the 8 channels
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        uint32_t od[4];
+      for (int r = 0; r < 4; ++r) {
+        ssq[r] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; e += 2) {
+        for (int p = 0; p < 4; ++p) {
           float o2[2];
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            const int ee = e + u;
+            const int ee = 2 * p + u;
             float acc = 0.f;
 #pragma unroll
             for (int tau = 0; tau < 4; ++tau) {
-              const uint32_t wd = raw[r + tau][ee >> 1];
-              acc = fmaf(w[ee][tau], __uint_as_float(ee & 1 ? wd & 0xffff0000u : wd << 16), acc);
+              const uint32_t wd = raw[n][r + tau][p];
+              acc = fmaf(w[ee][tau], __uint_as_float(u ? wd & 0xffff0000u : wd << 16), acc);
             }
-            o2[u] = tb + r < a.T ? round_bf16(silu_g(round_bf16(acc))) : 0.f;
+            const float sv = silu_g(gc_rbf(acc));
+            o2[u] = r < nvalid ? sv : 0.f;
           }
-          od[e >> 1] = f32_to_bf16(o2[0]) | ((uint32_t)f32_to_bf16(o2[1]) << 16);
+          pk[r][p] = gc_pack(o2[0], o2[1]);
+          const float x0 = __uint_as_float(pk[r][p] << 16), x1 = __uint_as_float(pk[r][p] & 0xffff0000u);
+          ssq[r] = fmaf(x0, x0, ssq[r]);
+          ssq[r] = fmaf(x1, x1, ssq[r]);
         }
-        *reinterpret_cast<u32x4_t*>(dst + (16 * tg + r) * GC_PB + col) = u32x4_t{od[0], od[1], od[2], od[3]};
       }
-    }
-    if (tid < GC_C) {
-      const int t = t0 + tid;
-      float gg = 0.f, bb = 0.f;
-      if (t < a.T) {
-        const size_t base = ((size_t)b * a.T + t) * a.P + a.C + a.value_dim;
-        const float braw = gc_bf(a.proj[base + h]);
-        const float araw = gc_bf(a.proj[base + a.Hv + h]);
-        gg = -__expf(a_log) * softplus_g(araw + dtb);
-        bb = round_bf16(1.f / (1.f + __expf(-braw)));
-      }
-      sh.gv[tid] = gg;
-      sh.btv[tid] = bb;
-    }
-    __syncthreads();
-    // L2-norm factors of q and k per token (4 threads x 32 channels); q stays in
-    // registers until V is consumed
-    uint32_t qreg[16];
-    {
-      const int tok = tid >> 2, part = tid & 3;
-      float sq = 0.f, sk = 0.f;
+      // the 16 lanes of a DPP row hold the 16 channel vectors of one kind (q, k or v)
+      // for the same 4 tokens: the row sum is the squared norm over 128 channels
 #pragma unroll
-      for (int e = 0; e < 32; e += 2) {
-        const uint16_t q0 = qraw[tok][part * 32 + e], q1 = qraw[tok][part * 32 + e + 1];
-        const float xq0 = gc_bf(q0), xq1 = gc_bf(q1);
-        const float xk0 = gc_bf(sh.kb[tok][part * 32 + e]), xk1 = gc_bf(sh.kb[tok][part * 32 + e + 1]);
-        sq = fmaf(xq0, xq0, sq); sq = fmaf(xq1, xq1, sq);
-        sk = fmaf(xk0, xk0, sk); sk = fmaf(xk1, xk1, sk);
-        qreg[e / 2] = (uint32_t)q0 | ((uint32_t)q1 << 16);
+      for (int r = 0; r < 4; ++r) ssq[r] = gc_row16_sum(ssq[r]);
+      const int kind = cv >> 4, col = (cv & 15) * 8;   // 0 q, 1 k, 2 v
+      if (kind < 2 && (cv & 15) == 0) {
+        float* dstv = kind == 0 ? sh.rqv : sh.rkv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dstv[4 * tq + r] = rsqrtf(ssq[r] + 1e-6f);
       }
-      sq += __shfl_xor(sq, 1, 64); sq += __shfl_xor(sq, 2, 64);
-      sk += __shfl_xor(sk, 1, 64); sk += __shfl_xor(sk, 2, 64);
-      if (part == 0) {
-        sh.rqv[tok] = rsqrtf(sq + 1e-6f);
-        sh.rkv[tok] = rsqrtf(sk + 1e-6f);
+      if (kind < 2) {
+        uint16_t* dst = kind == 0 ? &sh.qc[0][0] : &sh.r1.kc[0][0];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<u32x4_t*>(dst + (4 * tq + r) * GC_PW + col) =
+              u32x4_t{pk[r][0], pk[r][1], pk[r][2], pk[r][3]};
+      }
+      if (kind > 0) {
+        uint16_t* dst = kind == 1 ? &sh.kt[0][0] : &sh.vt[0][0];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          uint32_t c[2];
+#pragma unroll
+          for (int r2 = 0; r2 < 2; ++r2) {
+            const uint32_t x0 = pk[2 * r2][e >> 1], x1 = pk[2 * r2 + 1][e >> 1];
+            c[r2] = e & 1 ? (x0 >> 16) | (x1 & 0xffff0000u) : (x0 & 0xffffu) | (x1 << 16);
+          }
+          *reinterpret_cast<uint2*>(dst + (col + e) * GC_PN + 4 * tq) = make_uint2(c[0], c[1]);
+        }
       }
     }
-    if (tid == 0) {
-      float run = 0.f;
-      for (int i = 0; i < GC_C; ++i) {
-        run += sh.gv[i];
-        sh.gcv[i] = run;
+    if (wave == 0) {   // lane = token
+      float gg = 0.f, bb = 0.f;
+      if (t0 + lane < a.T) {
+        gg = -__expf(a_log) * softplus_g(gc_bf(araw) + dtb);
+        bb = round_bf16(1.f / (1.f + __expf(-gc_bf(braw))));
       }
+      sh.gv[lane] = gg;
+      sh.btv[lane] = bb;
+      __builtin_amdgcn_wave_barrier();
+      if (lane == 0) {   // cumsum in token order, as the reference's torch.cumsum
+        float run = 0.f;
+#pragma unroll
+        for (int i = 0; i < GC_C; ++i) {
+          run += sh.gv[i];
+          sh.gcv[i] = run;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      sh.egv[lane] = expf(sh.gcv[lane]);
+    }
+    // z of this chunk for the gated norm (rows 16 n + tid / 16, 8 columns), issued after
+    // the conv's loads were consumed and in flight until the end of the chunk
+    uint4 zreg[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const int t = t0 + 16 * n + (tid >> 4);
+      zreg[n] = *reinterpret_cast<const uint4*>(projb + (size_t)(t < a.T ? t : a.T - 1) * a.P + a.C +
+                                                (size_t)h * GL_DK + (tid & 15) * 8);
     }
     __syncthreads();
     if (tid < GC_C) {
-      const float eg = expf(sh.gcv[tid]);
-      sh.egv[tid] = eg;
-      sh.fwv[tid] = sh.rkv[tid] * sh.btv[tid] * eg;
+      sh.fwv[tid] = sh.rkv[tid] * sh.btv[tid] * sh.egv[tid];
       sh.f7v[tid] = sh.rkv[tid] * expf(sh.gcv[GC_C - 1] - sh.gcv[tid]);
     }
-    // ================= B1. A = -(beta_i k_i.k_j) exp(gc_i - gc_j), j < i =================
-    {
-      const int ti = wave;
-      gc_f32x4 acc[4];
+    // ================= A = -(beta_i k_i.k_j) exp(gc_i - gc_j), j < i =================
+    // the 10 lower 16 x 16 tiles (ti >= tj), dealt to the waves
 #pragma unroll
-      for (int tj = 0; tj < 4; ++tj) acc[tj] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int k0 = 0; k0 < GL_DK; k0 += 4) {
-        const float av = gc_bf(sh.kb[16 * ti + r16][k0 + kq]);
+    for (int n = 0; n < 3; ++n) {
+      const int q = wave + 4 * n;
+      if (q < 10) {
+        const int ti = q < 1 ? 0 : (q < 3 ? 1 : (q < 6 ? 2 : 3));
+        const int tj = q - ti * (ti + 1) / 2;
+        gc_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
-          if (tj <= ti) acc[tj] = gc_mma(av, gc_bf(sh.kb[16 * tj + r16][k0 + kq]), acc[tj]);
+        for (int s = 0; s < 4; ++s)
+          acc = gc_mma(gc_ld8(&sh.r1.kc[16 * ti + r16][32 * s + 8 * g4]),
+                       gc_ld8(&sh.r1.kc[16 * tj + r16][32 * s + 8 * g4]), acc);
+        const int i0 = 16 * ti + 4 * g4, jj = 16 * tj + r16;
+        const float4 bt = *reinterpret_cast<const float4*>(&sh.btv[i0]);
+        const float4 rk = *reinterpret_cast<const float4*>(&sh.rkv[i0]);
+        const float4 gi = *reinterpret_cast<const float4*>(&sh.gcv[i0]);
+        const float bta[4] = {bt.x, bt.y, bt.z, bt.w}, rka[4] = {rk.x, rk.y, rk.z, rk.w};
+        const float gia[4] = {gi.x, gi.y, gi.z, gi.w};
+        const float rkj = sh.rkv[jj], gj = sh.gcv[jj];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          sh.r2.s.am[i0 + j][jj] = jj < i0 + j ? -bta[j] * (acc[j] * rka[j] * rkj) * __expf(gia[j] - gj) : 0.f;
       }
-#pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = 16 * ti + 4 * kq + j, jj = 16 * tj + r16;
-          sh.tm[i][jj] = jj < i ? -sh.btv[i] * (acc[tj][j] * sh.rkv[i] * sh.rkv[jj]) * expf(sh.gcv[i] - sh.gcv[jj]) : 0.f;
-        }
     }
     __syncthreads();
-    // ================= B2. Tm = (I - A)^-1 (wave 0) =================
+    // ======== Tm = (I - A)^-1 (wave 0) | masked s q.k decay (waves 1..3) ========
+    gc_f32x4 qk[4];   // this wave's q.k decay tiles, written after the barrier
     if (wave == 0) {
-      // lane j holds column j; row i's original entries (still in LDS until the end)
-      // are read as broadcasts, four at a time
-      float col[GC_C];
+      // diagonal blocks: lane = 16 blk + column; rows broadcast from LDS per block
+      {
+        const int base = 16 * (lane >> 4), c = lane & 15;
+        float col[16];
 #pragma unroll
-      for (int m = 0; m < GC_C; ++m) col[m] = sh.tm[m][lane];
+        for (int m = 0; m < 16; ++m) col[m] = sh.r2.s.am[base + m][base + c];
 #pragma unroll
-      for (int i = 1; i < GC_C; ++i) {
-        float acc = 0.f;
+        for (int i = 1; i < 16; ++i) {
+          float acc = 0.f;
 #pragma unroll
-        for (int m4 = 0; m4 < i; m4 += 4) {
-          const float4 rowv = *reinterpret_cast<const float4*>(&sh.tm[i][m4]);
-          const float rv[4] = {rowv.x, rowv.y, rowv.z, rowv.w};
+          for (int m4 = 0; m4 < i; m4 += 4) {
+            const float4 rowv = *reinterpret_cast<const float4*>(&sh.r2.s.am[base + i][base + m4]);
+            const float rv[4] = {rowv.x, rowv.y, rowv.z, rowv.w};
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
-            if (m4 + u < i) acc = fmaf(rv[u], col[m4 + u], acc);
+            for (int u = 0; u < 4; ++u)
+              if (m4 + u < i) acc = fmaf(rv[u], col[m4 + u], acc);
+          }
+          col[i] += acc;
         }
-        col[i] += acc;
+#pragma unroll
+        for (int m = 0; m < 16; ++m) sh.r2.s.tf[base + m][base + c] = col[m] + (m == c ? 1.f : 0.f);
       }
+      // off-diagonal blocks by block diagonals: T_ij = T_ii sum_{k=j}^{i-1} A_ik T_kj
 #pragma unroll
-      for (int m = 0; m < GC_C; ++m) sh.tm[m][lane] = col[m] + (m == lane ? 1.f : 0.f);
-    }
-    __syncthreads();
-    // ================= B3/B4. W and V' for this wave's 16 rows =================
-    // k outer, the 8 column tiles inner: each a operand is loaded once per k step
-    const int rw = 16 * wave;          // first row of this wave's row tile
-    const int nkb = wave + 1;          // 16-wide k blocks below the diagonal (Tm is lower triangular)
-    gc_f32x4 vn[8];
-    {
-      gc_f32x4 acc[8];
+      for (int q = 0; q < 6; ++q) {
+        const int bi = q < 3 ? q + 1 : (q < 5 ? q - 1 : 3);
+        const int bj = q < 3 ? q : (q < 5 ? q - 3 : 0);
+        __builtin_amdgcn_wave_barrier();
+        gc_f32x4 p = {0.f, 0.f, 0.f, 0.f};
+        for (int kb = bj; kb < bi; ++kb)
 #pragma unroll
-      for (int tc = 0; tc < 8; ++tc) acc[tc] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int kb16 = 0; kb16 < nkb; ++kb16) {
+          for (int s = 0; s < 4; ++s)
+            p = gc_mma4(sh.r2.s.am[16 * bi + r16][16 * kb + 4 * s + g4],
+                        sh.r2.s.tf[16 * kb + 4 * s + g4][16 * bj + r16], p);
+        gc_f32x4 t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k4 = 0; k4 < 16; k4 += 4) {
-          const int kk = 16 * kb16 + k4 + kq;
-          const float av = sh.tm[rw + r16][kk], f = sh.fwv[kk];
+        for (int s = 0; s < 4; ++s) t = gc_mma4(sh.r2.s.tf[16 * bi + r16][16 * bi + 4 * g4 + s], p[s], t);
 #pragma unroll
-          for (int tc = 0; tc < 8; ++tc) acc[tc] = gc_mma(av, gc_bf(sh.kb[kk][16 * tc + r16]) * f, acc[tc]);
-        }
+        for (int j = 0; j < 4; ++j) sh.r2.s.tf[16 * bi + 4 * g4 + j][16 * bj + r16] = t[j];
       }
+    } else {
+      // tiles (ti >= tj) of (q_i . k_j): wave 1 takes 0, 3, 6, 9; wave 2 1, 4, 7; wave 3 2, 5, 8
 #pragma unroll
-      for (int tc = 0; tc < 8; ++tc)
+      for (int n = 0; n < 4; ++n) {
+        const int q = wave - 1 + 3 * n;
+        qk[n] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
+        if (q < 10) {
+          const int ti = q < 1 ? 0 : (q < 3 ? 1 : (q < 6 ? 2 : 3));
+          const int tj = q - ti * (ti + 1) / 2;
+          gc_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sh.wm[rw + 4 * kq + j][16 * tc + r16] = acc[tc][j];
-      // V' = Tm diag(beta) V - W S, one accumulator per tile (W S enters with -S)
+          for (int s = 0; s < 4; ++s)
+            acc = gc_mma(gc_ld8(&sh.qc[16 * ti + r16][32 * s + 8 * g4]),
+                         gc_ld8(&sh.r1.kc[16 * tj + r16][32 * s + 8 * g4]), acc);
+          const int i0 = 16 * ti + 4 * g4, jj = 16 * tj + r16;
+          const float4 rq = *reinterpret_cast<const float4*>(&sh.rqv[i0]);
+          const float4 gi = *reinterpret_cast<const float4*>(&sh.gcv[i0]);
+          const float rqa[4] = {rq.x, rq.y, rq.z, rq.w}, gia[4] = {gi.x, gi.y, gi.z, gi.w};
+          const float rkj = sh.rkv[jj], gj = sh.gcv[jj];
 #pragma unroll
-      for (int tc = 0; tc < 8; ++tc) vn[tc] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int kb16 = 0; kb16 < nkb; ++kb16) {
-#pragma unroll
-        for (int k4 = 0; k4 < 16; k4 += 4) {
-          const int kk = 16 * kb16 + k4 + kq;
-          const float av = sh.tm[rw + r16][kk], f = sh.btv[kk];
-#pragma unroll
-          for (int tc = 0; tc < 8; ++tc) vn[tc] = gc_mma(av, gc_bf(sh.qv[kk][16 * tc + r16]) * f, vn[tc]);
-        }
-      }
-#pragma unroll 4
-      for (int k0 = 0; k0 < GL_DK; k0 += 4) {
-        const float av = sh.wm[rw + r16][k0 + kq];
-#pragma unroll
-        for (int tc = 0; tc < 8; ++tc) vn[tc] = gc_mma(av, -sh.sm[k0 + kq][16 * tc + r16], vn[tc]);
-      }
-    }
-    __syncthreads();   // every wave done with V (qv) and W
-#pragma unroll
-    for (int tc = 0; tc < 8; ++tc)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sh.wm[rw + 4 * kq + j][16 * tc + r16] = vn[tc][j];
-    {
-      const int tok = tid >> 2, part = tid & 3;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        sh.qv[tok][part * 32 + 2 * e] = (uint16_t)(qreg[e] & 0xffffu);
-        sh.qv[tok][part * 32 + 2 * e + 1] = (uint16_t)(qreg[e] >> 16);
-      }
-    }
-    __syncthreads();
-    // ================= B5. masked s q.k decay (this wave's rows) =================
-    {
-      gc_f32x4 acc[4];
-#pragma unroll
-      for (int tj = 0; tj < 4; ++tj) acc[tj] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int k0 = 0; k0 < GL_DK; k0 += 4) {
-        const float av = gc_bf(sh.qv[rw + r16][k0 + kq]);
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
-          if (tj <= wave) acc[tj] = gc_mma(av, gc_bf(sh.kb[16 * tj + r16][k0 + kq]), acc[tj]);
-      }
-#pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = rw + 4 * kq + j, jj = 16 * tj + r16;
-          sh.tm[i][jj] = jj <= i ? (acc[tj][j] * sh.rqv[i] * sh.rkv[jj]) * qscale * expf(sh.gcv[i] - sh.gcv[jj]) : 0.f;
-        }
-    }
-    // ================= B6. O = diag(s e^gc) Q S + intra V' =================
-    // the row scale rq s e^gc rides on the a operand (one row per lane)
-    gc_f32x4 ov[8];
-    {
-      const int ir = rw + r16;
-      const float rs = sh.rqv[ir] * qscale * sh.egv[ir];
-#pragma unroll
-      for (int tc = 0; tc < 8; ++tc) ov[tc] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int k0 = 0; k0 < GL_DK; k0 += 4) {
-        const float av = gc_bf(sh.qv[ir][k0 + kq]) * rs;
-#pragma unroll
-        for (int tc = 0; tc < 8; ++tc) ov[tc] = gc_mma(av, sh.sm[k0 + kq][16 * tc + r16], ov[tc]);
-      }
-      for (int kb16 = 0; kb16 < nkb; ++kb16) {
-#pragma unroll
-        for (int k4 = 0; k4 < 16; k4 += 4) {
-          const int kk = 16 * kb16 + k4 + kq;
-          const float av = sh.tm[ir][kk];
-#pragma unroll
-          for (int tc = 0; tc < 8; ++tc) ov[tc] = gc_mma(av, sh.wm[kk][16 * tc + r16], ov[tc]);
+          for (int j = 0; j < 4; ++j)
+            qk[n][j] = jj <= i0 + j ? (acc[j] * rqa[j] * rkj) * qscale * __expf(gia[j] - gj) : 0.f;
         }
       }
     }
-    __syncthreads();   // every wave done reading S
-    // ================= B7. S <- e^gc_63 S + K^T diag(e^(gc_63 - gc)) V' =================
-    // this wave's 32 key rows x 128 value columns: 2 x 8 tiles, t outer
-    {
-      const float elast = sh.egv[GC_C - 1];
-      gc_f32x4 acc[2][8];
+    __syncthreads();   // A, k (row layout) consumed; Tm complete
+    if (wave > 0) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int tc = 0; tc < 8; ++tc) acc[u][tc] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-      for (int k0 = 0; k0 < GC_C; k0 += 4) {
-        const int t = k0 + kq;
-        const float f = sh.f7v[t];
-        const float a0 = gc_bf(sh.kb[t][32 * wave + r16]), a1 = gc_bf(sh.kb[t][32 * wave + 16 + r16]);
-#pragma unroll
-        for (int tc = 0; tc < 8; ++tc) {
-          const float bv = sh.wm[t][16 * tc + r16] * f;
-          acc[0][tc] = gc_mma(a0, bv, acc[0][tc]);
-          acc[1][tc] = gc_mma(a1, bv, acc[1][tc]);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int tc = 0; tc < 8; ++tc)
+      for (int n = 0; n < 4; ++n) {
+        const int q = wave - 1 + 3 * n;
+        if (q < 10) {
+          const int ti = q < 1 ? 0 : (q < 3 ? 1 : (q < 6 ? 2 : 3));
+          const int tj = q - ti * (ti + 1) / 2;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            float& sv = sh.sm[32 * wave + 16 * u + 4 * kq + j][16 * tc + r16];
-            sv = fmaf(elast, sv, acc[u][tc][j]);
+            const __bf16 hi = (__bf16)qk[n][j];
+            sh.r1.in[0][16 * ti + 4 * g4 + j][16 * tj + r16] = gc_bits(hi);
+            sh.r1.in[1][16 * ti + 4 * g4 + j][16 * tj + r16] = gc_bits((__bf16)(qk[n][j] - (float)hi));
           }
+        }
+      }
+      // upper tiles (0, 1) and (2, 3) fall inside the 32-wide k steps of the O product
+      if (wave == 1) {
+        const int tr = lane < 32 ? 0 : 2, rr = (lane & 31) >> 1, half = lane & 1;
+        const u32x4_t z = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          *reinterpret_cast<u32x4_t*>(&sh.r1.in[p][16 * tr + rr][16 * (tr + 1) + 8 * half]) = z;
+        }
+      }
     }
-    __syncthreads();   // every wave done reading V'
+    // Tm diag(rk beta e^gc) and Tm diag(beta), hi / lo (thread = row, 16 columns)
+    {
+      const int i = tid >> 2, cb = tid & 3, c0 = 16 * cb;
+      const bool live = cb <= (i >> 4);
+      float tv[16];
 #pragma unroll
-    for (int tc = 0; tc < 8; ++tc)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sh.wm[rw + 4 * kq + j][16 * tc + r16] = ov[tc][j];
-    __syncthreads();
-    // ================= B8. gated RMSNorm, 16 threads per token, 8 columns each =================
-    for (int tb = 0; tb < GC_C; tb += 16) {
-      const int i = tb + (tid >> 4), part = tid & 15, t = t0 + i;
-      float ovs[8], ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        ovs[e] = round_bf16(sh.wm[i][part * 8 + e]);   // the core output is a bf16 tensor
-        ss += ovs[e] * ovs[e];
+      for (int c4 = 0; c4 < 16; c4 += 4) {
+        const float4 f = live ? *reinterpret_cast<const float4*>(&sh.r2.s.tf[i][c0 + c4])
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+        tv[c4] = f.x; tv[c4 + 1] = f.y; tv[c4 + 2] = f.z; tv[c4 + 3] = f.w;
       }
 #pragma unroll
-      for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
-      if (t < a.T) {
-        const float rr = rsqrtf(ss / (float)GL_DK + a.eps);
-        const size_t zb = ((size_t)b * a.T + t) * a.P + a.C + (size_t)h * GL_DK + part * 8;
-        const uint4 zu = *reinterpret_cast<const uint4*>(a.proj + zb);
-        const uint4 wu = *reinterpret_cast<const uint4*>(a.norm_w + part * 8);
-        const uint32_t zd[4] = {zu.x, zu.y, zu.z, zu.w}, wd[4] = {wu.x, wu.y, wu.z, wu.w};
-        uint32_t od[4];
+      for (int m = 0; m < 2; ++m) {
+        const float* f = m == 0 ? sh.fwv : sh.btv;
 #pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          float y2[2];
+        for (int c8 = 0; c8 < 16; c8 += 8) {
+          const gc_f32x4 fa = *reinterpret_cast<const gc_f32x4*>(f + c0 + c8);
+          const gc_f32x4 fb = *reinterpret_cast<const gc_f32x4*>(f + c0 + c8 + 4);
+          gc_f32x4 p, q;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            p[j] = tv[c8 + j] * fa[j];
+            q[j] = tv[c8 + 4 + j] * fb[j];
+          }
+          gc_bf16x8 hi, lo;
+          gc_split(p, q, hi, lo);
+          *reinterpret_cast<gc_bf16x8*>(&sh.r3.tm[2 * m][i][c0 + c8]) = hi;
+          *reinterpret_cast<gc_bf16x8*>(&sh.r3.tm[2 * m + 1][i][c0 + c8]) = lo;
+        }
+      }
+    }
+    __syncthreads();
+    // ================= W^T = K^T (Tm diag(rk beta e^gc))^T, stored as -W =================
+    // wave w: key blocks 2w, 2w + 1 x the 4 token blocks (k steps limited by Tm's triangle)
+    {
+      gc_f32x4 acc[2][4];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) acc[c][ib] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int s = 0; s <= (ib >> 1); ++s) {
+          const gc_bf16x8 bh = gc_ld8(&sh.r3.tm[0][16 * ib + r16][32 * s + 8 * g4]);
+          const gc_bf16x8 bl = gc_ld8(&sh.r3.tm[1][16 * ib + r16][32 * s + 8 * g4]);
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const gc_bf16x8 av = gc_ld8(&sh.kt[32 * wave + 16 * c + r16][32 * s + 8 * g4]);
+            acc[c][ib] = gc_mma(av, bh, acc[c][ib]);
+            acc[c][ib] = gc_mma(av, bl, acc[c][ib]);
+          }
+        }
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) {
+          uint16_t hb[4], lb[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float x = -acc[c][ib][j];
+            const __bf16 hi = (__bf16)x;
+            hb[j] = gc_bits(hi);
+            lb[j] = gc_bits((__bf16)(x - (float)hi));
+          }
+          const int i = 16 * ib + r16, k0 = 32 * wave + 16 * c + 4 * g4;
+          *reinterpret_cast<uint2*>(&sh.r2.w[0][i][k0]) =
+              make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
+          *reinterpret_cast<uint2*>(&sh.r2.w[1][i][k0]) =
+              make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
+        }
+    }
+    __syncthreads();
+    // ================= V' = Tm diag(beta) V - W S (this wave's value columns) =================
+    gc_bf16x8 sth[4][2], stl[4][2];   // hi / lo of S as B operands, k-step s = keys 32s .. 32s+31
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) gc_split(st[2 * s][u], st[2 * s + 1][u], sth[s][u], stl[s][u]);
+    gc_f32x4 vn[4][2];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) vn[tb][u] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
+    {
+      gc_bf16x8 vb[2][2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) vb[s][u] = gc_ld8(&sh.vt[vcol + 16 * u + r16][32 * s + 8 * g4]);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int s = 0; s <= (tb >> 1); ++s) {
+          const gc_bf16x8 ah = gc_ld8(&sh.r3.tm[2][16 * tb + r16][32 * s + 8 * g4]);
+          const gc_bf16x8 al = gc_ld8(&sh.r3.tm[3][16 * tb + r16][32 * s + 8 * g4]);
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            const int ee = e + u;
-            const float z = __uint_as_float(ee & 1 ? zd[ee >> 1] & 0xffff0000u : zd[ee >> 1] << 16);
-            const float w = __uint_as_float(ee & 1 ? wd[ee >> 1] & 0xffff0000u : wd[ee >> 1] << 16);
-            const float hn = round_bf16(ovs[ee] * rr);
-            y2[u] = round_bf16(w * hn) * silu_g(z);
+            vn[tb][u] = gc_mma(ah, vb[s][u], vn[tb][u]);
+            vn[tb][u] = gc_mma(al, vb[s][u], vn[tb][u]);
           }
-          od[e >> 1] = f32_to_bf16(y2[0]) | ((uint32_t)f32_to_bf16(y2[1]) << 16);
         }
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const uint16_t* rh = &sh.r2.w[0][16 * tb + r16][32 * s + 4 * g4];
+          const uint16_t* rl = &sh.r2.w[1][16 * tb + r16][32 * s + 4 * g4];
+          const gc_bf16x8 ah = gc_ld44(rh, rh + 16), al = gc_ld44(rl, rl + 16);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            vn[tb][u] = gc_mma(ah, sth[s][u], vn[tb][u]);
+            vn[tb][u] = gc_mma(ah, stl[s][u], vn[tb][u]);
+            vn[tb][u] = gc_mma(al, sth[s][u], vn[tb][u]);
+          }
+        }
+    }
+    // V' and diag(rk e^(gc_63 - gc)) V' as B operands over tokens (k step s2 = tokens
+    // 32 s2 .. 32 s2 + 31, accumulator row order)
+    gc_bf16x8 vph[2][2], vpl[2][2], vqh[2][2], vql[2][2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        gc_split(vn[2 * s2][u], vn[2 * s2 + 1][u], vph[s2][u], vpl[s2][u]);
+        gc_f32x4 p, q;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          p[j] = vn[2 * s2][u][j] * sh.f7v[32 * s2 + 4 * g4 + j];
+          q[j] = vn[2 * s2 + 1][u][j] * sh.f7v[32 * s2 + 16 + 4 * g4 + j];
+        }
+        gc_split(p, q, vqh[s2][u], vql[s2][u]);
+      }
+    __syncthreads();   // Tm and W consumed: the O staging may overwrite them
+    // ================= O = diag(rq s e^gc) Q S + (masked s q.k decay) V' =================
+    {
+      gc_f32x4 ov[4][2];
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) ov[ib][u] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const uint16_t* rq = &sh.qc[16 * ib + r16][32 * s + 4 * g4];
+          const gc_bf16x8 aq = gc_ld44(rq, rq + 16);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            ov[ib][u] = gc_mma(aq, sth[s][u], ov[ib][u]);
+            ov[ib][u] = gc_mma(aq, stl[s][u], ov[ib][u]);
+          }
+        }
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = 16 * ib + 4 * g4 + j;
+          const float rs = sh.rqv[i] * qscale * sh.egv[i];
+          ov[ib][0][j] *= rs;
+          ov[ib][1][j] *= rs;
+        }
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int s2 = 0; s2 <= (ib >> 1); ++s2) {
+          const uint16_t* rh = &sh.r1.in[0][16 * ib + r16][32 * s2 + 4 * g4];
+          const uint16_t* rl = &sh.r1.in[1][16 * ib + r16][32 * s2 + 4 * g4];
+          const gc_bf16x8 ah = gc_ld44(rh, rh + 16), al = gc_ld44(rl, rl + 16);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            ov[ib][u] = gc_mma(ah, vph[s2][u], ov[ib][u]);
+            ov[ib][u] = gc_mma(ah, vpl[s2][u], ov[ib][u]);
+            ov[ib][u] = gc_mma(al, vph[s2][u], ov[ib][u]);
+          }
+        }
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sh.r3.o[16 * ib + 4 * g4 + j][vcol + 16 * u + r16] = ov[ib][u][j];
+    }
+    // ================= S <- e^gc_63 S + K^T diag(rk e^(gc_63 - gc)) V' =================
+    {
+      const float elast = sh.egv[GC_C - 1];
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) st[kb][u] *= elast;
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const uint16_t* rk = &sh.kt[16 * kb + r16][32 * s2 + 4 * g4];
+          const gc_bf16x8 ak = gc_ld44(rk, rk + 16);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            st[kb][u] = gc_mma(ak, vqh[s2][u], st[kb][u]);
+            st[kb][u] = gc_mma(ak, vql[s2][u], st[kb][u]);
+          }
+        }
+    }
+    __syncthreads();   // O complete; every chunk buffer consumed
+    // the next chunk's inputs, issued unconditionally (after the last chunk: rows clamped
+    // into the call, never used) so the wait counts of the norm below stay exact
+    gc_prefetch(projb, a.P, a.T, t0 + GC_C, tid, c0n, raw);
+    gc_prefetch_ba(a, projb, h, t0 + GC_C, tid, braw, araw);
+    // ================= gated RMSNorm, 16 threads per token, 8 columns each =================
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const int i = 16 * n + (tid >> 4), part = tid & 15, t = t0 + i;
+      const float4 oa = *reinterpret_cast<const float4*>(&sh.r3.o[i][part * 8]);
+      const float4 ob = *reinterpret_cast<const float4*>(&sh.r3.o[i][part * 8 + 4]);
+      float ovs[8] = {oa.x, oa.y, oa.z, oa.w, ob.x, ob.y, ob.z, ob.w}, ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ovs[e] = gc_rbf(ovs[e]);   // the core output is a bf16 tensor
+        ss = fmaf(ovs[e], ovs[e], ss);
+      }
+      ss = gc_row16_sum(ss);
+      const float rr = rsqrtf(ss / (float)GL_DK + a.eps);
+      const uint32_t zd[4] = {zreg[n].x, zreg[n].y, zreg[n].z, zreg[n].w};
+      const uint32_t wd[4] = {nwreg.x, nwreg.y, nwreg.z, nwreg.w};
+      uint32_t od[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float y2[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int ee = e + u;
+          const float z = __uint_as_float(ee & 1 ? zd[ee >> 1] & 0xffff0000u : zd[ee >> 1] << 16);
+          const float w = __uint_as_float(ee & 1 ? wd[ee >> 1] & 0xffff0000u : wd[ee >> 1] << 16);
+          y2[u] = gc_rbf(w * gc_rbf(ovs[ee] * rr)) * silu_g(z);
+        }
+        od[e >> 1] = gc_pack(y2[0], y2[1]);
+      }
+      if (t < a.T)
         *reinterpret_cast<uint4*>(a.out + ((size_t)b * a.T + t) * a.value_dim + (size_t)h * GL_DK +
                                   part * 8) = make_uint4(od[0], od[1], od[2], od[3]);
-      }
     }
   }
-  __syncthreads();
   // ---- final state in slot 0 of the written half; final K-1 raw inputs in the window ----
   {
     float* sf = a.rec + ((size_t)(b * 2 * a.S + rbase) * a.Hv + h) * SS;
-    for (int i = tid; i < GL_DK * GL_DK / 4; i += 256) {
-      const int row = i / (GL_DK / 4), c4 = (i % (GL_DK / 4)) * 4;
-      *reinterpret_cast<float4*>(sf + (size_t)row * GL_DK + c4) =
-          make_float4(sh.sm[row][c4], sh.sm[row][c4 + 1], sh.sm[row][c4 + 2], sh.sm[row][c4 + 3]);
-    }
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          sf[(size_t)(16 * kb + 4 * g4 + j) * GL_DK + vcol + 16 * u + r16] = st[kb][u][j];
     for (int i = tid; i < Km1 * GL_CH; i += 256) {
       const int r = i / GL_CH, lc = i % GL_CH;
       if (lc >= 2 * GL_DK || write_qk) {
-        const int c = gchan(lc);
+        const int c = gc_chan(a, hk, h, lc);
         a.win[(win_b + wbase + r) * a.C + c] = a.proj[((size_t)b * a.T + a.T - Km1 + r) * a.P + c];
       }
     }
