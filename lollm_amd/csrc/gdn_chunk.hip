@@ -52,6 +52,7 @@ constexpr int GC_PO = 132;   // fp32 pitch of the output rows
 
 typedef float gc_f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 gc_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 gc_bf16x2 __attribute__((ext_vector_type(2)));
 
 struct GcSmem {
   union {
@@ -72,7 +73,7 @@ struct GcSmem {
     uint16_t tm[4][GC_C][GC_PN];        // hi, lo of Tm diag(rk beta e^gc), of Tm diag(beta)
     float o[GC_C][GC_PO];               // O (fp32) for the gated norm
   } r3;
-  float gcv[GC_C], egv[GC_C], btv[GC_C], gv[GC_C], rqv[GC_C], rkv[GC_C];
+  float gcv[GC_C], egv[GC_C], btv[GC_C], rqv[GC_C], rkv[GC_C];
   float fwv[GC_C], f7v[GC_C];  // rk beta e^gc (W), rk e^(gc_63 - gc) (state update)
   uint16_t cw[GL_CH][4];       // conv weights of the head's q, k, v channels
 };
@@ -143,33 +144,45 @@ __device__ __forceinline__ int gc_chan(const GdnLayerArgs& a, int hk, int h, int
 
 // Conv work of a chunk: item n of thread tid = (8-channel vector cv of the 48, 4-token
 // group tq of the 16) with it = tid + 256 n; its 7 input rows (3 history + 4) are
-// loaded ahead of use.  Every load is issued unconditionally and nothing touches the
-// loaded values before the conv uses them, so no wait is placed at the loads and a
-// later wait never drains loads issued after these.  A row past the call is read at
-// row T - 1 instead: it only feeds outputs of tokens past the call, which are zero.
-// (Chunks after the first never reach back into the conv window.)
+// loaded ahead of use.  Chunks after the first read the projection through a buffer
+// descriptor over this sequence's rows: a row past the call reads as zero (it only
+// feeds outputs of tokens past the call), no address is clamped, and a load costs one
+// 32-bit add.  The loads are issued unconditionally and nothing touches the loaded
+// values before their use, so no wait is placed at the loads and a later wait never
+// drains loads issued after these.
 constexpr int GC_ITEMS = 3;
 
-__device__ __forceinline__ void gc_prefetch(const uint16_t* projb, long long P, int T, int tc, int tid,
-                                            const int (&c0n)[GC_ITEMS], u32x4_t (&raw)[GC_ITEMS][7]) {
-#pragma unroll
-  for (int n = 0; n < GC_ITEMS; ++n) {
-    const int t4 = tc + 4 * ((tid + 256 * n) / 48);
-#pragma unroll
-    for (int r = 0; r < 7; ++r) {
-      const int t = t4 - 3 + r;
-      raw[n][r] = *reinterpret_cast<const u32x4_t*>(projb + (size_t)(t < T ? t : T - 1) * P + c0n[n]);
-    }
-  }
+__device__ __forceinline__ u32x4_t gc_bload(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
 }
 
-// bf16 b and a (gating inputs) of token tc + (tid & 63)
-__device__ __forceinline__ void gc_prefetch_ba(const GdnLayerArgs& a, const uint16_t* projb, int h, int tc,
-                                               int tid, uint16_t& braw, uint16_t& araw) {
-  const int t = tc + (tid & (GC_C - 1));
-  const uint16_t* p = projb + (size_t)(t < a.T ? t : a.T - 1) * a.P + a.C + a.value_dim + h;
-  braw = p[0];
-  araw = p[a.Hv];
+// The NB blocks T_(j+d, j), d = 4 - NB, of Tm's block diagonal d (64 x 64, 16 x 16 blocks).
+template <int NB>
+__device__ __forceinline__ void gc_off_diagonal(float (*am)[GC_PF], float (*tf)[GC_PF], int r16, int g4) {
+  constexpr int d = 4 - NB;
+  gc_f32x4 p[NB], t[NB];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    p[n] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
+    t[n] = gc_f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int kb = 0; kb < d; ++kb)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int n = 0; n < NB; ++n)
+        p[n] = gc_mma4(am[16 * (n + d) + r16][16 * (n + kb) + 4 * s + g4],
+                       tf[16 * (n + kb) + 4 * s + g4][16 * n + r16], p[n]);
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+      t[n] = gc_mma4(tf[16 * (n + d) + r16][16 * (n + d) + 4 * g4 + s], p[n][s], t[n]);
+#pragma unroll
+  for (int n = 0; n < NB; ++n)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tf[16 * (n + d) + 4 * g4 + j][16 * n + r16] = t[n][j];
 }
 
 __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
@@ -212,6 +225,22 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
 #pragma unroll
   for (int n = 0; n < GC_ITEMS; ++n) c0n[n] = gc_chan(a, hk, h, 8 * ((tid + 256 * n) % 48));
   const uint16_t* projb = a.proj + (size_t)b * a.T * a.P;   // this sequence's projection rows
+  const uint32_t P2 = (uint32_t)a.P * 2u;                    // bytes per projection row
+  // (base and size made explicitly uniform, so the descriptor stays in scalar registers)
+  const uint64_t pbase = (uint64_t)projb;
+  const uint32_t plo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)pbase);
+  const uint32_t phi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(pbase >> 32));
+  const uint64_t pbu = ((uint64_t)phi << 32) | (uint64_t)plo;   // no sign extension of the low word
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)pbu, (short)0, __builtin_amdgcn_readfirstlane((int)((uint32_t)a.T * P2)), 0x00020000);
+  // byte offsets, relative to the chunk's first row: item n's first input row (3 before
+  // its group), the gating b of token tid & 63, z of norm row tid / 16
+  uint32_t roff[GC_ITEMS];
+#pragma unroll
+  for (int n = 0; n < GC_ITEMS; ++n)
+    roff[n] = (uint32_t)((4 * ((tid + 256 * n) / 48) - 3) * (int)P2 + 2 * c0n[n]);
+  const uint32_t boff = (uint32_t)(tid & (GC_C - 1)) * P2 + 2u * (uint32_t)(a.C + a.value_dim + h);
+  const uint32_t zoff = (uint32_t)(tid >> 4) * P2 + 2u * (uint32_t)(a.C + h * GL_DK + (tid & 15) * 8);
   u32x4_t raw[GC_ITEMS][7];
   uint16_t braw, araw;
   // the first chunk's history rows come from the committed conv window
@@ -226,8 +255,15 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
       raw[n][r] = *reinterpret_cast<const u32x4_t*>(src);
     }
   }
-  gc_prefetch_ba(a, projb, h, 0, tid, braw, araw);
-  const uint4 nwreg = *reinterpret_cast<const uint4*>(a.norm_w + (tid & 15) * 8);   // gated-norm weight
+  braw = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(prs, boff, 0, 0);
+  araw = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(prs, boff + 2u * a.Hv, 0, 0);
+  float nwf[8];   // gated-norm weight of this thread's 8 columns
+  {
+    const uint4 nw = *reinterpret_cast<const uint4*>(a.norm_w + (tid & 15) * 8);
+    const uint32_t nd[4] = {nw.x, nw.y, nw.z, nw.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) nwf[e] = __uint_as_float(e & 1 ? nd[e >> 1] & 0xffff0000u : nd[e >> 1] << 16);
+  }
   if (tid < GL_CH / 2)   // two channels (16 bytes) per thread
     *reinterpret_cast<u32x4_t*>(&sh.cw[2 * tid][0]) =
         *reinterpret_cast<const u32x4_t*>(a.conv_w + (size_t)gc_chan(a, hk, h, 2 * tid) * 4);
@@ -246,15 +282,24 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
     for (int n = 0; n < GC_ITEMS; ++n) {
       const int it = tid + 256 * n, cv = it % 48, tq = it / 48;
       const int nvalid = a.T - (t0 + 4 * tq);   // tokens of the group inside the call
+      // the 4-tap conv as two bf16 dot products per output: weights (tap 0, 1) and
+      // (tap 2, 3) of a channel are consecutive bf16 pairs; the inputs are paired
+      // (row r, row r + 1) per channel with a byte permute
       const u32x4_t* cwp = reinterpret_cast<const u32x4_t*>(&sh.cw[8 * cv][0]);
-      float w[8][4];
+      uint32_t w01[8], w23[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const u32x4_t cw = cwp[e >> 1];
-        const uint32_t lo = cw[(e & 1) * 2], hi = cw[(e & 1) * 2 + 1];
-        w[e][0] = __uint_as_float(lo << 16); w[e][1] = __uint_as_float(lo & 0xffff0000u);
-        w[e][2] = __uint_as_float(hi << 16); w[e][3] = __uint_as_float(hi & 0xffff0000u);
+      for (int q = 0; q < 4; ++q) {
+        const u32x4_t cw = cwp[q];
+        w01[2 * q] = cw[0]; w23[2 * q] = cw[1]; w01[2 * q + 1] = cw[2]; w23[2 * q + 1] = cw[3];
       }
+      uint32_t prs[6][8];   // (row r, row r + 1) of channel e
+#pragma unroll
+      for (int r = 0; r < 6; ++r)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          prs[r][2 * p] = __builtin_amdgcn_perm(raw[n][r + 1][p], raw[n][r][p], 0x05040100u);
+          prs[r][2 * p + 1] = __builtin_amdgcn_perm(raw[n][r + 1][p], raw[n][r][p], 0x07060302u);
+        }
       uint32_t pk[4][4];   // token r: bf16 pairs (channels 2p, 2p + 1)
       float ssq[4];        // token r: sum of squares over the 8 channels
 #pragma unroll
@@ -266,19 +311,17 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const int ee = 2 * p + u;
-            float acc = 0.f;
-#pragma unroll
-            for (int tau = 0; tau < 4; ++tau) {
-              const uint32_t wd = raw[n][r + tau][p];
-              acc = fmaf(w[ee][tau], __uint_as_float(u ? wd & 0xffff0000u : wd << 16), acc);
-            }
-            const float sv = silu_g(gc_rbf(acc));
-            o2[u] = r < nvalid ? sv : 0.f;
+            float acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(gc_bf16x2, prs[r][ee]),
+                                                        __builtin_bit_cast(gc_bf16x2, w01[ee]), 0.f, false);
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(gc_bf16x2, prs[r + 2][ee]),
+                                                  __builtin_bit_cast(gc_bf16x2, w23[ee]), acc, false);
+            o2[u] = silu_g(gc_rbf(acc));
           }
-          pk[r][p] = gc_pack(o2[0], o2[1]);
-          const float x0 = __uint_as_float(pk[r][p] << 16), x1 = __uint_as_float(pk[r][p] & 0xffff0000u);
-          ssq[r] = fmaf(x0, x0, ssq[r]);
-          ssq[r] = fmaf(x1, x1, ssq[r]);
+          const uint32_t pv = gc_pack(o2[0], o2[1]);
+          pk[r][p] = r < nvalid ? pv : 0u;
+          // the two squares in one bf16 dot product (exact products, fp32 sum)
+          ssq[r] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(gc_bf16x2, pk[r][p]),
+                                                   __builtin_bit_cast(gc_bf16x2, pk[r][p]), ssq[r], false);
         }
       }
       // the 16 lanes of a DPP row hold the 16 channel vectors of one kind (q, k or v)
@@ -302,12 +345,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
         uint16_t* dst = kind == 1 ? &sh.kt[0][0] : &sh.vt[0][0];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          uint32_t c[2];
+          uint32_t c[2];   // channel e of tokens (2 r2, 2 r2 + 1)
 #pragma unroll
-          for (int r2 = 0; r2 < 2; ++r2) {
-            const uint32_t x0 = pk[2 * r2][e >> 1], x1 = pk[2 * r2 + 1][e >> 1];
-            c[r2] = e & 1 ? (x0 >> 16) | (x1 & 0xffff0000u) : (x0 & 0xffffu) | (x1 << 16);
-          }
+          for (int r2 = 0; r2 < 2; ++r2)
+            c[r2] = __builtin_amdgcn_perm(pk[2 * r2 + 1][e >> 1], pk[2 * r2][e >> 1],
+                                          e & 1 ? 0x07060302u : 0x05040100u);
           *reinterpret_cast<uint2*>(dst + (col + e) * GC_PN + 4 * tq) = make_uint2(c[0], c[1]);
         }
       }
@@ -315,36 +357,30 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
     if (wave == 0) {   // lane = token
       float gg = 0.f, bb = 0.f;
       if (t0 + lane < a.T) {
-        gg = -__expf(a_log) * softplus_g(gc_bf(araw) + dtb);
-        bb = round_bf16(1.f / (1.f + __expf(-gc_bf(braw))));
+        const float x = gc_bf(araw) + dtb;   // softplus with torch's linear range above 20
+        gg = -__expf(a_log) * (x > 20.f ? x : __logf(1.f + __expf(x)));
+        bb = gc_rbf(__builtin_amdgcn_rcpf(1.f + __expf(-gc_bf(braw))));
       }
-      sh.gv[lane] = gg;
-      sh.btv[lane] = bb;
-      __builtin_amdgcn_wave_barrier();
-      if (lane == 0) {   // cumsum in token order, as the reference's torch.cumsum
-        float run = 0.f;
+      // cumsum(g) over the chunk as an inclusive lane scan
+      float gc = gg;
 #pragma unroll
-        for (int i = 0; i < GC_C; ++i) {
-          run += sh.gv[i];
-          sh.gcv[i] = run;
-        }
+      for (int d = 1; d < 64; d <<= 1) {
+        const float up = __shfl_up(gc, d, 64);
+        gc += lane >= d ? up : 0.f;
       }
-      __builtin_amdgcn_wave_barrier();
-      sh.egv[lane] = expf(sh.gcv[lane]);
+      sh.btv[lane] = bb;
+      sh.gcv[lane] = gc;
+      sh.egv[lane] = __expf(gc);
     }
     // z of this chunk for the gated norm (rows 16 n + tid / 16, 8 columns), issued after
     // the conv's loads were consumed and in flight until the end of the chunk
-    uint4 zreg[4];
+    u32x4_t zreg[4];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const int t = t0 + 16 * n + (tid >> 4);
-      zreg[n] = *reinterpret_cast<const uint4*>(projb + (size_t)(t < a.T ? t : a.T - 1) * a.P + a.C +
-                                                (size_t)h * GL_DK + (tid & 15) * 8);
-    }
+    for (int n = 0; n < 4; ++n) zreg[n] = gc_bload(prs, zoff + (uint32_t)(t0 + 16 * n) * P2);
     __syncthreads();
     if (tid < GC_C) {
       sh.fwv[tid] = sh.rkv[tid] * sh.btv[tid] * sh.egv[tid];
-      sh.f7v[tid] = sh.rkv[tid] * expf(sh.gcv[GC_C - 1] - sh.gcv[tid]);
+      sh.f7v[tid] = sh.rkv[tid] * __expf(sh.gcv[GC_C - 1] - sh.gcv[tid]);
     }
     // ================= A = -(beta_i k_i.k_j) exp(gc_i - gc_j), j < i =================
     // the 10 lower 16 x 16 tiles (ti >= tj), dealt to the waves
@@ -397,24 +433,14 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
 #pragma unroll
         for (int m = 0; m < 16; ++m) sh.r2.s.tf[base + m][base + c] = col[m] + (m == c ? 1.f : 0.f);
       }
-      // off-diagonal blocks by block diagonals: T_ij = T_ii sum_{k=j}^{i-1} A_ik T_kj
-#pragma unroll
-      for (int q = 0; q < 6; ++q) {
-        const int bi = q < 3 ? q + 1 : (q < 5 ? q - 1 : 3);
-        const int bj = q < 3 ? q : (q < 5 ? q - 3 : 0);
-        __builtin_amdgcn_wave_barrier();
-        gc_f32x4 p = {0.f, 0.f, 0.f, 0.f};
-        for (int kb = bj; kb < bi; ++kb)
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            p = gc_mma4(sh.r2.s.am[16 * bi + r16][16 * kb + 4 * s + g4],
-                        sh.r2.s.tf[16 * kb + 4 * s + g4][16 * bj + r16], p);
-        gc_f32x4 t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) t = gc_mma4(sh.r2.s.tf[16 * bi + r16][16 * bi + 4 * g4 + s], p[s], t);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sh.r2.s.tf[16 * bi + 4 * g4 + j][16 * bj + r16] = t[j];
-      }
+      // off-diagonal blocks by block diagonals, T_ij = T_ii sum_{k=j}^{i-1} A_ik T_kj; the
+      // blocks of one diagonal are independent (their product chains interleave) and are
+      // stored together before the next diagonal reads them.  fp32 MFMA 16x16x4: in step
+      // s lane group g carries k = 4s + g of the sum, and k = 4g + s of the T_ii product,
+      // whose B operand is then the accumulator element s of the same lane.
+      gc_off_diagonal<3>(sh.r2.s.am, sh.r2.s.tf, r16, g4);
+      gc_off_diagonal<2>(sh.r2.s.am, sh.r2.s.tf, r16, g4);
+      gc_off_diagonal<1>(sh.r2.s.am, sh.r2.s.tf, r16, g4);
     } else {
       // tiles (ti >= tj) of (q_i . k_j): wave 1 takes 0, 3, 6, 9; wave 2 1, 4, 7; wave 3 2, 5, 8
 #pragma unroll
@@ -672,24 +698,34 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
     __syncthreads();   // O complete; every chunk buffer consumed
     // the next chunk's inputs, issued unconditionally (after the last chunk: rows clamped
     // into the call, never used) so the wait counts of the norm below stay exact
-    gc_prefetch(projb, a.P, a.T, t0 + GC_C, tid, c0n, raw);
-    gc_prefetch_ba(a, projb, h, t0 + GC_C, tid, braw, araw);
+    {
+      const uint32_t cb = (uint32_t)(t0 + GC_C) * P2;
+#pragma unroll
+      for (int n = 0; n < GC_ITEMS; ++n)
+#pragma unroll
+        for (int r = 0; r < 7; ++r) raw[n][r] = gc_bload(prs, roff[n] + cb + (uint32_t)r * P2);
+      braw = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(prs, boff + cb, 0, 0);
+      araw = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(prs, boff + cb + 2u * a.Hv, 0, 0);
+    }
     // ================= gated RMSNorm, 16 threads per token, 8 columns each =================
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const int i = 16 * n + (tid >> 4), part = tid & 15, t = t0 + i;
       const float4 oa = *reinterpret_cast<const float4*>(&sh.r3.o[i][part * 8]);
       const float4 ob = *reinterpret_cast<const float4*>(&sh.r3.o[i][part * 8 + 4]);
-      float ovs[8] = {oa.x, oa.y, oa.z, oa.w, ob.x, ob.y, ob.z, ob.w}, ss = 0.f;
+      const float ovf[8] = {oa.x, oa.y, oa.z, oa.w, ob.x, ob.y, ob.z, ob.w};
+      float ovs[8], ss = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        ovs[e] = gc_rbf(ovs[e]);   // the core output is a bf16 tensor
-        ss = fmaf(ovs[e], ovs[e], ss);
+      for (int e = 0; e < 8; e += 2) {   // the core output is a bf16 tensor
+        const uint32_t pv = gc_pack(ovf[e], ovf[e + 1]);
+        ss = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(gc_bf16x2, pv),
+                                             __builtin_bit_cast(gc_bf16x2, pv), ss, false);
+        ovs[e] = __uint_as_float(pv << 16);
+        ovs[e + 1] = __uint_as_float(pv & 0xffff0000u);
       }
       ss = gc_row16_sum(ss);
       const float rr = rsqrtf(ss / (float)GL_DK + a.eps);
-      const uint32_t zd[4] = {zreg[n].x, zreg[n].y, zreg[n].z, zreg[n].w};
-      const uint32_t wd[4] = {nwreg.x, nwreg.y, nwreg.z, nwreg.w};
+      const uint32_t zd[4] = {zreg[n][0], zreg[n][1], zreg[n][2], zreg[n][3]};
       uint32_t od[4];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
@@ -698,8 +734,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
         for (int u = 0; u < 2; ++u) {
           const int ee = e + u;
           const float z = __uint_as_float(ee & 1 ? zd[ee >> 1] & 0xffff0000u : zd[ee >> 1] << 16);
-          const float w = __uint_as_float(ee & 1 ? wd[ee >> 1] & 0xffff0000u : wd[ee >> 1] << 16);
-          y2[u] = gc_rbf(w * gc_rbf(ovs[ee] * rr)) * silu_g(z);
+          y2[u] = gc_rbf(nwf[ee] * gc_rbf(ovs[ee] * rr)) * silu_g(z);
         }
         od[e >> 1] = gc_pack(y2[0], y2[1]);
       }
@@ -749,6 +784,7 @@ LOLLM_API int lollm_gdn_layer_chunked(const void* proj, long long proj_stride, c
   if (T <= slots || conv_kernel - 1 + T <= win_rows || T < conv_kernel - 1) return LOLLM_EUNSUPPORTED;
   const int key_dim = Hk * Dk, value_dim = Hv * Dv, C = 2 * key_dim + value_dim;
   if (proj_stride < (long long)C + value_dim + 2 * Hv || proj_stride % 8) return LOLLM_EINVAL;
+  if ((long long)T * proj_stride * 2 >= (1LL << 31)) return LOLLM_EUNSUPPORTED;   // 32-bit row offsets
   GdnLayerArgs a;
   a.proj = (const uint16_t*)proj; a.conv_w = (const uint16_t*)conv_w; a.A_log = A_log;
   a.dt_bias = dt_bias; a.norm_w = (const uint16_t*)norm_w; a.win = (uint16_t*)win;

@@ -416,9 +416,12 @@ def attn_prologue(qkv, q_norm_w, k_norm_w, inv_freq, lengths, B, T, Hq, Hkv, D, 
 GDN_CHUNK_MIN_T = 64
 
 
-def gdn_chunked_ok(T, slots, win_rows, conv_kernel):
-    """Whether a call can take the chunked long-call kernel (lollm_gdn_layer_chunked)."""
-    return conv_kernel == 4 and T > slots and conv_kernel - 1 + T > win_rows
+def gdn_chunked_ok(T, slots, win_rows, conv_kernel, proj_stride=0):
+    """Whether a call can take the chunked long-call kernel (lollm_gdn_layer_chunked):
+    a call longer than the snapshot slots and the conv window, and one sequence's
+    projection rows addressable with 32-bit byte offsets."""
+    return (conv_kernel == 4 and T > slots and conv_kernel - 1 + T > win_rows
+            and T * proj_stride * 2 < 2 ** 31)
 
 
 def gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, fresh, B, T,
@@ -440,7 +443,7 @@ def gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot
         out = torch.empty(B, T, value_dim, dtype=torch.bfloat16, device=proj.device)
     W, S = win.shape[1] // 2, rec.shape[1] // 2
     if chunked is None:
-        chunked = T >= GDN_CHUNK_MIN_T and gdn_chunked_ok(T, S, W, conv_kernel)
+        chunked = T >= GDN_CHUNK_MIN_T and gdn_chunked_ok(T, S, W, conv_kernel, P)
     fn = "lollm_gdn_layer_chunked" if chunked else "lollm_gdn_layer"
     rc = getattr(_lib.lib(), fn)(
         _ptr(proj), P, _ptr(conv_w), _ptr(A_log), _ptr(dt_bias), _ptr(norm_w), _ptr(win),
