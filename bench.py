@@ -215,15 +215,24 @@ def isolated_gdn(B, kd):
 
 
 PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_BF16_MFMA_TFLOPS = 2500.0
+# MFMA instructions the chunked prefill kernel issues per (sequence, v-head, 64-token
+# chunk): bf16 16x16x32 (k.k^T, q.k^T tiles; W^T and Tm diag(beta) V with Tm as hi + lo;
+# W S with both operands hi + lo (3 products); Q S, intra V', K^T V' with one operand
+# hi + lo) and fp32 16x16x4 (the off-diagonal blocks of the triangular solve)
+GDN_CHUNK_BF16_MFMA = 40 + 40 + 96 + 480 + 400 + 256
+GDN_CHUNK_FP32_MFMA = 64
 
 
 def isolated_gdn_prefill(B=16, T=2048):
     """The chunked GDN prefill layer (conv + gating + chunked delta rule + gated norm)
-    at the e2e prompt shape; compute-bound, so reported against the fp32 matrix peak.
-    FLOPs counted: the chunk algorithm's products per (sequence, v-head, 64-token chunk)
-    -- k.k^T and q.k^T (2 x 64x64x128), W and Tm diag(beta) V (2 x 64x128x64), W S and
-    Q S (2 x 64x128x128), intra V' (64x128x64), K^T V' (128x128x64) -- at 2 flops per
-    multiply-add."""
+    at the e2e prompt shape.  Two rates: the algorithm's fp32 products per (sequence,
+    v-head, 64-token chunk) -- k.k^T and q.k^T (2 x 64x64x128), W and Tm diag(beta) V
+    (2 x 64x128x64), W S and Q S (2 x 64x128x128), intra V' (64x128x64), K^T V'
+    (128x128x64), 2 flops per multiply-add -- per second; and the MFMA work the kernel
+    issues for them (bf16 with hi/lo operand splits, plus the fp32 solve products) as a
+    fraction of the bf16 dense matrix peak.  Neither bound is reached: the chunks of a
+    (sequence, head) run in sequence and each is a chain of dependent phases."""
     import torch
     from lollm_amd import ops
     Hk, Hv, D, K, S = 16, 32, 128, 4, 4
@@ -246,9 +255,13 @@ def isolated_gdn_prefill(B=16, T=2048):
     per_chunk = 2 * (2 * C64 * C64 * D + 2 * C64 * D * C64 + 2 * C64 * D * D + C64 * D * C64 + D * D * C64)
     flops = B * Hv * (-(-T // C64)) * per_chunk
     tf = flops / us / 1e6
-    return {"B": B, "T": T, "us": round(us, 1), "GFLOP": round(flops / 1e9, 1),
-            "TFLOPs": round(tf, 2), "bound": "mfma", "peak": PEAK_FP32_MFMA_TFLOPS,
-            "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 3)}
+    chunks = B * Hv * (-(-T // C64))
+    issued = chunks * (GDN_CHUNK_BF16_MFMA * 16 * 16 * 32 * 2 + GDN_CHUNK_FP32_MFMA * 16 * 16 * 4 * 2)
+    mf = issued / us / 1e6
+    return {"B": B, "T": T, "us": round(us, 1), "algorithmic_GFLOP": round(flops / 1e9, 1),
+            "algorithmic_TFLOPs": round(tf, 2), "mfma_issued_GFLOP": round(issued / 1e9, 1),
+            "mfma_TFLOPs": round(mf, 2), "bound": "latency (serial chunks)",
+            "peak": PEAK_BF16_MFMA_TFLOPS, "frac": round(mf / PEAK_BF16_MFMA_TFLOPS, 3)}
 
 
 def isolated_attn():
