@@ -140,6 +140,16 @@ int lollm_philox_uniform_u24(uint64_t seed, uint64_t offset, int rows, int slots
 int lollm_rmsnorm(const void* x, const void* residual, void* x_out, const void* w, void* y,
                   int rows, int H, float eps, void* stream);
 
+/* The MTP head's fc input from draft token ids (src/qwen3_5/mtp.py:61-73, with the
+ * embedding lookup the draft chain does before it): out (B, 2H) bf16, row b =
+ * [RMSNorm_{1+w_emb}(table[tok[b]]) | RMSNorm_{1+w_hidden}(hidden[b])], each half with
+ * lollm_rmsnorm's arithmetic, so the bits equal the lookup + two norms + concatenation
+ * it replaces.  tok (B) int32, clamped into [0, vocab); hidden (B, H) bf16 with row
+ * stride ld_hidden; table (vocab, H) bf16.  Supported: H % 8 == 0, H <= 8192. */
+int lollm_mtp_input(const int32_t* tok, const void* hidden, long long ld_hidden, const void* table,
+                    int vocab, const void* w_emb, const void* w_hidden, void* out, int B, int H,
+                    float eps, void* stream);
+
 /* SwiGLU of blocks.py:341-342 on a fused [gate | up] projection: gate_up (rows, 2F)
  * bf16 -> out (rows, F) = bf16(bf16(silu(gate)) * up).  Supported: F % 8 == 0. */
 int lollm_swiglu(const void* gate_up, void* out, int rows, int F, void* stream);

@@ -3,6 +3,8 @@
 //   rmsnorm      (src/qwen3_5/blocks.py:23-35) y = x * rsqrt(mean x^2 + eps) * (1 + w)
 //                in fp32, optionally fused with the residual add of
 //                modeling_qwen3_5.py:59-60 (x <- x + h, then y = norm(x))
+//   mtp_input    (src/qwen3_5/mtp.py:61-73) the MTP head's fc input from token ids:
+//                embedding lookup, both pre-fc RMSNorms and the concatenation
 //   swiglu       (blocks.py:341-342) silu(gate) * up on a fused [gate | up] GEMM output
 //   attn_prologue (blocks.py:214-227 + RoPE blocks.py:166-183 + kv.py:26-33):
 //                split q_proj's per-head [query | gate], QK-norm (1 + w), partial
@@ -14,17 +16,16 @@
 
 namespace lollm {
 
-// One RMS_THREADS-thread workgroup per row; H % 8 == 0, vector loads of 8 bf16.
-__global__ __launch_bounds__(RMS_THREADS) void rmsnorm_kernel(const uint16_t* __restrict__ x,
-                                                              const uint16_t* __restrict__ h,
-                                                              uint16_t* __restrict__ x_out,
-                                                              const uint16_t* __restrict__ w,
-                                                              uint16_t* __restrict__ y, int H,
-                                                              float eps) {
-  __shared__ float red[RMS_THREADS / 64];
-  const size_t row = blockIdx.x;
-  const uint4* x4 = reinterpret_cast<const uint4*>(x + row * H);
-  const uint4* h4 = h ? reinterpret_cast<const uint4*>(h + row * H) : nullptr;
+// One row of RMSNorm (RMS_THREADS threads; H % 8 == 0, vector loads of 8 bf16): x_row,
+// optionally + h_row first (then written to xout_row when given), normalised into
+// y_row.  Shared by every kernel that normalises a row so their bits agree.
+__device__ __forceinline__ void rms_row(const uint16_t* __restrict__ x_row,
+                                        const uint16_t* __restrict__ h_row,
+                                        uint16_t* __restrict__ xout_row,
+                                        const uint16_t* __restrict__ w,
+                                        uint16_t* __restrict__ y_row, int H, float eps, float* red) {
+  const uint4* x4 = reinterpret_cast<const uint4*>(x_row);
+  const uint4* h4 = h_row ? reinterpret_cast<const uint4*>(h_row) : nullptr;
   const int n8 = H / 8;
   constexpr int MAXV = RMS_CHUNKS;  // H <= 8192
   float v[MAXV][8];
@@ -44,13 +45,13 @@ __global__ __launch_bounds__(RMS_THREADS) void rmsnorm_kernel(const uint16_t* __
         v[i][e] = f;
         ss += f * f;
       }
-      if (h4 && x_out) {
+      if (h4 && xout_row) {
         uint4 o;
         o.x = f32_to_bf16(v[i][0]) | ((uint32_t)f32_to_bf16(v[i][1]) << 16);
         o.y = f32_to_bf16(v[i][2]) | ((uint32_t)f32_to_bf16(v[i][3]) << 16);
         o.z = f32_to_bf16(v[i][4]) | ((uint32_t)f32_to_bf16(v[i][5]) << 16);
         o.w = f32_to_bf16(v[i][6]) | ((uint32_t)f32_to_bf16(v[i][7]) << 16);
-        reinterpret_cast<uint4*>(x_out + row * H)[c] = o;
+        reinterpret_cast<uint4*>(xout_row)[c] = o;
       }
     }
   }
@@ -65,8 +66,45 @@ __global__ __launch_bounds__(RMS_THREADS) void rmsnorm_kernel(const uint16_t* __
       uint32_t od[4];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) od[e >> 1] = rms_out2(v[i][e], v[i][e + 1], r, wd[e >> 1]);
-      reinterpret_cast<uint4*>(y + row * H)[c] = make_uint4(od[0], od[1], od[2], od[3]);
+      reinterpret_cast<uint4*>(y_row)[c] = make_uint4(od[0], od[1], od[2], od[3]);
     }
+  }
+}
+
+__global__ __launch_bounds__(RMS_THREADS) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                              const uint16_t* __restrict__ h,
+                                                              uint16_t* __restrict__ x_out,
+                                                              const uint16_t* __restrict__ w,
+                                                              uint16_t* __restrict__ y, int H,
+                                                              float eps) {
+  __shared__ float red[RMS_THREADS / 64];
+  const size_t row = blockIdx.x;
+  rms_row(x + row * H, h ? h + row * H : nullptr, x_out ? x_out + row * H : nullptr, w, y + row * H,
+          H, eps, red);
+}
+
+// The MTP head's input (src/qwen3_5/mtp.py:61-73 with the embedding lookup of the draft
+// chain): out[b] = [RMSNorm_{1+w_emb}(table[tok[b]]) | RMSNorm_{1+w_hid}(hidden[b])],
+// workgroup (b, half); the same row arithmetic as lollm_rmsnorm, so the bits equal the
+// embedding + two norms + concatenation it replaces.  Ids are clamped into the table.
+__global__ __launch_bounds__(RMS_THREADS) void mtp_input_kernel(const int32_t* __restrict__ tok,
+                                                                const uint16_t* __restrict__ hidden,
+                                                                long long ldh,
+                                                                const uint16_t* __restrict__ table,
+                                                                int V,
+                                                                const uint16_t* __restrict__ w_emb,
+                                                                const uint16_t* __restrict__ w_hid,
+                                                                uint16_t* __restrict__ out, int H,
+                                                                float eps) {
+  __shared__ float red[RMS_THREADS / 64];
+  const int b = blockIdx.x;
+  uint16_t* y = out + (size_t)b * 2 * H;
+  if (blockIdx.y == 0) {
+    int id = tok[b];
+    id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+    rms_row(table + (size_t)id * H, nullptr, nullptr, w_emb, y, H, eps, red);
+  } else {
+    rms_row(hidden + (size_t)b * ldh, nullptr, nullptr, w_hid, y + H, H, eps, red);
   }
 }
 
@@ -181,6 +219,18 @@ LOLLM_API int lollm_rmsnorm(const void* x, const void* residual, void* x_out, co
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(RMS_THREADS), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)residual, (uint16_t*)x_out,
                      (const uint16_t*)w, (uint16_t*)y, H, eps);
+  return launch_status();
+}
+
+LOLLM_API int lollm_mtp_input(const int32_t* tok, const void* hidden, long long ld_hidden,
+                              const void* table, int vocab, const void* w_emb, const void* w_hidden,
+                              void* out, int B, int H, float eps, void* stream) {
+  if (!tok || !hidden || !table || !w_emb || !w_hidden || !out || B <= 0 || H <= 0 || vocab <= 0)
+    return LOLLM_EINVAL;
+  if (H % 8 || H > 8192 || ld_hidden < H || ld_hidden % 8) return LOLLM_EUNSUPPORTED;
+  hipLaunchKernelGGL(mtp_input_kernel, dim3(B, 2), dim3(RMS_THREADS), 0, (hipStream_t)stream, tok,
+                     (const uint16_t*)hidden, ld_hidden, (const uint16_t*)table, vocab,
+                     (const uint16_t*)w_emb, (const uint16_t*)w_hidden, (uint16_t*)out, H, eps);
   return launch_status();
 }
 

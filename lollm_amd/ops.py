@@ -360,6 +360,31 @@ def philox_u24(seed, offset, rows, slots, device="cuda"):
 # ------------------------------------------------------------------------------------
 # fused decoder-layer kernels
 # ------------------------------------------------------------------------------------
+def mtp_input(tok, hidden, table, w_emb, w_hidden, eps, out=None):
+    """[RMSNorm_{1+w_emb}(table[tok]) | RMSNorm_{1+w_hidden}(hidden)] -> (B, 2H) bf16 in one
+    kernel (lollm_mtp_input).  tok (B,) int32; hidden (B, H) bf16 (rows may be strided);
+    table (V, H) bf16."""
+    B = tok.numel()
+    V, H = table.shape
+    _need(tok, "tok", torch.int32, (B,))
+    _need(table, "table", torch.bfloat16)
+    _need(w_emb, "w_emb", torch.bfloat16, (H,))
+    _need(w_hidden, "w_hidden", torch.bfloat16, (H,))
+    if hidden.dtype != torch.bfloat16 or hidden.shape[-1] != H or hidden.numel() != B * H:
+        raise ValueError(f"hidden must be ({B}, {H}) bf16, got {tuple(hidden.shape)} {hidden.dtype}")
+    hidden = hidden.reshape(B, H)
+    if hidden.stride(-1) != 1 or hidden.data_ptr() % 16 or hidden.stride(0) % 8:
+        hidden = hidden.contiguous()
+    if out is None:
+        out = torch.empty(B, 2 * H, dtype=torch.bfloat16, device=table.device)
+    _need(out, "out", torch.bfloat16, (B, 2 * H))
+    rc = _lib.lib().lollm_mtp_input(_ptr(tok), _ptr(hidden), hidden.stride(0), _ptr(table), V,
+                                    _ptr(w_emb), _ptr(w_hidden), _ptr(out), B, H, float(eps),
+                                    _stream())
+    _lib.check(rc, "lollm_mtp_input")
+    return out
+
+
 def rmsnorm(x, w, eps, residual=None, x_out=None, out=None):
     """y = RMSNorm_{1+w}(x) or, with residual, x_out = x + residual, y = norm(x_out).
     x: (..., H) bf16.  Returns y, or (y, x_out) when residual is given."""

@@ -48,10 +48,19 @@ class MTP:
                                [self.fc] + layer.self_attn.projections() + layer.mlp.projections()),
                            model.device)
 
-    def _block(self, hidden, next_emb, k_cache, v_cache, lengths, kv_len, rope_pos, ws):
-        """Returns (MTP layer output before the final norm, normed output)."""
-        x = self.fc(torch.cat([self.pre_fc_norm_embedding(next_emb),
-                               self.pre_fc_norm_hidden(hidden)], -1))
+    def _block(self, hidden, next_emb, k_cache, v_cache, lengths, kv_len, rope_pos, ws, tok=None):
+        """Returns (MTP layer output before the final norm, normed output).  Given the
+        next tokens' ids `tok` (B,) int32 instead of their embeddings, the lookup, both
+        pre-fc norms and the concatenation run as one kernel (lollm_mtp_input)."""
+        if tok is not None:
+            B = tok.numel()
+            x = self.fc(ops.mtp_input(tok, hidden, self.model.model.embed_tokens.weight,
+                                      self.pre_fc_norm_embedding.weight,
+                                      self.pre_fc_norm_hidden.weight,
+                                      self.pre_fc_norm_embedding.eps).view(B, 1, -1))
+        else:
+            x = self.fc(torch.cat([self.pre_fc_norm_embedding(next_emb),
+                                   self.pre_fc_norm_hidden(hidden)], -1))
         layer = self.layers[0]
         h_in = layer.input_layernorm(x)
         core = layer.self_attn.core(h_in, k_cache, v_cache, lengths, kv_len, rope_pos=rope_pos,
@@ -170,9 +179,8 @@ class SpecDecoder:
         tok = self.pending
         h = self.h_last.view(B, 1, -1)
         for j in range(1, k + 1):
-            emb = model.model.embed_tokens(tok.view(B, 1).long())
-            m, normed = mtp._block(h, emb, self.mkc, self.mvc, self.mtp_len[j - 1],
-                                   self.mtp_len[j], self.mtp_len[j], self.mtp_ws)
+            m, normed = mtp._block(h, None, self.mkc, self.mvc, self.mtp_len[j - 1],
+                                   self.mtp_len[j], self.mtp_len[j], self.mtp_ws, tok=tok)
             lg = model.lm_head(normed).view(B, -1)
             if self.draft_mode == "sample":
                 self.draft_logits[:, j - 1].copy_(lg)
@@ -190,7 +198,7 @@ class SpecDecoder:
         B, k, model, cache = self.B, self.k, self.model, self.cache
         self._draft_chain()
         verify_ids = torch.cat([self.pending.view(B, 1), self.drafts], 1)
-        hidden, normed = model.hidden_states(verify_ids.long(), cache)
+        hidden, normed = model.hidden_states(verify_ids, cache)   # int32 ids: no widening copy
         logits = model.lm_head(normed)
         ops.spec_accept(logits, self.draft_logits, self.drafts, self.temperature, self.top_k,
                         self.top_p, self.seed, 0, offset_dev=self.offset,
