@@ -144,11 +144,11 @@ int lollm_rmsnorm(const void* x, const void* residual, void* x_out, const void* 
  * embedding lookup the draft chain does before it): out (B, 2H) bf16, row b =
  * [RMSNorm_{1+w_emb}(table[tok[b]]) | RMSNorm_{1+w_hidden}(hidden[b])], each half with
  * lollm_rmsnorm's arithmetic, so the bits equal the lookup + two norms + concatenation
- * it replaces.  tok (B) int32, clamped into [0, vocab); hidden (B, H) bf16 with row
+ * it replaces.  tok[b * tok_stride] int32, clamped into [0, vocab); hidden (B, H) bf16 with row
  * stride ld_hidden; table (vocab, H) bf16.  Supported: H % 8 == 0, H <= 8192. */
-int lollm_mtp_input(const int32_t* tok, const void* hidden, long long ld_hidden, const void* table,
-                    int vocab, const void* w_emb, const void* w_hidden, void* out, int B, int H,
-                    float eps, void* stream);
+int lollm_mtp_input(const int32_t* tok, long long tok_stride, const void* hidden, long long ld_hidden,
+                    const void* table, int vocab, const void* w_emb, const void* w_hidden, void* out,
+                    int B, int H, float eps, void* stream);
 
 /* SwiGLU of blocks.py:341-342 on a fused [gate | up] projection: gate_up (rows, 2F)
  * bf16 -> out (rows, F) = bf16(bf16(silu(gate)) * up).  Supported: F % 8 == 0. */
@@ -194,6 +194,18 @@ long long lollm_gemm_workspace_bytes(int M, int N, int K, int grid);
 int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, long long ldc, int M,
                int N, int K, int epilogue, void* workspace, long long workspace_bytes, int grid,
                void* stream);
+
+/* The greedy draft pick fused into the lm_head GEMM (src/qwen3_5/mtp.py:138: the draft
+ * is the argmax of the MTP head's logits; the reference computes the (B, V) logits with
+ * model.lm_head and argmaxes them): out[r * out_stride] = argmax_n of row r of
+ * A W^T, where each product is rounded to bf16 exactly as lollm_gemm writes it and ties
+ * go to the lowest column -- the same token as lollm_gemm followed by the greedy
+ * lollm_sample_rows, without materialising the logits.  Wt tiled with epilogue 0;
+ * shapes as lollm_gemm; workspace from lollm_gemm_argmax_workspace_bytes. */
+long long lollm_gemm_argmax_workspace_bytes(int M, int N, int K, int grid);
+int lollm_gemm_argmax(const void* A, long long lda, const void* Wt, int M, int N, int K,
+                      int32_t* out, long long out_stride, void* workspace, long long workspace_bytes,
+                      int grid, void* stream);
 
 /* A projection that feeds the residual stream, with the residual add and the next
  * RMSNorm fused into the GEMM's second kernel: C = A W^T (as lollm_gemm, epilogue 0),

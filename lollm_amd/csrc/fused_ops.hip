@@ -88,6 +88,7 @@ __global__ __launch_bounds__(RMS_THREADS) void rmsnorm_kernel(const uint16_t* __
 // workgroup (b, half); the same row arithmetic as lollm_rmsnorm, so the bits equal the
 // embedding + two norms + concatenation it replaces.  Ids are clamped into the table.
 __global__ __launch_bounds__(RMS_THREADS) void mtp_input_kernel(const int32_t* __restrict__ tok,
+                                                                long long tok_stride,
                                                                 const uint16_t* __restrict__ hidden,
                                                                 long long ldh,
                                                                 const uint16_t* __restrict__ table,
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(RMS_THREADS) void mtp_input_kernel(const int32_t* _
   const int b = blockIdx.x;
   uint16_t* y = out + (size_t)b * 2 * H;
   if (blockIdx.y == 0) {
-    int id = tok[b];
+    int id = tok[(size_t)b * tok_stride];
     id = id < 0 ? 0 : (id >= V ? V - 1 : id);
     rms_row(table + (size_t)id * H, nullptr, nullptr, w_emb, y, H, eps, red);
   } else {
@@ -222,14 +223,15 @@ LOLLM_API int lollm_rmsnorm(const void* x, const void* residual, void* x_out, co
   return launch_status();
 }
 
-LOLLM_API int lollm_mtp_input(const int32_t* tok, const void* hidden, long long ld_hidden,
-                              const void* table, int vocab, const void* w_emb, const void* w_hidden,
-                              void* out, int B, int H, float eps, void* stream) {
-  if (!tok || !hidden || !table || !w_emb || !w_hidden || !out || B <= 0 || H <= 0 || vocab <= 0)
+LOLLM_API int lollm_mtp_input(const int32_t* tok, long long tok_stride, const void* hidden,
+                              long long ld_hidden, const void* table, int vocab, const void* w_emb,
+                              const void* w_hidden, void* out, int B, int H, float eps, void* stream) {
+  if (!tok || !hidden || !table || !w_emb || !w_hidden || !out || B <= 0 || H <= 0 || vocab <= 0 ||
+      tok_stride < 1)
     return LOLLM_EINVAL;
   if (H % 8 || H > 8192 || ld_hidden < H || ld_hidden % 8) return LOLLM_EUNSUPPORTED;
   hipLaunchKernelGGL(mtp_input_kernel, dim3(B, 2), dim3(RMS_THREADS), 0, (hipStream_t)stream, tok,
-                     (const uint16_t*)hidden, ld_hidden, (const uint16_t*)table, vocab,
+                     tok_stride, (const uint16_t*)hidden, ld_hidden, (const uint16_t*)table, vocab,
                      (const uint16_t*)w_emb, (const uint16_t*)w_hidden, (uint16_t*)out, H, eps);
   return launch_status();
 }

@@ -46,7 +46,21 @@ constexpr int GM_P = 4;                     // weight units in flight per wave
 constexpr int GM_MAXW = 1024;               // grid limit (piece table)
 constexpr int GM_PB = 8;                    // piece loads a merge issues together
 
-enum { GM_EPI_NONE = 0, GM_EPI_SWIGLU = 1 };
+enum { GM_EPI_NONE = 0, GM_EPI_SWIGLU = 1, GM_EPI_ARGMAX = 2 };
+
+// Row argmax without the logits (lollm_gemm_argmax): each (row, 16-column n-tile) keeps
+// the packed maximum ((order key of the bf16 value) << 32 | ~column), so the highest
+// value wins and ties go to the lowest column -- the rule of the sampler's greedy rows.
+__device__ __forceinline__ uint64_t gm_key(float v, int col) {
+  const uint32_t b = f32_to_bf16(v);
+  const uint32_t o = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+  return ((uint64_t)o << 32) | (0xFFFFFFFFu - (uint32_t)col);
+}
+__device__ __forceinline__ uint64_t gm_max_xor(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m, 64), hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+  const uint64_t o = ((uint64_t)hi << 32) | lo;
+  return o > v ? o : v;
+}
 
 struct GemmArgs {
   const uint16_t* A;     // (M, K) activations, row stride lda
@@ -56,6 +70,7 @@ struct GemmArgs {
   long long lda, ldc;
   int M, N, K, G, SK, nw, epi, U;
   int rowmajor;          // piece layout: 0 = accumulator order (float4 (i, wave, lane)), 1 = row major
+  uint64_t* am;          // GM_EPI_ARGMAX: (M, N / 16) packed row maxima per n-tile
 };
 
 __device__ __forceinline__ void gm_lds_barrier() {
@@ -140,7 +155,21 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   // n-tile 4 g + wave
   auto finish = [&](int g, bool whole) {
     if (whole) {
-      if (a.epi == GM_EPI_SWIGLU) {
+      if (a.epi == GM_EPI_ARGMAX) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const int m = 16 * i + l16, col = GM_COLS * g + 16 * wave + 4 * g4;
+          uint64_t best = gm_key(acc[i][0], col);
+#pragma unroll
+          for (int j = 1; j < 4; ++j) {
+            const uint64_t k2 = gm_key(acc[i][j], col + j);
+            best = k2 > best ? k2 : best;
+          }
+          best = gm_max_xor(best, 16);
+          best = gm_max_xor(best, 32);
+          if (g4 == 0 && m < a.M) a.am[(size_t)m * (a.N / 16) + 4 * g + wave] = best;
+        }
+      } else if (a.epi == GM_EPI_SWIGLU) {
         // partner lane (g4 ^ 2) holds the other half of the same output columns
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
@@ -274,7 +303,19 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
       if (k0 + j < np) { s.x += p[j].x; s.y += p[j].y; s.z += p[j].z; s.w += p[j].w; }
   }
   // lane holds row m, tiled columns 4 g4 .. + 3 of n-tile 4 g + wave
-  if (a.epi == GM_EPI_SWIGLU) {
+  if (a.epi == GM_EPI_ARGMAX) {
+    const int col = GM_COLS * g + 16 * wave + 4 * g4;
+    const float sv[4] = {s.x, s.y, s.z, s.w};
+    uint64_t best = gm_key(sv[0], col);
+#pragma unroll
+    for (int j = 1; j < 4; ++j) {
+      const uint64_t k2 = gm_key(sv[j], col + j);
+      best = k2 > best ? k2 : best;
+    }
+    best = gm_max_xor(best, 16);
+    best = gm_max_xor(best, 32);
+    if (g4 == 0 && m < a.M) a.am[(size_t)m * (a.N / 16) + 4 * g + wave] = best;
+  } else if (a.epi == GM_EPI_SWIGLU) {
     // partner lane (g4 ^ 2) holds the up half of the same output columns
     const float o[4] = {__shfl_xor(s.x, 32, 64), __shfl_xor(s.y, 32, 64), __shfl_xor(s.z, 32, 64),
                         __shfl_xor(s.w, 32, 64)};
@@ -293,6 +334,37 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
     *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
         make_uint2((uint32_t)f32_to_bf16(s.x) | ((uint32_t)f32_to_bf16(s.y) << 16),
                    (uint32_t)f32_to_bf16(s.z) | ((uint32_t)f32_to_bf16(s.w) << 16));
+  }
+}
+
+// The argmax of each row from its (N / 16) n-tile maxima (1024 threads, four loads in
+// flight per thread); the token to out[row * stride].
+constexpr int GM_AF_THREADS = 1024;
+__global__ __launch_bounds__(GM_AF_THREADS) void gemm_argmax_final_kernel(
+    const uint64_t* __restrict__ am, int ntiles, int32_t* __restrict__ out, long long out_stride) {
+  __shared__ uint64_t red[GM_AF_THREADS / 64];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const uint64_t* rp = am + (size_t)row * ntiles;
+  uint64_t b4[4] = {0, 0, 0, 0};
+  for (int t = tid; t < ntiles; t += 4 * GM_AF_THREADS) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tt = t + u * GM_AF_THREADS;
+      const uint64_t v = tt < ntiles ? rp[tt] : 0;
+      b4[u] = v > b4[u] ? v : b4[u];
+    }
+  }
+  uint64_t best = b4[0];
+#pragma unroll
+  for (int u = 1; u < 4; ++u) best = b4[u] > best ? b4[u] : best;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) best = gm_max_xor(best, m);
+  if ((tid & 63) == 0) red[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t r = red[0];
+    for (int w = 1; w < GM_AF_THREADS / 64; ++w) r = red[w] > r ? red[w] : r;
+    out[(size_t)row * out_stride] = (int32_t)(0xFFFFFFFFu - (uint32_t)(r & 0xFFFFFFFFu));
   }
 }
 
@@ -411,7 +483,7 @@ static int gemm_grid(int grid) {
 static bool gemm_shape_ok(int M, int N, int K, int epi) {
   if (M <= 0 || M > 64 || N <= 0 || K <= 0) return false;
   if (N % GM_COLS || K % GM_KC) return false;
-  if (epi != GM_EPI_NONE && epi != GM_EPI_SWIGLU) return false;
+  if (epi != GM_EPI_NONE && epi != GM_EPI_SWIGLU && epi != GM_EPI_ARGMAX) return false;
   return true;
 }
 
@@ -455,6 +527,9 @@ static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, 
   a.M = M; a.N = N; a.K = K; a.G = N / GM_COLS; a.SK = K / GM_KC; a.nw = nw; a.epi = epilogue;
   a.U = a.G * a.SK;
   a.rowmajor = rowmajor;
+  a.am = nullptr;
+  if (epilogue == GM_EPI_ARGMAX)
+    a.am = (uint64_t*)((char*)workspace + ((gemm_ws_bytes(M, N, nw) + 255) / 256) * 256);
   switch ((M + 15) / 16) {
     case 1: hipLaunchKernelGGL(gemm_kernel<1>, dim3(nw), dim3(256), 0, st, a); break;
     case 2: hipLaunchKernelGGL(gemm_kernel<2>, dim3(nw), dim3(256), 0, st, a); break;
@@ -467,6 +542,7 @@ static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, 
 LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, long long ldc,
                          int M, int N, int K, int epilogue, void* workspace,
                          long long workspace_bytes, int grid, void* stream) {
+  if (epilogue != GM_EPI_NONE && epilogue != GM_EPI_SWIGLU) return LOLLM_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   GemmArgs a;
   int rc = gemm_main(a, A, lda, Wt, C, ldc, M, N, K, epilogue, workspace, workspace_bytes, grid, 0, st);
@@ -474,6 +550,43 @@ LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, 
   // every range a whole number of whole groups (grid divides the groups): nothing to merge
   if (a.G % a.nw == 0) return LOLLM_OK;
   hipLaunchKernelGGL(gemm_fixup_kernel, dim3(a.G, (M + 15) / 16), dim3(256), 0, st, a);
+  return launch_status();
+}
+
+// Workspace of lollm_gemm_argmax: the pieces, then the (M, N / 16) n-tile maxima.
+static long long gemm_argmax_ws_bytes(int M, int N, int nw) {
+  return (gemm_ws_bytes(M, N, nw) + 255) / 256 * 256 + (long long)M * (N / 16) * 8;
+}
+
+LOLLM_API long long lollm_gemm_argmax_workspace_bytes(int M, int N, int K, int grid) {
+  if (!gemm_shape_ok(M, N, K, GM_EPI_NONE)) return -1;
+  const int nw = gemm_grid(grid);
+  if (nw <= 0 || nw > GM_MAXW) return -1;
+  return gemm_argmax_ws_bytes(M, N, nw);
+}
+
+LOLLM_API int lollm_gemm_argmax(const void* A, long long lda, const void* Wt, int M, int N, int K,
+                                int32_t* out, long long out_stride, void* workspace,
+                                long long workspace_bytes, int grid, void* stream) {
+  if (!out || out_stride < 1) return LOLLM_EINVAL;
+  if (!gemm_shape_ok(M, N, K, GM_EPI_NONE)) return LOLLM_EUNSUPPORTED;
+  const int nw = gemm_grid(grid);
+  if (nw <= 0 || nw > GM_MAXW) return LOLLM_EUNSUPPORTED;
+  if (workspace_bytes < gemm_argmax_ws_bytes(M, N, nw)) return LOLLM_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  GemmArgs a;
+  // no output matrix: the main kernel and the merge write n-tile maxima only (C is never
+  // written in this epilogue; the workspace stands in for the pointer check)
+  int rc = gemm_main(a, A, lda, Wt, workspace, N, M, N, K, GM_EPI_ARGMAX, workspace, workspace_bytes,
+                     grid, 0, st);
+  if (rc) return rc;
+  if (a.G % a.nw) {
+    hipLaunchKernelGGL(gemm_fixup_kernel, dim3(a.G, (M + 15) / 16), dim3(256), 0, st, a);
+    rc = launch_status();
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(gemm_argmax_final_kernel, dim3(M), dim3(GM_AF_THREADS), 0, st,
+                     (const uint64_t*)a.am, N / 16, out, out_stride);
   return launch_status();
 }
 

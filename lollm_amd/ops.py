@@ -243,6 +243,31 @@ def gemm(x, tiled, N, K, epilogue=GEMM_NONE, out=None, grid=0):
     return out
 
 
+def gemm_argmax(x, tiled, N, K, out=None, grid=0):
+    """argmax over the N columns of each row of x W^T (bf16-rounded products, ties to the
+    lowest column) without writing the logits (lollm_gemm_argmax).  x (M, K) bf16 with
+    M <= 64; `tiled` from gemm_tile_weights(W, GEMM_NONE).  out: (M,) int32, rows may be
+    strided (e.g. one column of a (M, k) draft table)."""
+    M = x.numel() // K
+    if x.shape[-1] != K or M > GEMM_MAX_ROWS or M <= 0:
+        raise ValueError(f"gemm_argmax takes 1..{GEMM_MAX_ROWS} rows of {K} features")
+    x = x.contiguous()
+    _need(x, "x", torch.bfloat16)
+    _need(tiled, "tiled", torch.bfloat16, (N * K,))
+    if out is None:
+        out = torch.empty(M, dtype=torch.int32, device=x.device)
+    if out.dtype != torch.int32 or out.dim() != 1 or out.numel() != M or not out.is_cuda:
+        raise ValueError(f"out must be ({M},) int32 on the device")
+    need = _lib.lib().lollm_gemm_argmax_workspace_bytes(M, N, K, grid)
+    if need < 0:
+        raise ValueError(f"gemm_argmax does not support M={M} N={N} K={K}")
+    ws = gemm_workspace(need, x.device)
+    rc = _lib.lib().lollm_gemm_argmax(_ptr(x), K, _ptr(tiled), M, N, K, _ptr(out), out.stride(0),
+                                      _ptr(ws), ws.numel(), grid, _stream())
+    _lib.check(rc, "lollm_gemm_argmax")
+    return out
+
+
 def gemm_rmsnorm_supported(M, N, K, grid=0):
     """Whether lollm_gemm_rmsnorm takes this shape (N <= 8192 and at least one
     (64-column, 128-k) unit per workgroup)."""
@@ -366,7 +391,8 @@ def mtp_input(tok, hidden, table, w_emb, w_hidden, eps, out=None):
     table (V, H) bf16."""
     B = tok.numel()
     V, H = table.shape
-    _need(tok, "tok", torch.int32, (B,))
+    if tok.dtype != torch.int32 or tok.dim() != 1 or not tok.is_cuda:
+        raise ValueError("tok must be a (B,) int32 device tensor (rows may be strided)")
     _need(table, "table", torch.bfloat16)
     _need(w_emb, "w_emb", torch.bfloat16, (H,))
     _need(w_hidden, "w_hidden", torch.bfloat16, (H,))
@@ -378,7 +404,7 @@ def mtp_input(tok, hidden, table, w_emb, w_hidden, eps, out=None):
     if out is None:
         out = torch.empty(B, 2 * H, dtype=torch.bfloat16, device=table.device)
     _need(out, "out", torch.bfloat16, (B, 2 * H))
-    rc = _lib.lib().lollm_mtp_input(_ptr(tok), _ptr(hidden), hidden.stride(0), _ptr(table), V,
+    rc = _lib.lib().lollm_mtp_input(_ptr(tok), tok.stride(0), _ptr(hidden), hidden.stride(0), _ptr(table), V,
                                     _ptr(w_emb), _ptr(w_hidden), _ptr(out), B, H, float(eps),
                                     _stream())
     _lib.check(rc, "lollm_mtp_input")

@@ -181,14 +181,20 @@ class SpecDecoder:
         for j in range(1, k + 1):
             m, normed = mtp._block(h, None, self.mkc, self.mvc, self.mtp_len[j - 1],
                                    self.mtp_len[j], self.mtp_len[j], self.mtp_ws, tok=tok)
-            lg = model.lm_head(normed).view(B, -1)
+            lm = model.lm_head
             if self.draft_mode == "sample":
+                lg = lm(normed).view(B, -1)
                 self.draft_logits[:, j - 1].copy_(lg)
                 d = ops.sample_rows(lg, self.temperature, self.top_k, self.top_p, self.seed, 0,
                                     slot=k + 1 + j, offset_dev=self.offset, workspace=self.row_ws)
+                self.drafts[:, j - 1].copy_(d)
+            elif lm.tiled is not None and B <= ops.GEMM_MAX_ROWS:
+                # greedy draft straight from the lm_head GEMM (no logits), into its column
+                d = ops.gemm_argmax(normed.reshape(B, -1), lm.tiled, lm.N, lm.K,
+                                    out=self.drafts[:, j - 1])
             else:
-                d = ops.sample_rows(lg, 0.0, workspace=self.row_ws)
-            self.drafts[:, j - 1].copy_(d)
+                d = ops.sample_rows(lm(normed).view(B, -1), 0.0, workspace=self.row_ws)
+                self.drafts[:, j - 1].copy_(d)
             tok, h = d, m
 
     @torch.no_grad()

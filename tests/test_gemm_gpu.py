@@ -143,3 +143,44 @@ def test_gemm_rmsnorm_rejects_unsupported():
                                   st) == 2
     assert lib.lollm_gemm_rmsnorm(p, 128, p, 1, 8256, 128, p, p, 1e-6, p, p, p, p, buf.numel(), 1,
                                   st) == 2
+
+
+@pytest.mark.parametrize("M", [1, 16, 17, 64])
+@pytest.mark.parametrize("N,K,grid", [(2048, 256, 0), (8256, 512, 0), (1024, 128, 16), (4096, 384, 7)])
+def test_gemm_argmax_equals_gemm_then_greedy(M, N, K, grid):
+    """lollm_gemm_argmax (the greedy draft pick fused into the lm_head GEMM, mtp.py:138)
+    returns exactly the token lollm_gemm + the greedy lollm_sample_rows return: the same
+    bf16-rounded products, ties to the lowest column -- with every group whole in one
+    workgroup (grid 16 over 16 groups) and with groups cut and merged."""
+    from lollm_amd import ops
+    print(f"case gemm_argmax M={M} N={N} K={K} grid={grid}", flush=True)
+    x, W = case(M, N, K, 11 * M + N)
+    W = W.cuda()
+    t = ops.gemm_tile_weights(W, ops.GEMM_NONE)
+    xd = x.cuda()
+    logits = ops.gemm(xd, t, N, K, grid=grid)
+    ref = ops.sample_rows(logits, 0.0)
+    got = ops.gemm_argmax(xd, t, N, K, grid=grid)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), ref.cpu())
+    assert torch.equal(got.cpu().long(), logits.float().cpu().argmax(-1))
+
+
+def test_gemm_argmax_ties_and_strided_out():
+    """Equal columns: the lowest index wins; the token lands in one column of a (M, k)
+    table (row stride k), the others untouched."""
+    from lollm_amd import ops
+    M, N, K, k = 5, 1024, 256, 3
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).bfloat16()
+    best = (x.float() @ W.float().t()).argmax(-1)
+    for r in range(M):                       # duplicate each row's winner at a higher column
+        W[(int(best[r]) + 517) % N] = W[int(best[r])]
+    t = ops.gemm_tile_weights(W.cuda(), ops.GEMM_NONE)
+    table = torch.full((M, k), -7, dtype=torch.int32, device="cuda")
+    ops.gemm_argmax(x.cuda(), t, N, K, out=table[:, 1])
+    ref = ops.sample_rows(ops.gemm(x.cuda(), t, N, K), 0.0)
+    torch.cuda.synchronize()
+    assert torch.equal(table[:, 1].cpu(), ref.cpu())
+    assert bool((table[:, 0] == -7).all()) and bool((table[:, 2] == -7).all())
