@@ -168,6 +168,19 @@ int lollm_attn_prologue(const void* qkv, const void* q_norm_w, const void* k_nor
                         int Hkv, int D, int rotary_dim, float eps, void* q_out, void* gate_out,
                         void* k_cache, void* v_cache, int max_len, void* stream);
 
+/* Gated attention of one new token per sequence over a short cache, prologue fused
+ * (GatedAttention.forward, blocks.py:208-235, for the MTP head's draft block with the
+ * chain's per-step cache, mtp.py:61-73): from the fused qkv (B, Hq*2D + 2*Hkv*D) of the
+ * token, the new k / v are formed and appended at row lengths[b] exactly as
+ * lollm_attn_prologue does, then out (B, Hq*D) bf16 = softmax(q k^T scale) v *
+ * sigmoid(gate) over the first kv_len[b] cache rows, with lollm_attn_verify's arithmetic
+ * up to the order of the dot-product sums.  rope_pos as in lollm_attn_prologue.
+ * Supported: D == 256, max_len <= 16, Hq / Hkv <= 16. */
+int lollm_attn_small(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                     const float* inv_freq, const int32_t* lengths, const int32_t* rope_pos,
+                     const int32_t* kv_len, int B, int Hq, int Hkv, int D, int rotary_dim, float eps,
+                     float scale, void* k_cache, void* v_cache, int max_len, void* out, void* stream);
+
 /* Few-row weight GEMM: y = x W^T for x with M <= 64 rows (the verify pass over
  * B x (1 + k) positions, the draft pass over B), bf16 in / fp32 accumulate / bf16 out.
  *

@@ -46,6 +46,8 @@ SIGNATURES = {
     "lollm_gemm_argmax": ([_P, ctypes.c_longlong, _P, _I, _I, _I, _P, ctypes.c_longlong, _P,
                            ctypes.c_longlong, _I, _P], _I),
     "lollm_swiglu": ([_P, _P, _I, _I, _P], _I),
+    "lollm_attn_small": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P, _P, _I, _P,
+                          _P], _I),
     "lollm_attn_prologue": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P,
                              _I, _P], _I),
     "lollm_gdn_layer": ([_P, ctypes.c_longlong, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P,

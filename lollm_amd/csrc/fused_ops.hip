@@ -135,6 +135,30 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
 // One 256-thread workgroup per (token, head slot): slots [0, Hq) are query heads,
 // [Hq, Hq + Hkv) key heads, [Hq + Hkv, Hq + 2 Hkv) value heads.  D == 256: one
 // element per thread.
+// QK-norm (1 + w) of one 256-value head vector (thread d holds x) followed by the partial
+// rotate-half RoPE at position rpos (blocks.py:166-183,221-227); returns thread d's output,
+// a bf16 value.  Shared by the prologue and the short-cache attention so both give the
+// same bits.  (red and xs are reused by the next call only after the barriers inside
+// block_sum_f.)
+__device__ __forceinline__ float qk_norm_rope(float x, float wv, const float* __restrict__ inv_freq,
+                                              int rpos, int rd, float eps, float* red, float* xs) {
+  constexpr int D = 256;
+  const int d = threadIdx.x;
+  const float r = rsqrtf(block_sum_f<256>(x * x, red) / (float)D + eps);
+  const float xn = round_bf16(x * r * (1.f + wv));  // QK-norm output (bf16 tensor)
+  xs[d] = xn;
+  __syncthreads();
+  float y = xn;
+  if (d < rd) {
+    const int half = rd / 2, i = d % half;
+    const float ang = (float)rpos * inv_freq[i];
+    const float c = round_bf16(cosf(ang)), s = round_bf16(sinf(ang));
+    const float rot = d < half ? -xs[d + half] : xs[d - half];
+    y = round_bf16(round_bf16(xn * c) + round_bf16(rot * s));
+  }
+  return y;
+}
+
 __global__ __launch_bounds__(256) void attn_prologue_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, const float* __restrict__ inv_freq,
@@ -160,25 +184,127 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
   const bool is_q = slot < Hq;
   const uint16_t* xin = is_q ? src + (long long)slot * 2 * D : src + (long long)Hq * 2 * D + (slot - Hq) * D;
   if (is_q) gate_out[((long long)bt * Hq + slot) * D + d] = src[(long long)slot * 2 * D + D + d];
-  const float x = bf16_to_f32(xin[d]);
-  const float r = rsqrtf(block_sum_f<256>(x * x, red) / (float)D + eps);
-  const float wv = bf16_to_f32((is_q ? qn_w : kn_w)[d]);
-  const float xn = round_bf16(x * r * (1.f + wv));  // QK-norm output (bf16 tensor)
-  xs[d] = xn;
-  __syncthreads();
-  float y = xn;
-  if (d < rd) {
-    const int half = rd / 2, i = d % half;
-    const float ang = (float)rpos * inv_freq[i];
-    const float c = round_bf16(cosf(ang)), s = round_bf16(sinf(ang));
-    const float rot = d < half ? -xs[d + half] : xs[d - half];
-    y = round_bf16(round_bf16(xn * c) + round_bf16(rot * s));
-  }
+  const float y = qk_norm_rope(bf16_to_f32(xin[d]), bf16_to_f32((is_q ? qn_w : kn_w)[d]), inv_freq,
+                               rpos, rd, eps, red, xs);
   if (is_q) {
     q_out[((long long)bt * Hq + slot) * D + d] = f32_to_bf16(y);
   } else if (pos >= 0 && pos < max_len) {
     const int kvh = slot - Hq;
     kc[(((long long)b * Hkv + kvh) * max_len + pos) * D + d] = f32_to_bf16(y);
+  }
+}
+
+// Gated attention of one new token over a short cache (the MTP head's draft block:
+// src/qwen3_5/mtp.py:61-73 with the chain's per-step cache) with the prologue fused:
+// workgroup (sequence b, kv head) forms the new k (QK-norm + RoPE) and v, appends them at
+// row lengths[b], forms its n_rep query heads and their gates exactly as the prologue
+// does, then, one wave per query head, scores the first kv_len[b] rows (dot products in
+// fp32, lane = 4 of the 256 dims), p = exp2(s c - max c) with c = scale log2(e),
+// l = sum p, o = sum bf16(p) v / l, out = o sigmoid(gate) -- the arithmetic of the
+// split-K kernel up to the order of the dot-product sums (blocks.py:208-235).
+constexpr int AS_MAXL = 16;     // cache rows
+constexpr int AS_MAXREP = 16;   // query heads per kv head
+
+__device__ __forceinline__ float as_sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
+
+__global__ __launch_bounds__(256) void attn_small_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qn_w,
+    const uint16_t* __restrict__ kn_w, const float* __restrict__ inv_freq,
+    const int32_t* __restrict__ lengths, const int32_t* __restrict__ rope_pos,
+    const int32_t* __restrict__ kv_len, int Hq, int Hkv, int rd, float eps, float cl2,
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int max_len, uint16_t* __restrict__ out) {
+  constexpr int D = 256;
+  __shared__ float red[4];
+  __shared__ float xs[D];
+  __shared__ float knew[D], vnew[D];
+  __shared__ float qsh[AS_MAXREP][D], gsh[AS_MAXREP][D];
+  const int b = blockIdx.x, kvh = blockIdx.y, d = threadIdx.x;
+  const int lane = d & 63, wave = d >> 6;
+  const int n_rep = Hq / Hkv;
+  const long long row_w = (long long)Hq * 2 * D + 2LL * Hkv * D;
+  const uint16_t* src = qkv + (long long)b * row_w;
+  const int pos = lengths[b];
+  const int rpos = rope_pos ? rope_pos[b] : pos;
+  const size_t cbase = ((size_t)b * Hkv + kvh) * max_len;
+  {
+    const float y = qk_norm_rope(bf16_to_f32(src[(long long)Hq * 2 * D + kvh * D + d]),
+                                 bf16_to_f32(kn_w[d]), inv_freq, rpos, rd, eps, red, xs);
+    const uint16_t yb = f32_to_bf16(y), vb = src[(long long)Hq * 2 * D + Hkv * D + kvh * D + d];
+    knew[d] = bf16_to_f32(yb);
+    vnew[d] = bf16_to_f32(vb);
+    if (pos >= 0 && pos < max_len) {
+      kc[(cbase + pos) * D + d] = yb;
+      vc[(cbase + pos) * D + d] = vb;
+    }
+  }
+  for (int hr = 0; hr < n_rep; ++hr) {
+    const int h = kvh * n_rep + hr;
+    qsh[hr][d] = qk_norm_rope(bf16_to_f32(src[(long long)h * 2 * D + d]), bf16_to_f32(qn_w[d]),
+                              inv_freq, rpos, rd, eps, red, xs);
+    gsh[hr][d] = bf16_to_f32(src[(long long)h * 2 * D + D + d]);
+  }
+  __syncthreads();
+  int L = kv_len[b];
+  L = L < 0 ? 0 : (L > max_len ? max_len : L);
+  for (int hr = wave; hr < n_rep; hr += 4) {
+    float q4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q4[e] = qsh[hr][4 * lane + e];
+    float sc[AS_MAXL];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < AS_MAXL; ++j) {
+      sc[j] = -INFINITY;
+      if (j < L) {
+        float kv4[4];
+        if (j == pos) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) kv4[e] = knew[4 * lane + e];
+        } else {
+          const uint2 u = *reinterpret_cast<const uint2*>(kc + (cbase + j) * D + 4 * lane);
+          kv4[0] = __uint_as_float(u.x << 16); kv4[1] = __uint_as_float(u.x & 0xffff0000u);
+          kv4[2] = __uint_as_float(u.y << 16); kv4[3] = __uint_as_float(u.y & 0xffff0000u);
+        }
+        float dot = q4[0] * kv4[0];
+#pragma unroll
+        for (int e = 1; e < 4; ++e) dot = fmaf(q4[e], kv4[e], dot);
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) dot += __shfl_xor(dot, o, 64);
+        sc[j] = dot;
+        m = fmaxf(m, dot);
+      }
+    }
+    const float base = m * cl2;
+    float l = 0.f, o4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < AS_MAXL; ++j) {
+      if (j < L) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j], cl2, -base));
+        l += p;
+        const float pb = round_bf16(p);
+        float vv4[4];
+        if (j == pos) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vv4[e] = vnew[4 * lane + e];
+        } else {
+          const uint2 u = *reinterpret_cast<const uint2*>(vc + (cbase + j) * D + 4 * lane);
+          vv4[0] = __uint_as_float(u.x << 16); vv4[1] = __uint_as_float(u.x & 0xffff0000u);
+          vv4[2] = __uint_as_float(u.y << 16); vv4[3] = __uint_as_float(u.y & 0xffff0000u);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[e] = fmaf(pb, vv4[e], o4[e]);
+      }
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int h = kvh * n_rep + hr;
+    uint32_t ow[2];
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) {
+      const float y0 = o4[e] * inv * as_sigmoid(gsh[hr][4 * lane + e]);
+      const float y1 = o4[e + 1] * inv * as_sigmoid(gsh[hr][4 * lane + e + 1]);
+      ow[e >> 1] = (uint32_t)f32_to_bf16(y0) | ((uint32_t)f32_to_bf16(y1) << 16);
+    }
+    *reinterpret_cast<uint2*>(out + ((size_t)b * Hq + h) * D + 4 * lane) = make_uint2(ow[0], ow[1]);
   }
 }
 
@@ -263,6 +389,26 @@ LOLLM_API int lollm_attn_prologue(const void* qkv, const void* q_norm_w, const v
                      rotary_dim, eps,
                      (uint16_t*)q_out, (uint16_t*)gate_out, (uint16_t*)k_cache,
                      (uint16_t*)v_cache, max_len);
+  return launch_status();
+}
+
+LOLLM_API int lollm_attn_small(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                               const float* inv_freq, const int32_t* lengths,
+                               const int32_t* rope_pos, const int32_t* kv_len, int B, int Hq,
+                               int Hkv, int D, int rotary_dim, float eps, float scale,
+                               void* k_cache, void* v_cache, int max_len, void* out,
+                               void* stream) {
+  if (!qkv || !q_norm_w || !k_norm_w || !lengths || !kv_len || !k_cache || !v_cache || !out)
+    return LOLLM_EINVAL;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || max_len <= 0) return LOLLM_EINVAL;
+  if (D != 256 || rotary_dim < 0 || rotary_dim > D || rotary_dim % 2) return LOLLM_EUNSUPPORTED;
+  if (max_len > AS_MAXL || Hq / Hkv > AS_MAXREP) return LOLLM_EUNSUPPORTED;
+  if (rotary_dim > 0 && !inv_freq) return LOLLM_EINVAL;
+  hipLaunchKernelGGL(attn_small_kernel, dim3(B, Hkv), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)qkv, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w,
+                     inv_freq, lengths, rope_pos, kv_len, Hq, Hkv, rotary_dim, eps,
+                     scale * 1.4426950408889634f, (uint16_t*)k_cache, (uint16_t*)v_cache, max_len,
+                     (uint16_t*)out);
   return launch_status();
 }
 

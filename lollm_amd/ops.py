@@ -464,6 +464,35 @@ def attn_prologue(qkv, q_norm_w, k_norm_w, inv_freq, lengths, B, T, Hq, Hkv, D, 
     return q_out, gate_out
 
 
+ATTN_SMALL_MAXL = 16
+
+
+def attn_small(qkv, q_norm_w, k_norm_w, inv_freq, lengths, kv_len, B, Hq, Hkv, D, rotary_dim, eps,
+               k_cache, v_cache, rope_pos=None, scale=None, out=None):
+    """One new token per sequence attending over a cache of at most ATTN_SMALL_MAXL rows,
+    with the prologue fused (lollm_attn_small).  qkv (B, Hq*2D + 2*Hkv*D) bf16; caches
+    (B, Hkv, max_len, D).  Returns (B, 1, Hq*D) bf16."""
+    _need(qkv, "qkv", torch.bfloat16)
+    if qkv.numel() != B * (Hq * 2 * D + 2 * Hkv * D):
+        raise ValueError("qkv has the wrong size")
+    _need(lengths, "lengths", torch.int32, (B,))
+    _need(kv_len, "kv_len", torch.int32, (B,))
+    _need(k_cache, "k_cache", torch.bfloat16)
+    _need(v_cache, "v_cache", torch.bfloat16, tuple(k_cache.shape))
+    max_len = k_cache.shape[2]
+    if scale is None:
+        scale = D ** -0.5
+    if out is None:
+        out = torch.empty(B, 1, Hq * D, dtype=torch.bfloat16, device=qkv.device)
+    _need(out, "out", torch.bfloat16, (B, 1, Hq * D))
+    rc = _lib.lib().lollm_attn_small(
+        _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(inv_freq), _ptr(lengths), _ptr(rope_pos),
+        _ptr(kv_len), B, Hq, Hkv, D, rotary_dim, float(eps), float(scale), _ptr(k_cache),
+        _ptr(v_cache), max_len, _ptr(out), _stream())
+    _lib.check(rc, "lollm_attn_small")
+    return out
+
+
 GDN_CHUNK_MIN_T = 64
 
 

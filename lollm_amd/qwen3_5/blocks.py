@@ -223,6 +223,12 @@ class GatedAttention:
         B, T, _ = x.shape
         cfg = self.cfg
         qkv = self.qkv(x)
+        if T == 1 and k_cache.shape[2] <= ops.ATTN_SMALL_MAXL:
+            # one token over a short cache (the MTP head's draft block): prologue fused
+            return ops.attn_small(qkv, self.q_norm, self.k_norm, self.inv_freq, lengths, kv_len, B,
+                                  cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
+                                  cfg.rotary_dim, cfg.rms_norm_eps, k_cache, v_cache,
+                                  rope_pos=rope_pos)
         q, gate = ops.attn_prologue(qkv, self.q_norm, self.k_norm, self.inv_freq, lengths, B, T,
                                     cfg.num_attention_heads, cfg.num_key_value_heads,
                                     cfg.head_dim, cfg.rotary_dim, cfg.rms_norm_eps, k_cache,

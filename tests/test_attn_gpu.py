@@ -108,3 +108,41 @@ def test_attn_workspace_is_validated():
     with pytest.raises(RuntimeError):
         ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda(), grid=8,
                         workspace=small)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,rd,lens,rope", [(4, 32, 4, 64, [1, 2, 3, 3], False),
+                                                  (3, 16, 2, 128, [1, 9, 16], True),
+                                                  (2, 8, 8, 0, [5, 1], False)])
+def test_attn_small_equals_prologue_then_verify(B, Hq, Hkv, rd, lens, rope):
+    """lollm_attn_small (one token over a cache of at most 16 rows, prologue fused: the
+    MTP head's draft block) against lollm_attn_prologue + lollm_attn_verify on the same
+    qkv row and cache: the appended k / v rows bit for bit, the gated output within one
+    bf16 rounding (the two differ only in the order of the dot-product sums), and both
+    against the oracle's fp32 attention of the prologue's q."""
+    from lollm_amd import ops
+    print(f"case attn_small B={B} Hq={Hq} Hkv={Hkv} lens={lens}", flush=True)
+    gen = torch.Generator().manual_seed(sum(lens) + Hq)
+    max_len = 16
+    qkv = torch.randn(B, 1, Hq * 2 * D + 2 * Hkv * D, generator=gen).bfloat16().cuda()
+    qn = (0.1 * torch.randn(D, generator=gen)).bfloat16().cuda()
+    kn = (0.1 * torch.randn(D, generator=gen)).bfloat16().cuda()
+    inv_freq = (1.0 / (1e7 ** (torch.arange(0, max(rd, 2), 2).float() / max(rd, 2)))).cuda()
+    kv_len = torch.tensor(lens, dtype=torch.int32).cuda()
+    lengths = kv_len - 1                        # the new token goes to row kv_len - 1
+    rope_pos = (kv_len + 3).int() if rope else None
+    kc0 = torch.randn(B, Hkv, max_len, D, generator=gen).bfloat16().cuda()
+    vc0 = torch.randn(B, Hkv, max_len, D, generator=gen).bfloat16().cuda()
+    kc1, vc1 = kc0.clone(), vc0.clone()
+    got = ops.attn_small(qkv, qn, kn, inv_freq, lengths, kv_len, B, Hq, Hkv, D, rd, 1e-6, kc1, vc1,
+                         rope_pos=rope_pos)
+    kc2, vc2 = kc0.clone(), vc0.clone()
+    q, gate = ops.attn_prologue(qkv, qn, kn, inv_freq, lengths, B, 1, Hq, Hkv, D, rd, 1e-6, kc2, vc2,
+                                rope_pos=rope_pos)
+    ref = ops.attn_verify(q, kc2, vc2, kv_len, gate)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1.cpu(), kc2.cpu()) and torch.equal(vc1.cpu(), vc2.cpu())
+    g32, r32 = got.float().cpu(), ref.float().cpu()
+    torch.testing.assert_close(g32, r32, rtol=1e-2, atol=1e-2)
+    assert (g32 != r32).float().mean().item() <= 0.02
+    o = oracle(q.cpu(), kc2.cpu(), vc2.cpu(), kv_len.cpu(), gate.cpu())
+    torch.testing.assert_close(g32.view(B, -1), o.view(B, -1), **TOL)
