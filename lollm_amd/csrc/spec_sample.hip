@@ -20,12 +20,15 @@
 // -ffp-contract=off.
 //
 // Kernels:
-//   row_stats    one 1024-thread workgroup per row, ONE pass over HBM: the row is
-//                held in registers (19 x 16 B per thread covers V <= 155648; larger
-//                rows re-read the tail), giving the max key (packed 16-bit order keys,
-//                two tokens per max), then a per-key count histogram over the NBINS
-//                keys below the max in LDS and block scans for the top-k / top-p cut
-//                points and the kept mass Z;
+//   row_stats    one 1024-thread workgroup per row (target and draft rows in one
+//                launch), ONE pass over HBM: the row is held in registers (19 x 16 B per
+//                thread covers V <= 155648; larger rows re-read the tail), giving the
+//                max key (a packed signed 16-bit max of the raw bits, one op per two
+//                tokens; rows with no logit >= +0 take the order-key max), then a per-key
+//                count histogram over the NBINS keys below the max in LDS (distances
+//                computed two tokens at a time in packed 16-bit arithmetic; without top-k,
+//                tokens whose weight test fails are not counted) and block scans for the
+//                top-k / top-p cut points and the kept mass Z;
 //   argmax_*     greedy rows: the row split over 16 workgroups, partial maxima
 //                merged by a second tiny kernel (a greedy row needs no histogram);
 //   spec_partial / spec_final  the k accept tests in parallel, then the residual or
@@ -33,13 +36,15 @@
 //                weights over ns contiguous vocabulary slices, then one workgroup per
 //                sequence locates the slice holding the target and the token in it;
 //   sample_rows  one draw per row.
-// A draw is an inverse CDF over token ids in two steps: every wave of the block
-// sums the weights of its own contiguous sixteenth of the row (coalesced, one pass,
-// exact integers), then the one wave whose segment holds the target walks it again
-// with wave-level scans.  A token's weight depends only on its key's distance below
-// the row maximum, so each draw first fills an LDS table of the NBINS weights (the
-// same weight_of) and then reads one entry per token.  Residual masses are 64-bit
-// when q is one-hot (argmax drafts) and 128-bit when q is a sampled distribution.
+// A draw is an inverse CDF over token ids in three steps: every wave of the block sums
+// the weights of its own contiguous sixteenth of the range (coalesced, exact integers,
+// the next 2-4 chunks per lane in flight), the sixteenth holding the target is summed
+// again split over the 16 waves, and the one wave whose part holds the target walks it
+// with wave-level scans.  A token's weight depends only on its key's distance below the
+// row maximum (computed two tokens at a time in packed 16-bit arithmetic), so each draw
+// first fills an LDS table of the weights of the distances within the cut (the same
+// weight_of) and reads an entry only for tokens within the cut.  Residual masses are 64-bit when q is
+// one-hot (argmax drafts) and 128-bit when q is a sampled distribution.
 #include "common.h"
 
 #include <algorithm>
@@ -125,18 +130,12 @@ __device__ __forceinline__ uint64_t token_weight(const RowStat& s, float c, uint
 }
 
 // Weight table of a row's distribution: tab[d] = the weight of a token whose key is d
-// below the row's maximum key (zero past the cut) -- token_weight as a lookup.
+// below the row's maximum key, filled for d <= cut only (the only entries read).
 __device__ void build_table(const RowStat& s, float c, uint64_t* tab) {
+  if (s.greedy) return;
   const float xmax = key_value(s.kmax);
-  for (int d = threadIdx.x; d < SP_NBINS; d += blockDim.x)
-    tab[d] = (!s.greedy && d <= s.cut) ? weight_of(key_value(s.kmax - d), xmax, c) : 0;
-}
-
-__device__ __forceinline__ uint64_t table_weight(const RowStat& s, const uint64_t* tab,
-                                                 uint32_t b, int32_t tok) {
-  if (s.greedy) return tok == s.argmax ? 1u : 0u;
-  const uint32_t d = (uint32_t)(s.kmax - skey(b));   // >= 0: kmax is the row maximum
-  return d < (uint32_t)SP_NBINS ? tab[d] : 0;
+  for (int d = threadIdx.x; d <= s.cut; d += blockDim.x)
+    tab[d] = weight_of(key_value(s.kmax - d), xmax, c);
 }
 
 // Order keys of the two bf16 in a word, packed (ord16 per half).
@@ -146,9 +145,52 @@ __device__ __forceinline__ uint32_t ord_pair(uint32_t w) {
 }
 
 typedef unsigned short sp_us2 __attribute__((ext_vector_type(2)));
+typedef short sp_s2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(sp_us2, a),
                                                                 __builtin_bit_cast(sp_us2, b)));
+}
+
+// Signed 16-bit maximum of the raw bf16 halves: for non-negative bf16 the bit pattern
+// orders like the value, and every negative pattern is below every non-negative one.
+__device__ __forceinline__ sp_s2 max_s16x2(sp_s2 m, uint32_t w) {
+  return __builtin_elementwise_max(m, __builtin_bit_cast(sp_s2, w));
+}
+
+// Distances below the row's maximum key, kmax - skey(b), of the two bf16 of w as 16-bit
+// halves (every bf16 pattern gives a distance in [0, 2^16)).  km2 holds kmax mod 2^16 in
+// both halves.  With s = 0 / -1 the sign mask and m = max(|b| - SP_MAG0, 0):
+// skey = s ? -m : m, so kmax - skey = (kmax + s) - (m ^ s) modulo 2^16.
+__device__ __forceinline__ uint32_t dist_pair(uint32_t w, uint32_t km2) {
+  const sp_us2 s = __builtin_bit_cast(sp_us2, __builtin_bit_cast(sp_s2, w) >> (short)15);
+  const sp_us2 mag = __builtin_bit_cast(sp_us2, w & 0x7FFF7FFFu);
+  const sp_us2 m = __builtin_elementwise_sub_sat(mag, (sp_us2)((unsigned short)SP_MAG0));
+  const sp_us2 d = (__builtin_bit_cast(sp_us2, km2) + s) - (m ^ s);
+  return __builtin_bit_cast(uint32_t, d);
+}
+
+// The weights of the two tokens of word w (tokens t0, t0 + 1) under a row's distribution
+// (token_weight as a lookup): the table entry of each token's distance below the
+// maximum, read only for distances within the cut (every other token weighs 0).
+__device__ __forceinline__ void pair_weights(const RowStat& s, const uint64_t* tab, uint32_t w,
+                                             int t0, uint64_t& w0, uint64_t& w1) {
+  if (s.greedy) {
+    w0 = t0 == s.argmax ? 1u : 0u;
+    w1 = t0 + 1 == s.argmax ? 1u : 0u;
+    return;
+  }
+  const uint32_t dd = dist_pair(w, ((uint32_t)s.kmax & 0xFFFFu) * 0x10001u);
+  const int32_t d0 = (int32_t)(dd & 0xFFFFu), d1 = (int32_t)(dd >> 16);
+  w0 = d0 <= s.cut ? tab[d0] : 0;
+  w1 = d1 <= s.cut ? tab[d1] : 0;
+}
+
+__device__ __forceinline__ void chunk_weights(const RowStat& s, const uint64_t* tab,
+                                              const u32x4_t& u, int ch, uint64_t* w) {
+  pair_weights(s, tab, u.x, ch * 8, w[0], w[1]);
+  pair_weights(s, tab, u.y, ch * 8 + 2, w[2], w[3]);
+  pair_weights(s, tab, u.z, ch * 8 + 4, w[4], w[5]);
+  pair_weights(s, tab, u.w, ch * 8 + 6, w[6], w[7]);
 }
 
 // bf16 bits of an order key (inverse of ord16)
@@ -270,18 +312,24 @@ __device__ __forceinline__ void scan_chunk(uint4 u, int c, uint64_t& best, int32
   }
 }
 
-__device__ __forceinline__ void hist_chunk(uint4 u, int32_t km, uint32_t* hist) {
+// Counts of the 8 tokens of a chunk by distance below the maximum key; only distances
+// <= dlim (< SP_NBINS) are counted.
+__device__ __forceinline__ void hist_chunk(uint4 u, uint32_t km2, int32_t dlim, uint32_t* hist) {
   const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t b = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-    const int32_t d = km - skey(b);
-    if (d < SP_NBINS) atomicAdd(&hist[d], 1u);
+  for (int h = 0; h < 4; ++h) {
+    const uint32_t dd = dist_pair(w[h], km2);
+    const int32_t d0 = (int32_t)(dd & 0xFFFFu), d1 = (int32_t)(dd >> 16);
+    if (d0 <= dlim) atomicAdd(&hist[d0], 1u);
+    if (d1 <= dlim) atomicAdd(&hist[d1], 1u);
   }
 }
 
-// Sampled rows only (inv_temp > 0); greedy rows take the split argmax below.
-__global__ __launch_bounds__(SP_THREADS) void row_stats_kernel(const uint16_t* __restrict__ logits,
+// Sampled rows only (inv_temp > 0); greedy rows take the split argmax below.  Rows
+// [0, rows0) are read from x0, the rest from x1 (target and draft rows in one launch).
+__global__ __launch_bounds__(SP_THREADS) void row_stats_kernel(const uint16_t* __restrict__ x0,
+                                                               int rows0,
+                                                               const uint16_t* __restrict__ x1,
                                                                int V, float inv_temp, int top_k,
                                                                float top_p, RowStat* stats) {
   __shared__ uint32_t hist[SP_NBINS];
@@ -291,49 +339,91 @@ __global__ __launch_bounds__(SP_THREADS) void row_stats_kernel(const uint16_t* _
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
   const int nch = V >> 3;
-  const uint4* x4 = reinterpret_cast<const uint4*>(logits + (size_t)row * V);
+  const uint16_t* src = row < rows0 ? x0 + (size_t)row * V : x1 + (size_t)(row - rows0) * V;
+  const uint4* x4 = reinterpret_cast<const uint4*>(src);
   // ---- the row into registers (one HBM pass); zero the histogram meanwhile ----
   uint4 reg[SP_REG];
 #pragma unroll
   for (int i = 0; i < SP_REG; ++i) {
     const int c = i * SP_THREADS + tid;
-    reg[i] = c < nch ? x4[c] : make_uint4(0, 0, 0, 0);
+    reg[i] = c < nch ? x4[c] : make_uint4(0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u);
   }
   for (int i = tid; i < SP_NBINS; i += SP_THREADS) hist[i] = 0;
-  // ---- the maximum order key, two bf16 at a time ----
-  uint32_t m2 = 0;
+  // ---- the maximum: signed 16-bit maximum of the raw halves (one packed op per two
+  //      tokens; padding is -0, the lowest pattern of that order) ----
+  sp_s2 mraw = {(short)-32768, (short)-32768};
 #pragma unroll
   for (int i = 0; i < SP_REG; ++i) {
-    const int c = i * SP_THREADS + tid;
-    if (c < nch) {
-      m2 = max_u16x2(m2, ord_pair(reg[i].x));
-      m2 = max_u16x2(m2, ord_pair(reg[i].y));
-      m2 = max_u16x2(m2, ord_pair(reg[i].z));
-      m2 = max_u16x2(m2, ord_pair(reg[i].w));
-    }
+    mraw = max_s16x2(mraw, reg[i].x);
+    mraw = max_s16x2(mraw, reg[i].y);
+    mraw = max_s16x2(mraw, reg[i].z);
+    mraw = max_s16x2(mraw, reg[i].w);
   }
   for (int c = SP_REG * SP_THREADS + tid; c < nch; c += SP_THREADS) {
     const uint4 u = x4[c];
-    m2 = max_u16x2(max_u16x2(m2, ord_pair(u.x)), max_u16x2(ord_pair(u.y), max_u16x2(ord_pair(u.z), ord_pair(u.w))));
+    mraw = max_s16x2(max_s16x2(max_s16x2(max_s16x2(mraw, u.x), u.y), u.z), u.w);
   }
-  const uint32_t omax = (uint32_t)block_max<uint64_t>((uint64_t)max((m2 & 0xFFFFu), (m2 >> 16)), s64);
+  const int32_t mx =
+      (int32_t)block_max<uint64_t>((uint64_t)(max((int32_t)mraw.x, (int32_t)mraw.y) + 32768), s64) -
+      32768;
+  uint32_t top_bits = (uint32_t)mx;
+  if (mx < 0) {
+    // no logit is >= +0: the maximum in the full order of the keys (packed order keys,
+    // two tokens per max)
+    uint32_t m2 = 0;
+#pragma unroll
+    for (int i = 0; i < SP_REG; ++i) {
+      const int c = i * SP_THREADS + tid;
+      if (c < nch) {
+        m2 = max_u16x2(m2, ord_pair(reg[i].x));
+        m2 = max_u16x2(m2, ord_pair(reg[i].y));
+        m2 = max_u16x2(m2, ord_pair(reg[i].z));
+        m2 = max_u16x2(m2, ord_pair(reg[i].w));
+      }
+    }
+    for (int c = SP_REG * SP_THREADS + tid; c < nch; c += SP_THREADS) {
+      const uint4 u = x4[c];
+      m2 = max_u16x2(max_u16x2(m2, ord_pair(u.x)), max_u16x2(ord_pair(u.y), max_u16x2(ord_pair(u.z), ord_pair(u.w))));
+    }
+    top_bits = ord_bits((uint32_t)block_max<uint64_t>((uint64_t)max((m2 & 0xFFFFu), (m2 >> 16)), s64));
+  }
   RowStat st;
   st.greedy = 0;
   st.argmax = -1;   // only greedy rows use it
-  const int32_t km = skey(ord_bits(omax));   // skey is monotone in the order key
+  const int32_t km = skey(top_bits);
   st.kmax = km;
+  const float xmax = key_value(km);
+  const float c = inv_temp * 1.44269504088896341f;
+  // ---- which distances need counting: all below SP_NBINS when top-k reads the counts;
+  //      without top-k only the mass (count x weight) is read, so distances whose weight
+  //      test t = (x - xmax) c >= -40 fails (weight 0) are skipped.  t does not increase
+  //      with the distance, so those distances are a suffix: bisect for its start over
+  //      the distances of real keys (skey >= -(0x7FFF - SP_MAG0)). ----
+  int32_t dlim = SP_NBINS - 1;
+  if (top_k <= 0) {
+    if (!((xmax - xmax) * c >= -40.0f)) {
+      dlim = -1;   // the maximum is inf or NaN: every weight is zero
+    } else {
+      int lo = 0, hi = min(SP_NBINS - 1, km + (0x7FFF - SP_MAG0)) + 1;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if ((key_value(km - mid) - xmax) * c >= -40.0f) lo = mid; else hi = mid;
+      }
+      dlim = lo;
+    }
+  }
   // ---- per-key counts below the max (from registers) ----
+  const uint32_t km2 = ((uint32_t)km & 0xFFFFu) * 0x10001u;
 #pragma unroll
   for (int i = 0; i < SP_REG; ++i) {
-    const int c = i * SP_THREADS + tid;
-    if (c < nch) hist_chunk(reg[i], km, hist);
+    const int ch = i * SP_THREADS + tid;
+    if (ch < nch) hist_chunk(reg[i], km2, dlim, hist);
   }
-  for (int c = SP_REG * SP_THREADS + tid; c < nch; c += SP_THREADS) hist_chunk(x4[c], km, hist);
+  for (int ch = SP_REG * SP_THREADS + tid; ch < nch; ch += SP_THREADS)
+    hist_chunk(x4[ch], km2, dlim, hist);
   __syncthreads();
   // ---- cut points and kept mass: thread t owns bins [8t, 8t + 8) ----
   constexpr int PER = SP_NBINS / SP_THREADS;
-  const float xmax = key_value(km);
-  const float c = inv_temp * 1.44269504088896341f;
   uint32_t cnt[PER];
   uint64_t mass[PER];
   uint32_t csum = 0;
@@ -440,12 +530,13 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* __rest
 // ---------------------------------------------------------------- inverse-CDF draw
 // Over the chunk range [lo, hi), wave w of the 16 owns [lo + w seg, min(lo + (w + 1) seg,
 // hi)) with seg = ceil((hi - lo) / 16).  ld(c) loads chunk c (8 tokens; addresses stay in
-// [lo, hi)), wt(raw, c, w[8]) turns it into the 8 token weights.  The totals pass keeps
-// UN chunks per lane in flight.
+// [lo, hi)), wt(raw, c, w[8]) turns it into the 8 token weights.
 __device__ __forceinline__ int range_seg(int lo, int hi) {
   return (hi - lo + SP_THREADS / 64 - 1) / (SP_THREADS / 64);
 }
 
+// Per-wave totals of [lo, hi) into wtot[16]; returns the range total.  Every lane loads
+// UN chunks at a time (unconditionally, at clamped addresses) before it sums them.
 template <typename Acc, int UN, typename LD, typename WT>
 __device__ Acc draw_totals(int lo, int hi, LD ld, WT wt, Acc* wtot) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -453,18 +544,19 @@ __device__ Acc draw_totals(int lo, int hi, LD ld, WT wt, Acc* wtot) {
   const int seg = range_seg(lo, hi);
   const int c0 = lo + wave * seg, c1 = min(c0 + seg, hi);
   Acc acc = 0;
-  for (int c = c0 + lane; c < c1; c += 64 * UN) {
+  for (int cb = c0; cb < c1; cb += 64 * UN) {
     decltype(ld(0)) r[UN];
 #pragma unroll
-    for (int u = 0; u < UN; ++u) r[u] = ld(min(c + 64 * u, c1 - 1));
+    for (int u = 0; u < UN; ++u) r[u] = ld(min(cb + lane + 64 * u, c1 - 1));
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      if (c + 64 * u < c1) {
-        Acc w[8];
-        wt(r[u], c + 64 * u, w);
+      const int c = cb + lane + 64 * u;
+      Acc w[8];
+      wt(r[u], c, w);
+      Acc s = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += w[e];
-      }
+      for (int e = 0; e < 8; ++e) s += w[e];
+      acc += c < c1 ? s : (Acc)0;
     }
   }
   acc = wave_sum_any(acc);
@@ -531,28 +623,50 @@ __device__ int32_t draw_find(int lo, int hi, LD ld, WT wt, const Acc* wtot, Acc 
   return f < 0 ? V - 1 : f;
 }
 
+// The token at target in [lo, hi), given the per-wave totals draw_totals(lo, hi) left in
+// wtot: for wave segments over two wave steps long, the segment that holds the target is
+// summed again by all 16 waves first, so draw_find walks a sixteenth of it (1/256 of the
+// range).
+template <typename Acc, typename LD, typename WT>
+__device__ int32_t draw_refine(int lo, int hi, LD ld, WT wt, Acc* wtot, Acc target, int V,
+                               int32_t* found) {
+  // a sixteenth of at most two wave steps is walked directly
+  if (range_seg(lo, hi) <= 128) return draw_find<Acc>(lo, hi, ld, wt, wtot, target, V, found);
+  Acc before = 0;
+  int ow = SP_THREADS / 64 - 1;
+  for (int w = 0; w < SP_THREADS / 64; ++w) {
+    if (before + wtot[w] > target) { ow = w; break; }
+    before += wtot[w];
+  }
+  const int seg = range_seg(lo, hi);
+  const int lo1 = min(hi, lo + ow * seg), hi1 = min(lo1 + seg, hi);
+  draw_totals<Acc, 1>(lo1, hi1, ld, wt, wtot);
+  return draw_find<Acc>(lo1, hi1, ld, wt, wtot, target - before, V, found);
+}
+
 struct ChunkPair { u32x4_t p, q; };   // vector members: copies stay in registers
+
+// chunks in flight per lane in the totals passes (64-bit and 128-bit masses)
+constexpr int SP_UN64 = 4, SP_UN128 = 2;
 
 __device__ __forceinline__ u128 scaled_target(uint32_t U, u128 M) {
   return (u128)U * (M >> 24) + (((u128)U * (uint64_t)(M & 0xFFFFFFu)) >> 24);
 }
 
 // Plain draw from a row's own distribution p (u64 masses, target floor(U Z / 2^24));
-// tab is p's weight table (build_table), complete before the call.
+// tab is p's weight table (build_table), complete before the call.  REFINE: sum the
+// sixteenth holding the target again before the walk (whole-row draws).
+template <bool REFINE>
 __device__ int32_t draw_plain(const uint16_t* xp, const RowStat& sp, const uint64_t* tab, uint32_t U,
                               int V, uint64_t* wtot, int32_t* found) {
   if (sp.greedy) return sp.argmax;
   const int nch = V >> 3;
   const u32x4_t* v4 = reinterpret_cast<const u32x4_t*>(xp);
   auto ld = [=](int ch) { return v4[ch]; };
-  auto wt = [=](const u32x4_t& u, int ch, uint64_t* w) {
-    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      w[e] = table_weight(sp, tab, (wd[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, ch * 8 + e);
-  };
-  draw_totals<uint64_t, 4>(0, nch, ld, wt, wtot);
+  auto wt = [=](const u32x4_t& u, int ch, uint64_t* w) { chunk_weights(sp, tab, u, ch, w); };
+  draw_totals<uint64_t, SP_UN64>(0, nch, ld, wt, wtot);
   const uint64_t tgt = (uint64_t)(((u128)U * sp.Z) >> 24);
+  if constexpr (REFINE) return draw_refine<uint64_t>(0, nch, ld, wt, wtot, tgt, V, found);
   return draw_find<uint64_t>(0, nch, ld, wt, wtot, tgt, V, found);
 }
 
@@ -596,6 +710,12 @@ __device__ AcceptPlan accept_plan(const uint16_t* target, const uint16_t* draft,
   int32_t d = pl.a < k ? drafts[b * k + pl.a] : 0;
   pl.d = d < 0 ? 0 : (d >= V ? V - 1 : d);
   pl.U = philox_u24(seed, offset, (uint32_t)b, (uint32_t)k);
+  // the same in every lane (read from LDS after the barrier): make that visible to the
+  // compiler so the plan, and the rows it selects, live in scalar registers
+  pl.a = __builtin_amdgcn_readfirstlane(pl.a);
+  pl.kind = __builtin_amdgcn_readfirstlane(pl.kind);
+  pl.d = __builtin_amdgcn_readfirstlane(pl.d);
+  pl.U = (uint32_t)__builtin_amdgcn_readfirstlane((int)pl.U);
   return pl;
 }
 
@@ -618,15 +738,21 @@ __device__ void with_draw(const AcceptPlan& pl, const uint16_t* target, const ui
     __syncthreads();
     auto ld = [=](int ch) { return ChunkPair{vp[ch], vq[ch]}; };
     auto wt = [=](const ChunkPair& r, int ch, u128* w) {
-      const u32x4_t up = r.p, uq = r.q;
-      const uint32_t pw[4] = {up.x, up.y, up.z, up.w}, qw[4] = {uq.x, uq.y, uq.z, uq.w};
+      const uint32_t pw[4] = {r.p.x, r.p.y, r.p.z, r.p.w}, qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int t = ch * 8 + e;
-        const uint64_t wpt = table_weight(sp, tab_p, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
-        const uint64_t wqt = table_weight(sq, tab_q, (qw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
-        const u128 l = (u128)wpt * Zq, r = (u128)wqt * sp.Z;
-        w[e] = l > r ? l - r : (u128)0;
+      for (int h = 0; h < 4; ++h) {
+        uint64_t wp[2], wq[2];
+        pair_weights(sp, tab_p, pw[h], ch * 8 + 2 * h, wp[0], wp[1]);
+        pair_weights(sq, tab_q, qw[h], ch * 8 + 2 * h, wq[0], wq[1]);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          u128 v = 0;
+          if (wp[e] != 0) {   // most tokens lie past p's cut: skip the 128-bit products
+            const u128 l = (u128)wp[e] * Zq, rr = (u128)wq[e] * sp.Z;
+            v = l > rr ? l - rr : (u128)0;
+          }
+          w[2 * h + e] = v;
+        }
       }
     };
     f(ld, wt, (u128)0);
@@ -636,13 +762,12 @@ __device__ void with_draw(const AcceptPlan& pl, const uint16_t* target, const ui
     const int d = pl.d;
     auto ld = [=](int ch) { return vp[ch]; };
     auto wt = [=](const u32x4_t& up, int ch, uint64_t* w) {
-      const uint32_t pw[4] = {up.x, up.y, up.z, up.w};
+      uint64_t wp[8];
+      chunk_weights(sp, tab_p, up, ch, wp);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int t = ch * 8 + e;
-        const uint64_t wpt = table_weight(sp, tab_p, (pw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, t);
-        const uint64_t r = t == d ? sp.Z : 0;
-        w[e] = wpt > r ? wpt - r : 0;
+        const uint64_t r = ch * 8 + e == d ? sp.Z : 0;
+        w[e] = wp[e] > r ? wp[e] - r : 0;
       }
     };
     f(ld, wt, (uint64_t)0);
@@ -650,12 +775,7 @@ __device__ void with_draw(const AcceptPlan& pl, const uint16_t* target, const ui
     // the bonus: p of row k itself
     __syncthreads();
     auto ld = [=](int ch) { return vp[ch]; };
-    auto wt = [=](const u32x4_t& u, int ch, uint64_t* w) {
-      const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        w[e] = table_weight(sp, tab_p, (wd[e >> 1] >> (16 * (e & 1))) & 0xFFFFu, ch * 8 + e);
-    };
+    auto wt = [=](const u32x4_t& u, int ch, uint64_t* w) { chunk_weights(sp, tab_p, u, ch, w); };
     f(ld, wt, (uint64_t)0);
   }
 }
@@ -689,12 +809,13 @@ __global__ __launch_bounds__(SP_THREADS) void spec_partial_kernel(
     using Acc = decltype(tag);
     Acc* wtot;
     if constexpr (sizeof(Acc) == 16) wtot = wt128; else wtot = wt64;
-    const Acc tot = draw_totals<Acc, sizeof(Acc) == 16 ? 2 : 4>(lo, hi, ld, wt, wtot);
+    const Acc tot = draw_totals<Acc, sizeof(Acc) == 16 ? SP_UN128 : SP_UN64>(lo, hi, ld, wt, wtot);
     if (threadIdx.x == 0) part[(size_t)b * ns + s] = (u128)tot;
   });
 }
 
-// Pass 2, grid (B): the slice holding the target, then the token inside it.
+// Pass 2, grid (B): the slice holding the target, then the token inside it (the slice
+// summed by the 16 waves, the owning sixteenth summed again, its owning sixteenth walked).
 __global__ __launch_bounds__(SP_THREADS) void spec_final_kernel(
     const uint16_t* __restrict__ target, const uint16_t* __restrict__ draft,
     const int32_t* __restrict__ drafts, int k, int V, float inv_temp, uint64_t seed,
@@ -722,8 +843,7 @@ __global__ __launch_bounds__(SP_THREADS) void spec_final_kernel(
   } else if (pl.kind != 0 && R == 0) {
     // the residual is empty: draw from p itself (whole row, this workgroup)
     build_table(sp, c, tab_p);
-    __syncthreads();
-    tok = draw_plain(target + ((size_t)b * (k + 1) + pl.a) * V, sp, tab_p, pl.U, V, wt64, &found);
+    tok = draw_plain<false>(target + ((size_t)b * (k + 1) + pl.a) * V, sp, tab_p, pl.U, V, wt64, &found);
   } else {
     // target: floor(U Z / 2^24) for the bonus (Z = the kept mass of p), U R scaled for
     // a residual; then the slice whose running total passes it
@@ -739,9 +859,10 @@ __global__ __launch_bounds__(SP_THREADS) void spec_final_kernel(
     split_range(nch, ns, s_hit, lo, hi);
     with_draw(pl, target, draft, k, V, c, st_t, st_d, b, tab_p, tab_q, [&](auto ld, auto wt, auto tag) {
       using Acc = decltype(tag);
+      constexpr int UN = sizeof(Acc) == 16 ? SP_UN128 : SP_UN64;
       Acc* wtot;
       if constexpr (sizeof(Acc) == 16) wtot = wt128; else wtot = wt64;
-      draw_totals<Acc, sizeof(Acc) == 16 ? 2 : 4>(lo, hi, ld, wt, wtot);
+      draw_totals<Acc, UN>(lo, hi, ld, wt, wtot);
       tok = draw_find<Acc>(lo, hi, ld, wt, wtot, (Acc)(tgt - before), V, &found);
     });
   }
@@ -765,7 +886,7 @@ __global__ __launch_bounds__(SP_THREADS) void sample_rows_kernel(
   const uint32_t U = philox_u24(seed, offset, (uint32_t)(row_base + r), (uint32_t)slot);
   build_table(sp, c, tab);
   __syncthreads();
-  const int32_t tok = draw_plain(logits + (size_t)r * V, sp, tab, U, V, wt64, &found);
+  const int32_t tok = draw_plain<true>(logits + (size_t)r * V, sp, tab, U, V, wt64, &found);
   if (threadIdx.x == 0) out[r] = tok;
 }
 
@@ -785,21 +906,33 @@ static bool sampler_args_ok(int V, float top_p, float inv_temp) {
   return true;
 }
 
-// Row statistics for `rows` rows: the histogram kernel, or for greedy rows the split
+// Row statistics for rows0 rows of x0 followed by rows1 rows of x1 (one RowStat array):
+// the histogram kernel for all of them in one launch, or for greedy rows the split
 // argmax (partials at `part`).
-static int launch_row_stats(const uint16_t* x, int rows, int V, float inv_temp, int top_k,
-                            float top_p, RowStat* st, uint64_t* part, hipStream_t s) {
+static int launch_row_stats(const uint16_t* x0, int rows0, const uint16_t* x1, int rows1, int V,
+                            float inv_temp, int top_k, float top_p, RowStat* st, uint64_t* part,
+                            hipStream_t s) {
   if (inv_temp > 0.0f) {
-    hipLaunchKernelGGL(row_stats_kernel, dim3(rows), dim3(SP_THREADS), 0, s, x, V, inv_temp,
-                       top_k, top_p, st);
+    hipLaunchKernelGGL(row_stats_kernel, dim3(rows0 + rows1), dim3(SP_THREADS), 0, s, x0, rows0,
+                       x1, V, inv_temp, top_k, top_p, st);
     return launch_status();
   }
-  hipLaunchKernelGGL(argmax_partial_kernel, dim3(SP_NSPLIT, rows), dim3(256), 0, s, x, V, part);
-  int rc = launch_status();
-  if (rc) return rc;
-  hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, s, (const uint64_t*)part, st,
-                     (int32_t*)nullptr);
-  return launch_status();
+  const uint16_t* xs[2] = {x0, x1};
+  const int rs[2] = {rows0, rows1};
+  int base = 0;
+  for (int h = 0; h < 2; ++h) {
+    if (rs[h] <= 0) continue;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(SP_NSPLIT, rs[h]), dim3(256), 0, s, xs[h], V,
+                       part + (size_t)base * SP_NSPLIT);
+    int rc = launch_status();
+    if (rc) return rc;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(rs[h]), dim3(64), 0, s,
+                       (const uint64_t*)(part + (size_t)base * SP_NSPLIT), st + base,
+                       (int32_t*)nullptr);
+    if ((rc = launch_status())) return rc;
+    base += rs[h];
+  }
+  return 0;
 }
 
 static long long stats_bytes(long long rows) {
@@ -838,20 +971,14 @@ LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int
   RowStat* st_t = (RowStat*)workspace;
   RowStat* st_d = st_t + rt;
   uint64_t* part = (uint64_t*)(st_d + rd);
-  int rc = launch_row_stats((const uint16_t*)target, rt, V, inv_temperature, top_k, top_p, st_t,
-                            part, st);
+  int rc = launch_row_stats((const uint16_t*)target, rt, (const uint16_t*)draft, k > 0 ? rd : 0, V,
+                            inv_temperature, top_k, top_p, st_t, part, st);
   if (rc) return rc;
-  if (draft && k > 0) {
-    rc = launch_row_stats((const uint16_t*)draft, rd, V, inv_temperature, top_k, top_p, st_d,
-                          part + (size_t)rt * SP_NSPLIT, st);
-    if (rc) return rc;
-  }
-  // the draw: vocabulary slices summed by B x ns workgroups (about two per CU), then one
-  // workgroup per sequence finds the slice and the token
-  const int ns = std::max(1, std::min(SP_MAXSLICE, (512 + B - 1) / B));
+  // the draw: B x ns workgroups sum the draw's weights over ns vocabulary slices (one
+  // round of workgroups: one 1024-thread workgroup fits a CU), then one workgroup per
+  // sequence finds the slice and the token in it
+  const int ns = std::max(1, std::min(SP_MAXSLICE, 256 / B));
   u128* apart = (u128*)((char*)workspace + accept_part_offset(B, k, draft != nullptr));
-  // LDS: the weight table of p, and of q when the drafts are sampled (one-hot drafts
-  // need only p's, which leaves room for two workgroups per CU)
   const size_t tabs = (draft ? 2 : 1) * SP_NBINS * sizeof(uint64_t);
   static bool lds_set[64] = {};   // per device: the attribute is set on the current device
   int dev = 0;
@@ -895,8 +1022,8 @@ LOLLM_API int lollm_sample_rows(const void* logits, int rows, int V, float inv_t
                        (RowStat*)nullptr, out);
     return launch_status();
   }
-  int rc = launch_row_stats((const uint16_t*)logits, rows, V, inv_temperature, top_k, top_p, stats,
-                            part, st);
+  int rc = launch_row_stats((const uint16_t*)logits, rows, nullptr, 0, V, inv_temperature, top_k,
+                            top_p, stats, part, st);
   if (rc) return rc;
   hipLaunchKernelGGL(sample_rows_kernel, dim3(rows), dim3(SP_THREADS), 0, st,
                      (const uint16_t*)logits, V, inv_temperature, seed, offset, offset_dev, row_base,

@@ -138,3 +138,31 @@ def test_sample_rows_vocab_beyond_register_rows(temp):
         ref = S.sample_rows(rows, inv, 0, 0.9, 17, off, row_base=0, slot=1)
         got = ops.sample_rows(rows.cuda(), temp, 0, 0.9, 17, off, row_base=0, slot=1)
         assert np.array_equal(got.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("temp,top_k,top_p", [(0.7, 0, 0.95), (0.8, 0, 1.0), (1.3, 40, 0.9)])
+def test_sample_rows_negative_and_extreme_rows(temp, top_k, top_p):
+    """Rows the statistics kernel treats specially: every logit negative (the maximum is
+    taken over order keys), only -0 and negatives, a +inf or NaN maximum (every weight
+    zero), and a dominant logit far above the rest (without top-k most tokens fail the
+    weight test and are not counted)."""
+    from lollm_amd import ops
+    print(f"case extreme rows T={temp} top_k={top_k} top_p={top_p}", flush=True)
+    V = 151936
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(7, V, generator=gen) * 3
+    x[0] = -x[0].abs() - 0.25                       # all negative
+    x[1] = -x[1].abs()
+    x[1, ::3] = -0.0                                # -0 is the maximum
+    x[2, 777] = float("inf")
+    x[3, 5] = float("nan")
+    x[4, 123456] = 80.0                             # far above the rest
+    x[5] = -x[5].abs() * 10 - 30.0
+    x[5, 99] = -2.0                                 # negative maximum far above the rest
+    x[6] = -1e-6                                    # every key flushed to 0: a flat row
+    rows = x.bfloat16()
+    inv = S.inv_temperature(temp)
+    for off in (0, 4):
+        ref = S.sample_rows(rows, inv, top_k, top_p, 23, off, row_base=1, slot=2)
+        got = ops.sample_rows(rows.cuda(), temp, top_k, top_p, 23, off, row_base=1, slot=2)
+        assert np.array_equal(got.cpu().numpy(), ref)
