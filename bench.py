@@ -297,7 +297,10 @@ def isolated_sampler():
     drafts = torch.stack([ops.sample_rows(drf[:, i].contiguous(), 0.7, 0, 0.95, 7, 0, slot=k + 1 + i)
                           for i in range(k)], 1)
     ws = torch.empty(ops._lib.lib().lollm_spec_workspace_bytes(B, k, 1), dtype=torch.uint8, device="cuda")
-    us = time_fn(lambda: ops.spec_accept(tgt, drf, drafts, 0.7, 0, 0.95, 7, 0, workspace=ws), 20)
+    na = torch.empty(B, dtype=torch.int32, device="cuda")
+    nt = torch.empty(B, dtype=torch.int32, device="cuda")
+    us = time_fn(lambda: ops.spec_accept(tgt, drf, drafts, 0.7, 0, 0.95, 7, 0, workspace=ws,
+                                         n_accepted=na, next_token=nt), 20)
     byt = B * (2 * k + 1) * V * 2
     return {"B": B, "k": k, "V": V, "us": round(us, 2), "MB": round(byt / 1e6, 1),
             "GBs": round(byt / us / 1e3, 1), "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
