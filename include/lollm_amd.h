@@ -77,8 +77,8 @@ int lollm_gdn_select_state(const float* snapshots, const int32_t* slot, float* s
  *   gate     (B, T, Hq * D) bf16 or NULL; out = attn * sigmoid(gate)
  *   out      (B, T, Hq * D) bf16
  *   workspace  split-K partials, lollm_attn_workspace_bytes() bytes (required)
- *   grid     workgroups of the balanced split (0: two per CU of the current device,
- *            at most 1024): the 64-key blocks of all (sequence, KV head) pairs are
+ *   grid     workgroups of the balanced split (0: one per CU of the current device,
+ *            at most 1024): the 128-key blocks of all (sequence, KV head) pairs are
  *            dealt out to them in equal contiguous ranges
  *   scale    softmax scale (D^-0.5)
  * Supported: D == 256, Hq / Hkv <= 32, B <= 512. */

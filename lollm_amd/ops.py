@@ -137,7 +137,7 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None,
 # gated GQA attention over the KV cache
 # ------------------------------------------------------------------------------------
 def attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, grid=0):
-    """Bytes of the split-K partials buffer for `grid` workgroups (0: two per CU)."""
+    """Bytes of the split-K partials buffer for `grid` workgroups (0: one per CU)."""
     n = _lib.lib().lollm_attn_workspace_bytes(B, T, Hq, Hkv, D, max_len, grid)
     if n < 0:
         raise ValueError("unsupported attention geometry")
@@ -149,7 +149,7 @@ def attn_verify(q, k_cache, v_cache, kv_len, gate=None, *, grid=0, scale=None,
     """q (B, T, Hq, D) bf16; k_cache / v_cache (B, Hkv, max_len, D) bf16 with the T
     new keys already written at positions kv_len-T .. kv_len-1; kv_len (B,) int32;
     gate (B, T, Hq*D) bf16 or None.  Returns (B, T, Hq*D) bf16.  The key blocks of
-    all sequences are dealt out evenly to `grid` workgroups (0: two per CU)."""
+    all sequences are dealt out evenly to `grid` workgroups (0: one per CU)."""
     B, T, Hq, D = q.shape
     _need(q, "q", torch.bfloat16)
     if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[3] != D:
