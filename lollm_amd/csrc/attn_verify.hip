@@ -26,8 +26,10 @@
 //   - Q: one unit ahead, staged in LDS (two buffers) at the pair's first unit;
 // and each unit is:
 //   - S^T for keys [16w, 16w+16) x 32 rows on wave w (16x16x32 MFMA, Q^T from LDS);
-//     masked row maxima exchanged through LDS so all waves share one running max; P^T
-//     to LDS as bf16;
+//     P^T to LDS as bf16 against a per-row reference max shared by all waves, with the
+//     masked row maxima to LDS, then one barrier: only when a block's maximum exceeds
+//     the reference by 16 in the exponent (and at a pair's first block) do all waves
+//     move the reference, rescale l and O and rewrite P^T behind a second barrier;
 //   - O^T[32w, 32w+32) += V^T P^T on wave w (32x32x16 MFMA, A = V^T read from LDS).
 #include "common.h"
 
@@ -333,8 +335,10 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
         issue_k(set, X2, live2);
 
         if (live) {
-          // 3. mask (key < L and <= the row's query position); row maxima
-          float mx[2];
+          // 3. mask (key < L and <= the row's query position); this wave's row maxima to
+          //    LDS, and P^T against the reference max m_s (the running max as of the last
+          //    rescale, the same in every wave), written before the one barrier
+          float mx[2], ps[2];
 #pragma unroll
           for (int r2 = 0; r2 < 2; ++r2) {
             const int qp = r2 ? qpos_s1 : qpos_s0;
@@ -349,38 +353,63 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
             mx[r2] = fmaxf(mx[r2], __shfl_xor(mx[r2], 16, 64));
             mx[r2] = fmaxf(mx[r2], __shfl_xor(mx[r2], 32, 64));
             if (lane < 16) m_lds[wave * AT_ROWS + 16 * r2 + lane] = mx[r2];
-          }
-          lds_barrier();
-          // 4. common running max, probabilities, P^T to LDS
-#pragma unroll
-          for (int r2 = 0; r2 < 2; ++r2) {
             const int row = 16 * r2 + l16;
-            float mb = m_lds[row];
-#pragma unroll
-            for (int ww = 1; ww < AT_WAVES; ++ww) mb = fmaxf(mb, m_lds[ww * AT_ROWS + row]);
-            const float mn = fmaxf(m_s[r2], mb);
-            const bool live = mn != -INFINITY;
-            const float alpha = live ? fast_exp2((m_s[r2] - mn) * a.cl2) : 1.f;
-            const float base = live ? mn * a.cl2 : 0.f;
+            const float base = m_s[r2] == -INFINITY ? 0.f : m_s[r2] * a.cl2;
             float p[4];
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) p[jj] = fast_exp2(__builtin_fmaf(S[r2][jj], a.cl2, -base));
-            l_s[r2] = l_s[r2] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-            m_s[r2] = mn;
+            ps[r2] = (p[0] + p[1]) + (p[2] + p[3]);
             const uint32_t lo = (uint32_t)f32_to_bf16(p[0]) | ((uint32_t)f32_to_bf16(p[1]) << 16);
             const uint32_t hi = (uint32_t)f32_to_bf16(p[2]) | ((uint32_t)f32_to_bf16(p[3]) << 16);
             *reinterpret_cast<uint2*>(p_lds + row * AT_PROW + (16 * wave + 4 * g4) * 2) = make_uint2(lo, hi);
           }
-          {
-            float mb = m_lds[l32];
+          lds_barrier();
+          // 4. the block maxima of all waves.  While no row's maximum exceeds its reference
+          //    by more than 16 in the exponent (weights up to 2^16, safe in bf16 P and fp32
+          //    sums), P^T stands and nothing is rescaled; otherwise (always at a pair's first
+          //    block) every wave moves the references to the running maxima, rescales l and
+          //    O, and rewrites its P^T.  Every wave evaluates all 32 rows from the same LDS
+          //    maxima and references, so all take the same branch.
+          float mb[2];
+          bool big = false;
 #pragma unroll
-            for (int ww = 1; ww < AT_WAVES; ++ww) mb = fmaxf(mb, m_lds[ww * AT_ROWS + l32]);
-            const float mn = fmaxf(m_o, mb);
+          for (int r2 = 0; r2 < 2; ++r2) {
+            const int row = 16 * r2 + l16;
+            mb[r2] = m_lds[row];
+#pragma unroll
+            for (int ww = 1; ww < AT_WAVES; ++ww) mb[r2] = fmaxf(mb[r2], m_lds[ww * AT_ROWS + row]);
+            big = big || (mb[r2] - m_s[r2]) * a.cl2 > 16.f;   // false when both are -inf
+          }
+          float mbo = m_lds[l32];
+#pragma unroll
+          for (int ww = 1; ww < AT_WAVES; ++ww) mbo = fmaxf(mbo, m_lds[ww * AT_ROWS + l32]);
+          big = big || (mbo - m_o) * a.cl2 > 16.f;
+          if (__builtin_amdgcn_readfirstlane((int)(__ballot(big) != 0))) {
+#pragma unroll
+            for (int r2 = 0; r2 < 2; ++r2) {
+              const int row = 16 * r2 + l16;
+              const float mn = fmaxf(m_s[r2], mb[r2]);
+              const bool live = mn != -INFINITY;
+              const float alpha = live ? fast_exp2((m_s[r2] - mn) * a.cl2) : 1.f;
+              const float base = live ? mn * a.cl2 : 0.f;
+              float p[4];
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj) p[jj] = fast_exp2(__builtin_fmaf(S[r2][jj], a.cl2, -base));
+              l_s[r2] = l_s[r2] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+              m_s[r2] = mn;
+              const uint32_t lo = (uint32_t)f32_to_bf16(p[0]) | ((uint32_t)f32_to_bf16(p[1]) << 16);
+              const uint32_t hi = (uint32_t)f32_to_bf16(p[2]) | ((uint32_t)f32_to_bf16(p[3]) << 16);
+              *reinterpret_cast<uint2*>(p_lds + row * AT_PROW + (16 * wave + 4 * g4) * 2) = make_uint2(lo, hi);
+            }
+            const float mn = fmaxf(m_o, mbo);
             const float alpha = mn == -INFINITY ? 1.f : fast_exp2((m_o - mn) * a.cl2);
             m_o = mn;
             O *= alpha;
+            lds_barrier();
+          } else {
+            l_s[0] += ps[0];
+            l_s[1] += ps[1];
           }
-          lds_barrier();
           // 5. O^T[32 w .. 32 w + 32) += V^T P^T over the 128 keys
 #pragma unroll
           for (int ks = 0; ks < AT_BLOCK / 16; ++ks) {
