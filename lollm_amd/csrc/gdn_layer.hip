@@ -277,8 +277,10 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
     const float* s0 = a.rec + ((size_t)(b * 2 * a.S + slot) * a.Hv + h) * SS;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float4 f = *reinterpret_cast<const float4*>(s0 + (size_t)(row0 + r) * GL_DK + col0);
-      S[r][0] = f.x; S[r][1] = f.y; S[r][2] = f.z; S[r][3] = f.w;
+      // read once per launch (a snapshot of the previous step): streamed past L2
+      const uint4 f = load_nt(s0 + (size_t)(row0 + r) * GL_DK + col0);
+      S[r][0] = __uint_as_float(f.x); S[r][1] = __uint_as_float(f.y);
+      S[r][2] = __uint_as_float(f.z); S[r][3] = __uint_as_float(f.w);
     }
   } else {
 #pragma unroll
