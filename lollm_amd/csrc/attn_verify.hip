@@ -170,6 +170,23 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
   const int PH = a.Hkv * a.qblocks;  // pairs per sequence
 
   const long long U = (long long)PH * build_prefix(a, pre, len, tmp);
+  {
+    // the combine's table: per pair, the first and last workgroup whose range touches it
+    // (-1 for a pair with no keys) and the unit count, so the combine reads one entry
+    // instead of rebuilding the block prefix
+    const int npairs = a.B * PH;
+    int4* tab = reinterpret_cast<int4*>(a.ws + (size_t)(a.nw + npairs) * AT_PART);
+    for (int p = w * AT_THREADS + tid; p < npairs; p += a.nw * AT_THREADS) {
+      const int pb = p / PH, pph = p % PH, pnb = pre[pb + 1] - pre[pb];
+      int wf = -1, wl = -1;
+      if (pnb > 0) {
+        const long long first = (long long)PH * pre[pb] + (long long)pph * pnb;
+        wf = unit_owner(U, first, a.nw);
+        wl = unit_owner(U, first + pnb - 1, a.nw);
+      }
+      tab[p] = make_int4(wf, wl, (int)(uint32_t)U, (int)(uint32_t)(U >> 32));
+    }
+  }
   const long long u0 = unit_begin(U, w, a.nw), u1 = unit_begin(U, w + 1, a.nw);
   if (u0 >= u1) return;
 
@@ -478,11 +495,11 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
 // Merge the pieces of pair blockIdx.y for row blockIdx.x and apply the gate: thread d
 // owns output column d; piece weights exp(m_s - M) live in LDS.  Every pair is
 // finished here (one piece when one workgroup covered it); pairs with no keys get zeros.
+// The pieces' workgroup range comes from the table the main kernel wrote.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   __shared__ float wsc[1024];   // piece weights (0 for workgroups with no units)
   __shared__ float lsc[1024];   // piece row sums
   __shared__ float red[8];
-  __shared__ int sred[8];
   const int r = blockIdx.x, pair = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int PH = a.Hkv * a.qblocks;
@@ -494,34 +511,23 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const int hr = r / QB, i = r % QB, h = kvh * a.n_rep + hr;
   const size_t o = ((size_t)b * a.T + q0 + i) * a.Hq * AT_D + (size_t)h * AT_D + tid;
   const float gl = a.gate ? bf16_to_f32(a.gate[o]) : 0.f;   // in flight from the start
-  // blocks before sequence b, and in total
-  int before = 0, total = 0;
-  for (int s = tid; s < a.B; s += 256) {
-    const int n = nblk_of(seq_len(a, s));
-    total += n;
-    if (s < b) before += n;
-  }
-#pragma unroll
-  for (int of = 32; of > 0; of >>= 1) {
-    before += __shfl_xor(before, of, 64);
-    total += __shfl_xor(total, of, 64);
-  }
-  if (lane == 0) { sred[wave] = before; sred[4 + wave] = total; }
-  __syncthreads();
-  before = sred[0] + sred[1] + sred[2] + sred[3];
-  total = sred[4] + sred[5] + sred[6] + sred[7];
-  const int nb = nblk_of(seq_len(a, b));
-  if (nb == 0) {
+  const int4 te = reinterpret_cast<const int4*>(a.ws + (size_t)(a.nw + a.B * PH) * AT_PART)[pair];
+  const int wf = te.x, wl = te.y;
+  const long long U = (long long)(((uint64_t)(uint32_t)te.w << 32) | (uint32_t)te.z);
+  if (wf < 0) {   // a pair with no keys
     a.out[o] = 0;
     return;
   }
-  const long long U = (long long)PH * total;
-  const long long first = (long long)PH * before + (long long)ph * nb;
-  const int wf = unit_owner(U, first, a.nw), wl = unit_owner(U, first + nb - 1, a.nw);
   // pieces: slot w + pair of every workgroup w in [wf, wl] whose range is not empty
   // (with fewer blocks than workgroups, empty workgroups sit between the owners)
   const int np = wl - wf + 1;
   const float* base = a.ws + ((size_t)wf + pair) * AT_PART;
+  // the output column of the first 16 pieces, in flight during the weight reductions
+  // (index clamped into the pieces: dead or extra slots are never weighted in)
+  const float* col = base + 2 * AT_ROWS + r * AT_D + tid;
+  float vv[16];
+#pragma unroll
+  for (int s = 0; s < 16; ++s) vv[s] = col[(size_t)min(s, np - 1) * AT_PART];
   float m = -INFINITY;
   for (int s = tid; s < np; s += 256) {
     const bool live = unit_begin(U, wf + s, a.nw) < unit_begin(U, wf + s + 1, a.nw);
@@ -547,10 +553,14 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   if (lane == 0) red[4 + wave] = l;
   __syncthreads();
   const float lsum = red[4] + red[5] + red[6] + red[7];
-  const float* col = base + 2 * AT_ROWS + r * AT_D + tid;
   float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const float wgt = s < np ? wsc[s] : 0.f;
+    acc += wgt != 0.f ? vv[s] * wgt : 0.f;   // junk in dead slots is never weighted in
+  }
 #pragma unroll 8
-  for (int s = 0; s < np; ++s) {
+  for (int s = 16; s < np; ++s) {
     const float wgt = wsc[s];
     const float v = col[(size_t)s * AT_PART];   // in bounds for every slot; junk if dead
     acc += wgt != 0.f ? v * wgt : 0.f;
@@ -563,6 +573,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 }  // namespace lollm
 
 using namespace lollm;
+
+// Workspace: one fp32 piece per workgroup plus one per pair, then the combine's table
+// (one int4 per pair).
+static long long attn_ws_bytes(long long nw, long long pairs) {
+  return (nw + pairs) * AT_PART * (long long)sizeof(float) + pairs * 16;
+}
 
 static int attn_geometry(int B, int T, int Hq, int Hkv, int D, int max_len, int* n_rep, int* QB,
                          int* qblocks) {
@@ -593,7 +609,7 @@ LOLLM_API long long lollm_attn_workspace_bytes(int B, int T, int Hq, int Hkv, in
   if (attn_geometry(B, T, Hq, Hkv, D, max_len, &n_rep, &QB, &qblocks)) return -1;
   const int nw = attn_grid(grid);
   if (nw <= 0) return -1;
-  return ((long long)nw + (long long)B * Hkv * qblocks) * AT_PART * (long long)sizeof(float);
+  return attn_ws_bytes(nw, (long long)B * Hkv * qblocks);
 }
 
 LOLLM_API int lollm_attn_verify(const void* q, const void* k_cache, const void* v_cache,
@@ -610,7 +626,7 @@ LOLLM_API int lollm_attn_verify(const void* q, const void* k_cache, const void* 
   if (head_stride % 8 || seq_stride % 8) return LOLLM_EINVAL;  // 16-byte aligned rows
   const int nw = attn_grid(grid);
   if (nw <= 0 || nw > 1024) return LOLLM_EUNSUPPORTED;
-  const long long need = ((long long)nw + (long long)B * Hkv * qblocks) * AT_PART * (long long)sizeof(float);
+  const long long need = attn_ws_bytes(nw, (long long)B * Hkv * qblocks);
   if (!workspace || workspace_bytes < need) return LOLLM_EINVAL;
   AttnArgs a;
   a.q = (const uint16_t*)q; a.kc = (const uint16_t*)k_cache; a.vc = (const uint16_t*)v_cache;
