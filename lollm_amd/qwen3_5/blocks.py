@@ -23,7 +23,7 @@ def _cat_rows(*ws):
 
 
 _FLUSH = {}
-_SHAPE_CHOICE = {}   # (N, K, epilogue, rows or ("norm", rows)) -> "gemm" | "blas"
+_SHAPE_CHOICE = {}   # (N, K, epilogue, rows or ("norm", rows)) -> "gemm" | "gemm1" | "blas"
 
 
 def _flush_caches(device):
@@ -54,7 +54,7 @@ class Projection:
         self.tiled = (ops.gemm_tile_weights(self.weight, epilogue)
                       if self.weight.is_cuda and ops.gemm_supported(self.N, self.K, epilogue)
                       else None)
-        self.choice = {}            # rows -> "gemm" | "blas"
+        self.choice = {}            # rows -> "gemm" | "gemm1" | "blas"
 
     def workspace_bytes(self, rows=ops.GEMM_MAX_ROWS):
         return ops.gemm_workspace_bytes(rows, self.N, self.K) if self.tiled is not None else 0
@@ -63,8 +63,8 @@ class Projection:
         y = F.linear(x, self.weight)
         return ops.swiglu(y) if self.epilogue == ops.GEMM_SWIGLU else y
 
-    def _gemm(self, x):
-        return ops.gemm(x, self.tiled, self.N, self.K, self.epilogue)
+    def _gemm(self, x, grid=0):
+        return ops.gemm(x, self.tiled, self.N, self.K, self.epilogue, grid=grid)
 
     def _pick(self, key, paths):
         shape = (self.N, self.K, self.epilogue, key)
@@ -93,9 +93,15 @@ class Projection:
         rows = x.numel() // self.K
         if self.tiled is None or rows > ops.GEMM_MAX_ROWS:
             return self._blas(x)
+        # lollm_gemm with its default grid (two workgroups per CU) or one per CU (half the
+        # split-K pieces to merge), or hipBLASLt: the fastest on cold caches
+        g1 = _cus()
         choice = self.choice.get(rows) or self._pick(
-            rows, {"gemm": lambda: self._gemm(x), "blas": lambda: self._blas(x)})
-        return self._gemm(x) if choice == "gemm" else self._blas(x)
+            rows, {"gemm": lambda: self._gemm(x), "gemm1": lambda: self._gemm(x, g1),
+                   "blas": lambda: self._blas(x)})
+        if choice == "blas":
+            return self._blas(x)
+        return self._gemm(x, g1 if choice == "gemm1" else 0)
 
     def add_norm(self, x, residual, norm):
         """The projection feeding the residual stream with the add and the next RMSNorm
@@ -107,15 +113,33 @@ class Projection:
                 or not ops.gemm_rmsnorm_supported(rows, self.N, self.K)):
             return norm(self._blas(x), residual=residual)
 
-        def fused():
-            return ops.gemm_rmsnorm(x, self.tiled, self.N, self.K, residual, norm.weight, norm.eps)
+        def fused(grid=0):
+            return ops.gemm_rmsnorm(x, self.tiled, self.N, self.K, residual, norm.weight, norm.eps,
+                                    grid=grid)
 
         def unfused():
             return norm(self._blas(x), residual=residual)
 
+        g1 = _cus()
         key = ("norm", rows)
-        choice = self.choice.get(key) or self._pick(key, {"gemm": fused, "blas": unfused})
-        return fused() if choice == "gemm" else unfused()
+        paths = {"gemm": fused, "blas": unfused}
+        if ops.gemm_rmsnorm_supported(rows, self.N, self.K, g1):
+            paths["gemm1"] = lambda: fused(g1)
+        choice = self.choice.get(key) or self._pick(key, paths)
+        if choice == "blas":
+            return unfused()
+        return fused(g1 if choice == "gemm1" else 0)
+
+
+_CUS = {}
+
+
+def _cus():
+    """Compute units of the current device (the one-workgroup-per-CU GEMM grid)."""
+    dev = torch.cuda.current_device()
+    if dev not in _CUS:
+        _CUS[dev] = torch.cuda.get_device_properties(dev).multi_processor_count
+    return _CUS[dev]
 
 
 class RMSNorm:
