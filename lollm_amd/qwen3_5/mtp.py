@@ -27,7 +27,7 @@ from __future__ import annotations
 import torch
 
 from .. import ops
-from .blocks import Projection, RMSNorm
+from .blocks import Projection, RMSNorm, _cus
 from .modeling_qwen3_5 import DecoderLayer, Qwen3_5Model
 from .random_init import weight_shapes
 from .weights import take_weights, to_raw
@@ -189,9 +189,18 @@ class SpecDecoder:
                                     slot=k + 1 + j, offset_dev=self.offset, workspace=self.row_ws)
                 self.drafts[:, j - 1].copy_(d)
             elif lm.tiled is not None and B <= ops.GEMM_MAX_ROWS:
-                # greedy draft straight from the lm_head GEMM (no logits), into its column
-                d = ops.gemm_argmax(normed.reshape(B, -1), lm.tiled, lm.N, lm.K,
-                                    out=self.drafts[:, j - 1])
+                # greedy draft straight from the lm_head GEMM (no logits), into its column;
+                # the grid (two workgroups per CU or one) timed once per shape like the
+                # projections' paths
+                x2 = normed.reshape(B, -1)
+                col = self.drafts[:, j - 1]
+                g1 = _cus()
+                key = ("argmax", B)
+                choice = lm.choice.get(key) or lm._pick(key, {
+                    "gemm": lambda: ops.gemm_argmax(x2, lm.tiled, lm.N, lm.K, out=col),
+                    "gemm1": lambda: ops.gemm_argmax(x2, lm.tiled, lm.N, lm.K, out=col, grid=g1)})
+                d = ops.gemm_argmax(x2, lm.tiled, lm.N, lm.K, out=col,
+                                    grid=g1 if choice == "gemm1" else 0)
             else:
                 d = ops.sample_rows(lm(normed).view(B, -1), 0.0, workspace=self.row_ws)
                 self.drafts[:, j - 1].copy_(d)

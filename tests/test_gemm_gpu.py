@@ -87,16 +87,18 @@ def test_gemm_rejects_bad_shapes_and_workspace():
 
 
 def test_projection_paths_agree():
-    """Projection: both paths for <= 64 rows (the timed choice and the forced other
-    one) and hipBLASLt for more rows all match the oracle."""
-    from lollm_amd.qwen3_5.blocks import Projection
+    """Projection: every path for <= 64 rows (the timed choice and the forced others:
+    lollm_gemm at two grids, hipBLASLt) and hipBLASLt for more rows all match the
+    oracle."""
+    from lollm_amd.qwen3_5.blocks import Projection, _cus
     x, W = case(80, 256, 512, seed=5)
     p = Projection(W.cuda())
     assert p.tiled is not None
     ref = R.linear(x.float(), W.float())
     close(p(x[:64].cuda()), ref[:64])
-    assert p.choice[64] in ("gemm", "blas")
+    assert p.choice[64] in ("gemm", "gemm1", "blas")
     close(p._gemm(x[:64].cuda()), ref[:64])
+    close(p._gemm(x[:64].cuda(), _cus()), ref[:64])
     close(p._blas(x[:64].cuda()), ref[:64])
     close(p(x.cuda()), ref)
 
