@@ -23,7 +23,8 @@
 // shared by the 4 waves, two stages per workgroup barrier (four LDS slots: a barrier
 // makes every wave wait for its oldest loads, so halving the barriers measured 2-6%
 // faster at M = 64); weight loads run 4 units ahead in a register ring, activation
-// loads 2 units ahead.  A group one workgroup covers whole is stored directly (with
+// loads 2 units ahead (for at most 32 rows gemm_ksplit_kernel splits each unit's k over
+// the waves instead, see there).  A group one workgroup covers whole is stored directly (with
 // the epilogue); a group cut between workgroups leaves an fp32 piece in slot
 // w + group: in accumulator order (each wave's store one contiguous 1 KB) when
 // gemm_fixup_kernel merges it with one float4 per thread over a (group, m-tile) grid,
@@ -102,6 +103,71 @@ __global__ void gemm_tile_kernel(const uint16_t* __restrict__ W, uint16_t* __res
   *reinterpret_cast<uint4*>(Wt + blk * 512 + L * 8) = v;
 }
 
+// A group's result (lane holds, for m-tile i, rows m = 16 i + l16 and tiled columns
+// 4 g4 .. 4 g4 + 3 of n-tile 4 g + wave): with the epilogue when the workgroup covered
+// the whole group, else as the workgroup's fp32 piece.
+template <int MT>
+__device__ __forceinline__ void gm_emit(const GemmArgs& a, const gm_f32x4 (&v)[MT], int g, bool whole,
+                                        int w, int wave, int lane) {
+  const int l16 = lane & 15, g4 = lane >> 4;
+  if (whole) {
+    if (a.epi == GM_EPI_ARGMAX) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = 16 * i + l16, col = GM_COLS * g + 16 * wave + 4 * g4;
+        uint64_t best = gm_key(v[i][0], col);
+#pragma unroll
+        for (int j = 1; j < 4; ++j) {
+          const uint64_t k2 = gm_key(v[i][j], col + j);
+          best = k2 > best ? k2 : best;
+        }
+        best = gm_max_xor(best, 16);
+        best = gm_max_xor(best, 32);
+        if (g4 == 0 && m < a.M) a.am[(size_t)m * (a.N / 16) + 4 * g + wave] = best;
+      }
+    } else if (a.epi == GM_EPI_SWIGLU) {
+      // partner lane (g4 ^ 2) holds the other half of the same output columns
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        float other[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) other[j] = __shfl_xor(v[i][j], 32, 64);
+        const int m = 16 * i + l16;
+        if (g4 < 2 && m < a.M) {
+          float y[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) y[j] = round_bf16(gm_silu_bf16(v[i][j]) * round_bf16(other[j]));
+          const int col = 8 * (4 * g + wave) + 4 * g4;
+          *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+              make_uint2((uint32_t)f32_to_bf16(y[0]) | ((uint32_t)f32_to_bf16(y[1]) << 16),
+                         (uint32_t)f32_to_bf16(y[2]) | ((uint32_t)f32_to_bf16(y[3]) << 16));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = 16 * i + l16;
+        if (m < a.M) {
+          const int col = GM_COLS * g + 16 * wave + 4 * g4;
+          *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+              make_uint2((uint32_t)f32_to_bf16(v[i][0]) | ((uint32_t)f32_to_bf16(v[i][1]) << 16),
+                         (uint32_t)f32_to_bf16(v[i][2]) | ((uint32_t)f32_to_bf16(v[i][3]) << 16));
+        }
+      }
+    }
+  } else {
+    // a piece: the raw fp32 sums of the group's 64 tiled columns, slot w + g (pieces
+    // are ordered in both w and g, so the slot is unique); padding rows included
+    float* pp = a.part + ((size_t)w + g) * ((size_t)MT * 16 * GM_COLS);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const size_t off = a.rowmajor ? (size_t)(16 * i + l16) * GM_COLS + 16 * wave + 4 * g4
+                                    : (((size_t)i * 4 + wave) * 64 + lane) * 4;
+      *reinterpret_cast<float4*>(pp + off) = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+    }
+  }
+}
+
 template <int MT>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   typedef unsigned int v4u __attribute__((ext_vector_type(4)));
@@ -151,65 +217,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   aload(an[1], u0 + 1 < u1 ? u0 + 1 : ulast);
   bool whole_from_start = (u0 % a.SK) == 0;
 
-  // lane holds, for m-tile i, rows m = 16 i + l16 and tiled columns 4 g4 .. 4 g4 + 3 of
-  // n-tile 4 g + wave
   auto finish = [&](int g, bool whole) {
-    if (whole) {
-      if (a.epi == GM_EPI_ARGMAX) {
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-          const int m = 16 * i + l16, col = GM_COLS * g + 16 * wave + 4 * g4;
-          uint64_t best = gm_key(acc[i][0], col);
-#pragma unroll
-          for (int j = 1; j < 4; ++j) {
-            const uint64_t k2 = gm_key(acc[i][j], col + j);
-            best = k2 > best ? k2 : best;
-          }
-          best = gm_max_xor(best, 16);
-          best = gm_max_xor(best, 32);
-          if (g4 == 0 && m < a.M) a.am[(size_t)m * (a.N / 16) + 4 * g + wave] = best;
-        }
-      } else if (a.epi == GM_EPI_SWIGLU) {
-        // partner lane (g4 ^ 2) holds the other half of the same output columns
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-          float other[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) other[j] = __shfl_xor(acc[i][j], 32, 64);
-          const int m = 16 * i + l16;
-          if (g4 < 2 && m < a.M) {
-            float y[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) y[j] = round_bf16(gm_silu_bf16(acc[i][j]) * round_bf16(other[j]));
-            const int col = 8 * (4 * g + wave) + 4 * g4;
-            *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
-                make_uint2((uint32_t)f32_to_bf16(y[0]) | ((uint32_t)f32_to_bf16(y[1]) << 16),
-                           (uint32_t)f32_to_bf16(y[2]) | ((uint32_t)f32_to_bf16(y[3]) << 16));
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-          const int m = 16 * i + l16;
-          if (m < a.M) {
-            const int col = GM_COLS * g + 16 * wave + 4 * g4;
-            *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
-                make_uint2((uint32_t)f32_to_bf16(acc[i][0]) | ((uint32_t)f32_to_bf16(acc[i][1]) << 16),
-                           (uint32_t)f32_to_bf16(acc[i][2]) | ((uint32_t)f32_to_bf16(acc[i][3]) << 16));
-          }
-        }
-      }
-    } else {
-      // a piece: the raw fp32 sums of the group's 64 tiled columns, slot w + g (pieces
-      // are ordered in both w and g, so the slot is unique); padding rows included
-      float* pp = a.part + ((size_t)w + g) * ((size_t)MT * 16 * GM_COLS);
-#pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const size_t off = a.rowmajor ? (size_t)(16 * i + l16) * GM_COLS + 16 * wave + 4 * g4
-                                      : (((size_t)i * 4 + wave) * 64 + lane) * 4;
-        *reinterpret_cast<float4*>(pp + off) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
-      }
-    }
+    gm_emit<MT>(a, acc, g, whole, w, wave, lane);
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
   };
@@ -261,6 +270,109 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 #undef GM_UNIT
 }
 
+
+// The same product for at most 32 rows: each wave takes one k-step of every unit for all
+// 4 n-tiles of the group, so it reads its MFMA operands straight from memory -- weights
+// (4 blocks, one per n-tile) and activations (one 16-row x 64 B chunk per m-tile) -- into
+// a register ring 4 units deep, with no LDS staging and no barrier in the unit loop.
+// At a group's end the 4 waves' k-quarters are summed through LDS in a fixed order
+// (wave 0 .. 3) and emitted as above.  The activation chunks are half cache lines (every
+// line is read by two waves), which costs more than the LDS staging at 64 rows; at 16
+// and 32 rows, with one workgroup per CU, this form measured 3-10% faster.
+template <int MT>
+__global__ __launch_bounds__(256, 2) void gemm_ksplit_kernel(GemmArgs a) {
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  // the waves' partial sums at a group's end: (n-tile j, wave v, m-tile i) x 64 lanes
+  __shared__ __attribute__((aligned(16))) gm_f32x4 red[4 * 4 * MT * 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int w = blockIdx.x;
+  const int u0 = gm_begin(a.U, w, a.nw), u1 = gm_begin(a.U, w + 1, a.nw);
+  if (u0 >= u1) return;
+  const int kt = a.K / 32;
+  const uint16_t* wlane = a.Wt + (size_t)wave * 512 + lane * 8;
+  const uint16_t* alane[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int r = min(16 * i + l16, a.M - 1);   // padding rows re-read the last row
+    alane[i] = a.A + (size_t)r * a.lda + 32 * wave + 8 * g4;
+  }
+  v4u wr[GM_P][4], ar[GM_P][MT];
+  // weights of unit u: n-tiles 4 g + j, k-step 4 st + wave; activations: k-step 4 st + wave
+  auto load = [&](v4u* dw, v4u* da, int u) {
+    const int g = u / a.SK, st = u - g * a.SK;
+    const uint16_t* p = wlane + ((size_t)4 * g * kt + (size_t)st * GM_KS) * 512;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      dw[j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p + (size_t)j * kt * 512));
+#pragma unroll
+    for (int i = 0; i < MT; ++i) da[i] = *reinterpret_cast<const v4u*>(alane[i] + st * GM_KC);
+  };
+  gm_f32x4 acc[4][MT];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[j][i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+  // every load is issued unconditionally (units past the range re-read the last one) and
+  // the slots are issued oldest first, so each unit waits only for its own slot
+  const int ulast = u1 - 1;
+#pragma unroll
+  for (int p = 0; p < GM_P; ++p) {
+    load(wr[p], ar[p], u0 + p < u1 ? u0 + p : ulast);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  bool whole_from_start = (u0 % a.SK) == 0;
+
+  auto finish = [&](int g, bool whole) {
+    gm_lds_barrier();   // the previous group's reads of red are done
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < MT; ++i) red[((j * 4 + wave) * MT + i) * 64 + lane] = acc[j][i];
+    gm_lds_barrier();
+    gm_f32x4 fin[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      fin[i] = red[((wave * 4) * MT + i) * 64 + lane];
+#pragma unroll
+      for (int v = 1; v < 4; ++v) fin[i] += red[((wave * 4 + v) * MT + i) * 64 + lane];
+    }
+    gm_emit<MT>(a, fin, g, whole, w, wave, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < MT; ++i) acc[j][i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+
+#define GM_KUNIT(J)                                                                           \
+  {                                                                                           \
+    const int u = ub + (J);                                                                   \
+    const bool livej = u < u1;                                                                \
+    if (livej) {                                                                              \
+      _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                         \
+        _Pragma("unroll") for (int i = 0; i < MT; ++i) {                                      \
+          acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                                \
+              __builtin_bit_cast(gm_bf16x8, wr[J][j]), __builtin_bit_cast(gm_bf16x8, ar[J][i]), \
+              acc[j][i], 0, 0, 0);                                                            \
+        }                                                                                     \
+      }                                                                                       \
+    }                                                                                         \
+    load(wr[J], ar[J], u + GM_P < u1 ? u + GM_P : ulast);                                     \
+    if (livej) {                                                                              \
+      const int st = u % a.SK;                                                                \
+      if (st == a.SK - 1 || u == ulast) {                                                     \
+        finish(u / a.SK, whole_from_start && st == a.SK - 1);                                 \
+        whole_from_start = true;                                                              \
+      }                                                                                       \
+    }                                                                                         \
+  }
+
+  static_assert(GM_P == 4, "the unit loop is unrolled by 4");
+  for (int ub = u0; ub < u1; ub += 4) {
+    GM_KUNIT(0) GM_KUNIT(1) GM_KUNIT(2) GM_KUNIT(3)
+  }
+#undef GM_KUNIT
+}
 
 // Merge the pieces of m-tile blockIdx.y of group blockIdx.x: the live piece slots are
 // listed in LDS by one wave (ballots over the workgroups whose ranges touch the group;
@@ -531,8 +643,8 @@ static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, 
   if (epilogue == GM_EPI_ARGMAX)
     a.am = (uint64_t*)((char*)workspace + ((gemm_ws_bytes(M, N, nw) + 255) / 256) * 256);
   switch ((M + 15) / 16) {
-    case 1: hipLaunchKernelGGL(gemm_kernel<1>, dim3(nw), dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(gemm_kernel<2>, dim3(nw), dim3(256), 0, st, a); break;
+    case 1: hipLaunchKernelGGL(gemm_ksplit_kernel<1>, dim3(nw), dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(gemm_ksplit_kernel<2>, dim3(nw), dim3(256), 0, st, a); break;
     case 3: hipLaunchKernelGGL(gemm_kernel<3>, dim3(nw), dim3(256), 0, st, a); break;
     default: hipLaunchKernelGGL(gemm_kernel<4>, dim3(nw), dim3(256), 0, st, a); break;
   }

@@ -40,12 +40,14 @@ def test_gemm_matches_oracle(M, N, K, grid):
     close(y, ref)
 
 
-def test_gemm_pieces_equal_whole_groups():
+@pytest.mark.parametrize("M", [16, 64])
+def test_gemm_pieces_equal_whole_groups(M):
     """grid=1: every group finished by one workgroup; grid=1024: every group cut into
-    pieces and merged by the fixup kernel; both sum the same fp32 terms in k order
-    within a workgroup, so they agree to fp32 reassociation (checked at 1 bf16 ulp)."""
+    pieces and merged by the fixup kernel; both sum the same fp32 terms, so they agree
+    to fp32 reassociation (checked at 1 bf16 ulp).  M = 16 runs the k-split kernel
+    (waves' k-quarters summed at each group's end), M = 64 the LDS-staged one."""
     from lollm_amd import ops
-    x, W = case(64, 1024, 2048, seed=3)
+    x, W = case(M, 1024, 2048, seed=3)
     Wt = ops.gemm_tile_weights(W.cuda())
     a = ops.gemm(x.cuda(), Wt, 1024, 2048, grid=1).float()
     b = ops.gemm(x.cuda(), Wt, 1024, 2048, grid=1024).float()
