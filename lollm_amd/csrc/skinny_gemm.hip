@@ -173,6 +173,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
   typedef unsigned int v4u __attribute__((ext_vector_type(4)));
   constexpr int CPR = GM_KC / 8;                          // 16 B chunks per activation row
   constexpr int ACH = (MT * 16 * CPR + 255) / 256;        // activation chunks per thread
+  // every thread stages exactly ACH chunks, so the staging needs no row test: such a
+  // test (always true) made the compiler wait for all staging loads at once instead of
+  // each one in turn, which measured 5-11% slower at 48-64 rows
+  static_assert(ACH * 256 == MT * 16 * CPR, "the staging covers the tile exactly");
   // activation stages of units ub + j in slot j & 3, written two at a time
   __shared__ __attribute__((aligned(16))) unsigned char al[4][MT * 16 * GM_PITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -197,10 +201,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
       const int c = i * 256 + tid, row = c / CPR, col = c % CPR;
-      if (row < MT * 16) {
-        const int rr = row < a.M ? row : a.M - 1;
-        dst[i] = *reinterpret_cast<const v4u*>(a.A + (size_t)rr * a.lda + k0 + col * 8);
-      }
+      const int rr = row < a.M ? row : a.M - 1;
+      dst[i] = *reinterpret_cast<const v4u*>(a.A + (size_t)rr * a.lda + k0 + col * 8);
     }
   };
 
@@ -237,7 +239,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
       _Pragma("unroll") for (int h = 0; h < 2; ++h)                                           \
       _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                       \
         const int c = i * 256 + tid, row = c / CPR, col = c % CPR;                            \
-        if (row < MT * 16) *reinterpret_cast<v4u*>(&al[(J) + h][row * GM_PITCH + col * 16]) = an[h][i]; \
+        *reinterpret_cast<v4u*>(&al[(J) + h][row * GM_PITCH + col * 16]) = an[h][i]; \
       }                                                                                       \
       gm_lds_barrier();                                                                       \
       aload(an[0], u + 2 < u1 ? u + 2 : ulast);                                               \
