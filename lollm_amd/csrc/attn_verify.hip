@@ -130,15 +130,8 @@ __device__ __forceinline__ int unit_owner(long long U, long long u, int nw) {
   return (int)(((u + 1) * nw - 1) / U);
 }
 
-// Buffer descriptor over [base, base + bytes): loads at offsets past the end return zero
-// and touch no memory.  Base and size are made explicitly uniform (scalar registers).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t at_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t p = (uint64_t)base;
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
-  const uint64_t pu = ((uint64_t)hi << 32) | (uint64_t)lo;   // no sign extension of the low word
-  return __builtin_amdgcn_make_buffer_rsrc((void*)pu, (short)0,
-                                           __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
+  return buf_rsrc(base, bytes);
 }
 // AUX = 2: the non-temporal hint (K and V are read once per launch and should not
 // displace reusable lines; measured 9% faster than the default policy on the C3 shape)

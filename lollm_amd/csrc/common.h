@@ -44,6 +44,17 @@ __device__ __forceinline__ uint4 load_nt(const void* p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+// Buffer descriptor over [base, base + bytes): loads at offsets past the end return zero
+// and touch no memory (bytes = 0 gives a descriptor whose loads are all zero).  Base and
+// size are made explicitly uniform (scalar registers).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+  const uint64_t pu = ((uint64_t)hi << 32) | (uint64_t)lo;   // no sign extension of the low word
+  return __builtin_amdgcn_make_buffer_rsrc((void*)pu, (short)0,
+                                           __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
+}
 __device__ __forceinline__ void store_nt(void* p, uint4 v) {
   u32x4_t w = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(p));

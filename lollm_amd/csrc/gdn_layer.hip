@@ -272,20 +272,6 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
   };
 
   // ---- 1. one batch of loads ----
-  float S[16][4];
-  if (!a.fresh) {
-    const float* s0 = a.rec + ((size_t)(b * 2 * a.S + slot) * a.Hv + h) * SS;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      // read once per launch (a snapshot of the previous step): streamed past L2
-      const uint4 f = load_nt(s0 + (size_t)(row0 + r) * GL_DK + col0);
-      S[r][0] = __uint_as_float(f.x); S[r][1] = __uint_as_float(f.y);
-      S[r][2] = __uint_as_float(f.z); S[r][3] = __uint_as_float(f.w);
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) S[r][0] = S[r][1] = S[r][2] = S[r][3] = 0.f;
-  }
   // conv inputs: (K-1+T) rows x 3 groups x 16 chunks of 8 channels
   const int nx = (Km1 + T) * 48;
   uint4 xv[3];
@@ -312,13 +298,29 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
                                          (size_t)h * GL_DK + part * 8);
   }
   if (tid >= 240) nwv = *reinterpret_cast<const uint4*>(a.norm_w + (tid - 240) * 8);
-  float bb = 0.f, aa = 0.f;
-  if (tid < T) {
-    const size_t base = ((size_t)b * T + tid) * a.P + a.C + a.value_dim;
-    bb = bf16_to_f32(a.proj[base + h]);
-    aa = bf16_to_f32(a.proj[base + a.Hv + h]);
-  }
+  // b, a of position min(tid, T - 1): unconditional, so no branch holds a wait that
+  // the compiler could hoist above the state loads below (used only for tid < T)
+  const size_t base_ba = ((size_t)b * T + (tid < T ? tid : T - 1)) * a.P + a.C + a.value_dim;
+  const uint16_t bb_raw = a.proj[base_ba + h], aa_raw = a.proj[base_ba + a.Hv + h];
   const float a_log = a.A_log[h], dtb = a.dt_bias[h];
+  // The state last: every load above is waited for before the conv, and the waits are
+  // in issue order, so the state (64 KB per workgroup) stays in flight through the conv,
+  // gating and norms.  Its loads are unconditional -- a fresh call reads through an empty
+  // descriptor (zeros, no memory touched) -- so the compiler counts them exactly.  Read
+  // once per launch (a snapshot of the previous step): non-temporal.
+  float S[16][4];
+  {
+    const float* s0 = a.rec + ((size_t)(b * 2 * a.S + slot) * a.Hv + h) * SS;
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(s0, a.fresh ? 0u : (uint32_t)(SS * sizeof(float)));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const u32x4_t f = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(((row0 + r) * GL_DK + col0) * 4), 0, 2));
+      S[r][0] = __uint_as_float(f.x); S[r][1] = __uint_as_float(f.y);
+      S[r][2] = __uint_as_float(f.z); S[r][3] = __uint_as_float(f.w);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);   // nothing that waits on a load moves above the state loads
 
   // ---- 2. to LDS, and the new conv window (state rows + raw inputs) to the other half ----
 #pragma unroll
@@ -340,6 +342,7 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
   if (tid < T * 16) *reinterpret_cast<uint4*>(&zb[tid / 16][(tid % 16) * 8]) = zv;
   if (tid >= 240) *reinterpret_cast<uint4*>(&nw[(tid - 240) * 8]) = nwv;
   if (tid < T) {
+    const float bb = bf16_to_f32(bb_raw), aa = bf16_to_f32(aa_raw);
     gb[tid][0] = -__expf(a_log) * softplus_g(aa + dtb);
     gb[tid][1] = round_bf16(1.f / (1.f + __expf(-bb)));
   }
