@@ -112,16 +112,20 @@ def run_e2e(model, mtp, cfg, B, prompt_len, k, steps, warmup, temperature, top_p
                  "final_context_mean": ctx}
 
 
-def projection_paths():
-    """The path each projection shape took ("gemm" = lollm_gemm, "blas" = hipBLASLt),
-    keyed "NxK rows" (+ " +norm" for the residual add / RMSNorm fused form)."""
-    from lollm_amd.qwen3_5 import blocks
+def projection_paths(model, mtp, B, k):
+    """The path of each projection shape of the step ("gemm" = lollm_gemm, "blas" =
+    hipBLASLt; a fixed function of the shape), keyed "NxK M=rows"."""
     out = {}
-    for (N, K, epi, key), choice in sorted(blocks._SHAPE_CHOICE.items(), key=str):
-        rows = key[1] if isinstance(key, tuple) else key
-        tag = f"{N}x{K}{' swiglu' if epi else ''} M={rows}{' +norm' if isinstance(key, tuple) else ''}"
-        out[tag] = choice
-    return out
+    layers = list(model.model.layers) + list(mtp.layers)
+    projs = [model.lm_head, mtp.fc]
+    for layer in layers:
+        mixer = layer.self_attn if layer.layer_type == "full_attention" else layer.linear_attn
+        projs += mixer.projections() + layer.mlp.projections()
+    for p in projs:
+        for rows in (B, B * (k + 1)):
+            tag = f"{p.N}x{p.K}{' swiglu' if p.epilogue else ''} M={rows}"
+            out[tag] = p.path(rows)
+    return dict(sorted(out.items()))
 
 
 def verify_breakdown(dec, iters=20):
@@ -490,7 +494,7 @@ def main():
             {k_: round(v, 1) for k_, v in parts.items()},
         "roofline": {k_: roof[k_] for k_ in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
         "roofline_kernel": roof["kernel"],
-        "projection_paths": projection_paths(),
+        "projection_paths": projection_paths(model, mtp, args.batch, args.k),
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

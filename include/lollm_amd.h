@@ -285,14 +285,42 @@ int lollm_gdn_layer_chunked(const void* proj, long long proj_stride, const void*
  * columns) at out_count[b], copy hidden[b, a] (B, T, H) to h_last (B, H) (the MTP
  * input, mtp.py:155,162), set pending = next_token, increment *offset (the
  * sampler's Philox step counter) and, if accept_hist != NULL, accept_hist[a] (T
- * counters: the accepted-length histogram).  No reference counterpart as one call: it folds
- * the reference's per-step host bookkeeping into one kernel so a step needs no sync. */
+ * counters: the accepted-length histogram) and, if seen != NULL, mark the accepted drafts
+ * verify_ids[b, 1..a] and the new pending token in the (B, seen_words) repetition-penalty
+ * bitmaps (the context.append calls of mtp.py:129,150).  No reference counterpart as one
+ * call: it folds the reference's per-step host bookkeeping into one kernel so a step needs
+ * no sync.  The caller guarantees out_count[b] + T <= out_cap and lengths[b] + T <= the
+ * cache length before each step (the Python host keeps upper bounds and raises first). */
 int lollm_spec_commit(const int32_t* verify_ids, const int32_t* n_accepted,
                       const int32_t* next_token, int32_t* lengths, int32_t* rec_slot,
                       int32_t* conv_off, int32_t* pending, int32_t* out_tokens, int32_t* out_count,
                       int out_cap, const void* hidden, void* h_last, int B, int T, int H,
                       int slots, int win_rows, long long* offset, int32_t* accept_hist,
-                      void* stream);
+                      uint32_t* seen, int seen_words, void* stream);
+
+/* Repetition penalty of sample_next (src/generate.py:18-22), in place on bf16 logits, before
+ * any sampler kernel reads them: every token of a row's penalty set becomes
+ * bf16(x / penalty) if x > 0 else bf16(x * penalty), each computed in fp32 and rounded once
+ * (torch's arithmetic on bf16 tensors), each token once however often it occurs
+ * (the reference's set(prev_ids)).
+ *   logits  B * T rows of V bf16, row (b, t) at logits + (b * T + t) * ld
+ *   seen    (B, words) uint32, words >= ceil(V / 32): bit v of row b set iff token v is in
+ *           sequence b's context (prompt, emitted tokens, the pending token)
+ *   extra   (B, extra_stride) int32 or NULL: row (b, t) also penalises
+ *           extra[b * extra_stride + 0 .. n_extra0 + t - 1] -- the drafts verified before
+ *           position t, which the reference appends to its context (mtp.py:150) before it
+ *           samples the next position -- skipping tokens already in the bitmap
+ * Replaces: the index / where / scatter of generate.py:18-22 over set(prev_ids), on the
+ * device and inside a captured step.  penalty > 0; B * T <= 65535. */
+int lollm_repetition_penalty(void* logits, long long ld, int B, int T, int V, const uint32_t* seen,
+                             int words, const int32_t* extra, int extra_stride, int n_extra0,
+                             float penalty, void* stream);
+
+/* seen[b] |= { tok[b * tok_stride + i] : i < n } for b < B (tokens outside [0, V) ignored):
+ * builds the repetition-penalty context of lollm_repetition_penalty from a prompt or a
+ * token list.  Replaces: the context list of src/generate.py:45,56 / mtp.py:108,129. */
+int lollm_seen_mark(uint32_t* seen, int words, int B, const int32_t* tok, long long tok_stride,
+                    int n, int V, void* stream);
 
 #ifdef __cplusplus
 }

@@ -314,7 +314,7 @@ __global__ __launch_bounds__(256) void spec_commit_kernel(
     const int32_t* __restrict__ next_tok, int32_t* lengths, int32_t* rec_slot, int32_t* conv_off,
     int32_t* pending, int32_t* out_tokens, int32_t* out_count, int cap,
     const uint16_t* __restrict__ hidden, uint16_t* __restrict__ h_last, int H, int T, int S,
-    int W, long long* offset, int* hist) {
+    int W, long long* offset, int* hist, uint32_t* seen, int words) {
   const int b = blockIdx.x;
   int a = n_acc[b];
   a = a < 0 ? 0 : (a > T - 1 ? T - 1 : a);
@@ -330,6 +330,13 @@ __global__ __launch_bounds__(256) void spec_commit_kernel(
       if (c + i < cap) out_tokens[(size_t)b * cap + c + i] = verify_ids[b * T + i];
     out_count[b] = c + a + 1;
     pending[b] = next_tok[b];
+    if (seen) {   // the repetition-penalty context: accepted drafts and the new pending token
+      uint32_t* sb = seen + (size_t)b * words;
+      for (int i = 1; i <= a + 1; ++i) {
+        const int t = i <= a ? verify_ids[b * T + i] : next_tok[b];
+        if (t >= 0 && t < 32 * words) atomicOr(&sb[t >> 5], 1u << (t & 31));
+      }
+    }
     if (hist) atomicAdd(&hist[a], 1);
     if (b == 0) offset[0] += 1;
   }
@@ -417,15 +424,17 @@ LOLLM_API int lollm_spec_commit(const int32_t* verify_ids, const int32_t* n_acce
                                 int32_t* conv_off, int32_t* pending, int32_t* out_tokens,
                                 int32_t* out_count, int out_cap, const void* hidden, void* h_last,
                                 int B, int T, int H, int slots, int win_rows, long long* offset,
-                                int32_t* accept_hist, void* stream) {
+                                int32_t* accept_hist, uint32_t* seen, int seen_words,
+                                void* stream) {
   if (!verify_ids || !n_accepted || !next_token || !lengths || !rec_slot || !conv_off ||
       !pending || !out_tokens || !out_count || !hidden || !h_last || !offset)
     return LOLLM_EINVAL;
   if (B <= 0 || T <= 0 || H <= 0 || out_cap <= 0 || slots < T || win_rows <= 0) return LOLLM_EINVAL;
   if (H % 8) return LOLLM_EUNSUPPORTED;
+  if (seen && seen_words <= 0) return LOLLM_EINVAL;
   hipLaunchKernelGGL(spec_commit_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, verify_ids,
                      n_accepted, next_token, lengths, rec_slot, conv_off, pending, out_tokens,
                      out_count, out_cap, (const uint16_t*)hidden, (uint16_t*)h_last, H, T, slots,
-                     win_rows, offset, accept_hist);
+                     win_rows, offset, accept_hist, seen, seen_words);
   return launch_status();
 }

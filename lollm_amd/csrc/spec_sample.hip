@@ -890,6 +890,60 @@ __global__ __launch_bounds__(SP_THREADS) void sample_rows_kernel(
   if (threadIdx.x == 0) out[r] = tok;
 }
 
+// Repetition penalty (src/generate.py:18-22) in place on bf16 logit rows: a token of the
+// row's penalty set becomes bf16(x / p) if x > 0 else bf16(x * p), computed in fp32 as
+// torch computes bf16 arithmetic (one rounding of the fp32 quotient / product to bf16).
+// Grid (word blocks, rows): a thread owns one 32-bit word of the sequence's seen bitmap,
+// i.e. 32 consecutive tokens, so no two threads touch the same token; thread 0 of
+// block 0 of row (b, t) also applies the extra tokens (the drafts verified before
+// position t), each once, skipping those already in the bitmap.
+__device__ __forceinline__ void penalise(uint16_t* p, float pen) {
+  const float x = __uint_as_float((uint32_t)*p << 16);
+  const float y = x > 0.f ? x / pen : x * pen;
+  *p = f32_to_bf16(y);
+}
+
+__global__ __launch_bounds__(256) void repetition_penalty_kernel(
+    uint16_t* __restrict__ logits, long long ld, int T, int V, const uint32_t* __restrict__ seen,
+    int words, const int32_t* __restrict__ extra, int extra_stride, int n0, float pen) {
+  const int row = blockIdx.y, b = row / T, t = row - b * T;
+  uint16_t* x = logits + (size_t)row * ld;
+  const uint32_t* sb = seen + (size_t)b * words;
+  const int w = blockIdx.x * 256 + threadIdx.x;
+  const int wmax = (V + 31) / 32;
+  if (w < wmax) {
+    uint32_t bits = sb[w];
+    while (bits) {
+      const int bit = __ffs(bits) - 1;
+      bits &= bits - 1;
+      const int tok = 32 * w + bit;
+      if (tok < V) penalise(x + tok, pen);
+    }
+  }
+  if (extra && blockIdx.x == 0 && threadIdx.x == 0) {
+    const int32_t* e = extra + (size_t)b * extra_stride;
+    const int n = n0 + t;
+    for (int j = 0; j < n; ++j) {
+      const int tok = e[j];
+      if (tok < 0 || tok >= V || ((sb[tok >> 5] >> (tok & 31)) & 1u)) continue;
+      bool dup = false;
+      for (int i = 0; i < j; ++i) dup |= e[i] == tok;
+      if (!dup) penalise(x + tok, pen);
+    }
+  }
+}
+
+// seen[b] |= {tok[b * tok_stride + i] : i < n} (tokens outside [0, V) ignored).
+__global__ void seen_mark_kernel(uint32_t* __restrict__ seen, int words,
+                                 const int32_t* __restrict__ tok, long long tok_stride, int n,
+                                 int V) {
+  const int b = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int t = tok[(size_t)b * tok_stride + i];
+  if (t >= 0 && t < V) atomicOr(&seen[(size_t)b * words + (t >> 5)], 1u << (t & 31));
+}
+
 __global__ void philox_kernel(uint64_t seed, uint64_t offset, int rows, int slots, uint32_t* out) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < rows * slots) out[i] = philox_u24(seed, offset, (uint32_t)(i / slots), (uint32_t)(i % slots));
@@ -1037,5 +1091,31 @@ LOLLM_API int lollm_philox_uniform_u24(uint64_t seed, uint64_t offset, int rows,
   const int n = rows * slots;
   hipLaunchKernelGGL(philox_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
                      seed, offset, rows, slots, out);
+  return launch_status();
+}
+
+LOLLM_API int lollm_repetition_penalty(void* logits, long long ld, int B, int T, int V,
+                                       const uint32_t* seen, int words, const int32_t* extra,
+                                       int extra_stride, int n_extra0, float penalty,
+                                       void* stream) {
+  if (!logits || !seen || B <= 0 || T <= 0 || V <= 0 || ld < V || n_extra0 < 0) return LOLLM_EINVAL;
+  if (words < (V + 31) / 32 || (long long)B * T > 65535) return LOLLM_EINVAL;
+  if (extra && extra_stride < n_extra0 + T - 1) return LOLLM_EINVAL;
+  if (!(penalty > 0.f) || !(penalty < 3.0e38f)) return LOLLM_EINVAL;
+  const int wmax = (V + 31) / 32;
+  hipLaunchKernelGGL(repetition_penalty_kernel, dim3((wmax + 255) / 256, B * T), dim3(256), 0,
+                     (hipStream_t)stream, (uint16_t*)logits, ld, T, V, seen, words, extra,
+                     extra_stride, n_extra0, penalty);
+  return launch_status();
+}
+
+LOLLM_API int lollm_seen_mark(uint32_t* seen, int words, int B, const int32_t* tok,
+                              long long tok_stride, int n, int V, void* stream) {
+  if (!seen || !tok || B <= 0 || B > 65535 || n < 0 || V <= 0 || words < (V + 31) / 32 ||
+      tok_stride < n)
+    return LOLLM_EINVAL;
+  if (n == 0) return LOLLM_OK;
+  hipLaunchKernelGGL(seen_mark_kernel, dim3((n + 255) / 256, B), dim3(256), 0, (hipStream_t)stream,
+                     seen, words, tok, tok_stride, n, V);
   return launch_status();
 }

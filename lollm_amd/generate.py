@@ -21,14 +21,18 @@ SEED = 0x5EED
 
 def sample_next(logits, temperature, top_k, top_p, repetition_penalty=1.0, prev_ids=None,
                 seed=None, offset=None):
-    """(V,) logits on the device -> int token."""
+    """(V,) logits on the device -> int token.  The repetition penalty runs in the
+    lollm_repetition_penalty kernel over the bitmap of set(prev_ids) (generate.py:18-22,
+    bf16 arithmetic as the reference's GPU logits have), on a copy of the row."""
     x = logits.reshape(1, -1)
+    V = x.shape[1]
+    x = x.to(torch.bfloat16)
+    if x.data_ptr() == logits.data_ptr() or not x.is_contiguous():
+        x = x.clone(memory_format=torch.contiguous_format)
     if repetition_penalty != 1.0 and prev_ids:
-        idx = torch.tensor(sorted(set(prev_ids)), device=x.device, dtype=torch.long)
-        x = x.clone()
-        s = x[0, idx]
-        x[0, idx] = torch.where(s > 0, s / repetition_penalty, s * repetition_penalty)
-    x = x.to(torch.bfloat16).contiguous()
+        seen = ops.new_seen(1, V, x.device)
+        ops.seen_mark(seen, torch.tensor(list(prev_ids), dtype=torch.int32, device=x.device), V)
+        ops.repetition_penalty(x, seen, repetition_penalty)
     off = next(_draws) if offset is None else offset
     tok = ops.sample_rows(x, temperature, top_k or 0, top_p if top_p else 1.0,
                           SEED if seed is None else seed, off)
@@ -38,11 +42,13 @@ def sample_next(logits, temperature, top_k, top_p, repetition_penalty=1.0, prev_
 @torch.no_grad()
 def generate(model, ids, decode, stop_ids, device="cuda", *, max_new_tokens=128,
              temperature=0.7, top_k=20, top_p=0.8, repetition_penalty=1.1):
-    """generate.py:40-62: prefill, then one token per forward; yields text pieces."""
+    """generate.py:40-62: prefill, then one token per forward; yields text pieces.  The
+    cache holds the prompt plus max_new_tokens (the reference's grows without bound)."""
     input_ids = torch.tensor([ids], device=device)
     context = list(ids)
     eos = set(stop_ids)
-    logits, past = model(input_ids)
+    past = model.new_cache(1, len(ids) + max_new_tokens + 1)
+    logits, past = model(input_ids, past)
     nxt = sample_next(logits[0, -1], temperature, top_k, top_p, repetition_penalty, context)
     generated, prev = [], ""
     for _ in range(max_new_tokens):

@@ -208,12 +208,18 @@ def gemm_workspace_bytes(M, N, K, grid=0):
     return n
 
 
+_gemm_ws_retired = []
+
+
 def gemm_workspace(nbytes, device):
-    """The shared piece buffer of lollm_gemm (one per device, grown on demand; reserve
-    the largest size before capturing a graph)."""
+    """The shared piece buffer of lollm_gemm (one per device, grown on demand; models
+    reserve their largest size when they are built).  A buffer that is outgrown is kept
+    alive, never freed: a HIP graph captured earlier may still write to its address."""
     key = torch.device(device)
     ws = _gemm_ws.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _gemm_ws_retired.append(ws)
         ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=key)
         _gemm_ws[key] = ws
     return ws
@@ -534,12 +540,82 @@ def gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot
 
 
 def spec_commit(verify_ids, n_accepted, next_token, lengths, rec_slot, conv_off, pending,
-                out_tokens, out_count, hidden, h_last, offset, slots, win_rows, accept_hist=None):
+                out_tokens, out_count, hidden, h_last, offset, slots, win_rows, accept_hist=None,
+                seen=None):
     B, T = verify_ids.shape
     H = hidden.shape[-1]
+    if seen is not None:
+        _need(seen, "seen", torch.int32)
+        if seen.dim() != 2 or seen.shape[0] != B:
+            raise ValueError("seen must be (B, words) int32")
     rc = _lib.lib().lollm_spec_commit(
         _ptr(verify_ids), _ptr(n_accepted), _ptr(next_token), _ptr(lengths), _ptr(rec_slot),
         _ptr(conv_off), _ptr(pending), _ptr(out_tokens), _ptr(out_count), out_tokens.shape[1],
         _ptr(hidden), _ptr(h_last), B, T, H, slots, win_rows, _ptr(offset), _ptr(accept_hist),
-        _stream())
+        _ptr(seen), 0 if seen is None else seen.shape[1], _stream())
     _lib.check(rc, "lollm_spec_commit")
+
+
+# ------------------------------------------------------------------------------------
+# repetition penalty (src/generate.py:18-22) on the device
+# ------------------------------------------------------------------------------------
+def seen_words(V):
+    """32-bit words of one sequence's seen-token bitmap."""
+    return (V + 31) // 32
+
+
+def new_seen(B, V, device):
+    """Empty (B, words) seen-token bitmaps (int32 storage of the uint32 words)."""
+    return torch.zeros(B, seen_words(V), dtype=torch.int32, device=device)
+
+
+def seen_mark(seen, tokens, V):
+    """seen[b] |= set(tokens[b]) for tokens (B, n) or (B,) integer ids on the device."""
+    _need(seen, "seen", torch.int32)
+    B = seen.shape[0]
+    t = tokens.reshape(B, -1)
+    if t.dtype != torch.int32 or t.stride(-1) != 1:
+        t = t.to(torch.int32).contiguous()
+    n = t.shape[1]
+    rc = _lib.lib().lollm_seen_mark(_ptr(seen), seen.shape[1], B, _ptr(t), t.stride(0), n, V,
+                                    _stream())
+    _lib.check(rc, "lollm_seen_mark")
+    return seen
+
+
+def repetition_penalty(logits, seen, penalty, extra=None, n_extra0=0):
+    """In place on bf16 logits (B, T, V) (or (B, V) = T 1): row (b, t) penalises the tokens
+    of seen[b] plus extra[b, :n_extra0 + t] (each once), the reference's
+    where(x > 0, x / p, x * p) in bf16 arithmetic.  Returns logits."""
+    if logits.dim() == 2:
+        B, V = logits.shape
+        T = 1
+    else:
+        B, T, V = logits.shape
+    if logits.dtype != torch.bfloat16 or not logits.is_cuda or logits.stride(-1) != 1:
+        raise ValueError("logits must be bf16 on the device with unit column stride")
+    # the kernel addresses row (b, t) at (b * T + t) * ld: one row stride for all rows
+    # (strides of size-1 dimensions are irrelevant)
+    if T > 1:
+        ld = logits.stride(-2)
+        if B > 1 and logits.stride(0) != T * ld:
+            raise ValueError("logits rows must be evenly strided")
+    else:
+        ld = logits.stride(0) if B > 1 else V
+    if ld < V:
+        raise ValueError("logits rows overlap")
+    _need(seen, "seen", torch.int32)
+    if seen.shape[0] != B or seen.shape[1] < seen_words(V):
+        raise ValueError("seen must be (B, >= ceil(V / 32)) int32")
+    stride = 0
+    if extra is not None:
+        if extra.dtype != torch.int32 or extra.dim() != 2 or extra.shape[0] != B or extra.stride(1) != 1:
+            raise ValueError("extra must be (B, n) int32 with unit column stride")
+        stride = extra.stride(0)
+        if extra.shape[1] < n_extra0 + T - 1:
+            raise ValueError("extra has fewer tokens than the rows need")
+    rc = _lib.lib().lollm_repetition_penalty(_ptr(logits), ld, B, T, V, _ptr(seen), seen.shape[1],
+                                             _ptr(extra), stride, int(n_extra0), float(penalty),
+                                             _stream())
+    _lib.check(rc, "lollm_repetition_penalty")
+    return logits

@@ -22,30 +22,31 @@ def _cat_rows(*ws):
     return torch.cat([w.reshape(w.shape[0], -1) for w in ws], 0).contiguous()
 
 
-_FLUSH = {}
-_SHAPE_CHOICE = {}   # (N, K, epilogue, rows or ("norm", rows)) -> "gemm" | "gemm1" | "blas"
+# Fixed GEMM path per projection shape, so a given (weights, inputs) gives the same bits in
+# every process (a timing-based choice could differ between runs and change rounding).
+# Rows <= 64 take lollm_gemm on one workgroup per CU, except the shapes listed here, which
+# measured faster on hipBLASLt at that row count with cold caches (weights streaming
+# from HBM, as in a step that walks every layer):
+#   (N, K, epilogue, rows) -> "blas"
+BLAS_SHAPES = {
+    (12352, 4096, 0, 64),      # GDN in_proj of the 4096-hidden model, verify pass
+    (151936, 4096, 0, 64),     # lm_head of the 151936-vocabulary model, verify pass
+}
 
 
-def _flush_caches(device):
-    """Read a 512 MiB buffer: evicts earlier data from L2 and the 256 MiB last-level
-    cache, so the next kernel's weight reads go to HBM."""
-    buf = _FLUSH.get(device)
-    if buf is None:
-        buf = _FLUSH[device] = torch.ones(1 << 27, dtype=torch.float32, device=device)
-    buf.sum()
+def gemm_path(N, K, epilogue, rows, tiled=True):
+    """'gemm' (lollm_gemm, one workgroup per CU) or 'blas' (hipBLASLt) for a projection
+    call; a pure function of the shape."""
+    if not tiled or rows > ops.GEMM_MAX_ROWS:
+        return "blas"
+    return "blas" if (N, K, epilogue, rows) in BLAS_SHAPES else "gemm"
 
 
 class Projection:
     """y = x W^T (blocks.py's nn.Linear layers, no bias).  Keeps the row-major weight
     for hipBLASLt (F.linear) and a tiled copy for lollm_gemm (<= 64 rows).
     epilogue=GEMM_SWIGLU: W = [gate; up], y = silu(x gate^T) * x up^T (blocks.py:341-342).
-
-    For a row count lollm_gemm supports, the first eager call of a weight shape times
-    both paths (five runs each, alternating, HIP events, each run after the caches were
-    flushed so the weight streams from HBM as it does in a step that walks every layer)
-    and keeps the faster median for that (shape, row count); every projection of that
-    shape -- and later calls and HIP-graph captures -- reuse the choice.  A call under
-    capture with no choice recorded yet takes lollm_gemm."""
+    The path of each call is gemm_path() of its shape."""
 
     def __init__(self, weight, epilogue=ops.GEMM_NONE):
         self.weight = weight.to(torch.bfloat16).contiguous()
@@ -54,81 +55,43 @@ class Projection:
         self.tiled = (ops.gemm_tile_weights(self.weight, epilogue)
                       if self.weight.is_cuda and ops.gemm_supported(self.N, self.K, epilogue)
                       else None)
-        self.choice = {}            # rows -> "gemm" | "gemm1" | "blas"
 
     def workspace_bytes(self, rows=ops.GEMM_MAX_ROWS):
-        return ops.gemm_workspace_bytes(rows, self.N, self.K) if self.tiled is not None else 0
+        if self.tiled is None:
+            return 0
+        return max(ops.gemm_workspace_bytes(rows, self.N, self.K),
+                   ops.gemm_workspace_bytes(rows, self.N, self.K, _cus()))
+
+    def path(self, rows):
+        return gemm_path(self.N, self.K, self.epilogue, rows, self.tiled is not None)
+
+    def argmax_grid(self, rows):
+        """Workgroups of the fused lm_head argmax (lollm_gemm_argmax): one per CU."""
+        return _cus()
 
     def _blas(self, x):
         y = F.linear(x, self.weight)
         return ops.swiglu(y) if self.epilogue == ops.GEMM_SWIGLU else y
 
-    def _gemm(self, x, grid=0):
-        return ops.gemm(x, self.tiled, self.N, self.K, self.epilogue, grid=grid)
-
-    def _pick(self, key, paths):
-        shape = (self.N, self.K, self.epilogue, key)
-        if shape in _SHAPE_CHOICE:
-            self.choice[key] = _SHAPE_CHOICE[shape]
-            return self.choice[key]
-        if torch.cuda.is_current_stream_capturing():
-            return "gemm"
-        times = {name: [] for name in paths}
-        for fn in paths.values():
-            fn()
-        for _ in range(5):
-            for name, fn in paths.items():
-                _flush_caches(torch.cuda.current_device())
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                fn()
-                e1.record()
-                e1.synchronize()
-                times[name].append(e0.elapsed_time(e1))
-        choice = min(times, key=lambda n: sorted(times[n])[len(times[n]) // 2])
-        _SHAPE_CHOICE[shape] = self.choice[key] = choice
-        return choice
-
     def __call__(self, x):
         rows = x.numel() // self.K
-        if self.tiled is None or rows > ops.GEMM_MAX_ROWS:
+        if self.path(rows) == "blas":
             return self._blas(x)
-        # lollm_gemm with its default grid (two workgroups per CU) or one per CU (half the
-        # split-K pieces to merge), or hipBLASLt: the fastest on cold caches
-        g1 = _cus()
-        choice = self.choice.get(rows) or self._pick(
-            rows, {"gemm": lambda: self._gemm(x), "gemm1": lambda: self._gemm(x, g1),
-                   "blas": lambda: self._blas(x)})
-        if choice == "blas":
-            return self._blas(x)
-        return self._gemm(x, g1 if choice == "gemm1" else 0)
+        return ops.gemm(x, self.tiled, self.N, self.K, self.epilogue, grid=_cus())
 
     def add_norm(self, x, residual, norm):
         """The projection feeding the residual stream with the add and the next RMSNorm
         (modeling_qwen3_5.py:59-60): x_out = residual + x W^T, y = norm(x_out); returns
         (y, x_out).  lollm_gemm_rmsnorm (one GEMM call, the norm fused into its second
-        kernel) or F.linear + lollm_rmsnorm, chosen per row count as in __call__."""
+        kernel) when the path is lollm_gemm and the shape fits it, else the projection
+        followed by lollm_rmsnorm."""
         rows = x.numel() // self.K
-        if (self.tiled is None or self.epilogue != ops.GEMM_NONE
-                or not ops.gemm_rmsnorm_supported(rows, self.N, self.K)):
-            return norm(self._blas(x), residual=residual)
-
-        def fused(grid=0):
-            return ops.gemm_rmsnorm(x, self.tiled, self.N, self.K, residual, norm.weight, norm.eps,
-                                    grid=grid)
-
-        def unfused():
-            return norm(self._blas(x), residual=residual)
-
         g1 = _cus()
-        key = ("norm", rows)
-        paths = {"gemm": fused, "blas": unfused}
-        if ops.gemm_rmsnorm_supported(rows, self.N, self.K, g1):
-            paths["gemm1"] = lambda: fused(g1)
-        choice = self.choice.get(key) or self._pick(key, paths)
-        if choice == "blas":
-            return unfused()
-        return fused(g1 if choice == "gemm1" else 0)
+        if (self.path(rows) == "gemm" and self.epilogue == ops.GEMM_NONE
+                and ops.gemm_rmsnorm_supported(rows, self.N, self.K, g1)):
+            return ops.gemm_rmsnorm(x, self.tiled, self.N, self.K, residual, norm.weight, norm.eps,
+                                    grid=g1)
+        return norm(self(x), residual=residual)
 
 
 _CUS = {}

@@ -26,6 +26,11 @@ import torch
 from .config import Qwen3_5Config
 
 
+def capturing() -> bool:
+    """Whether the current stream is recording a HIP graph (False without a device)."""
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
 class Qwen3_5Cache:
     def __init__(self, cfg: Qwen3_5Config, batch: int, max_len: int, spec_slots: int = 4,
                  device="cuda"):
@@ -53,10 +58,32 @@ class Qwen3_5Cache:
         self.rec_slot = torch.zeros(batch, dtype=torch.int32, device=device)
         self.conv_off = torch.zeros(batch, dtype=torch.int32, device=device)
         self.last_T = 0
+        # host-side upper bound of max(lengths): every forward or speculative step adds
+        # its T, rollbacks leave it, so capacity is checked without reading the device
+        self.len_bound = 0
 
     @property
     def win_rows(self):
         return self.cfg.linear_conv_kernel_dim - 1 + self.spec_slots
+
+    # -- capacity ----------------------------------------------------------------------
+    def reserve(self, T: int):
+        """Raise RuntimeError unless T more rows fit every sequence (lengths + T <=
+        max_len) -- the kernels would otherwise drop the KV rows past the end.  Reads the
+        device lengths (a host sync) only when the host-side bound says they may not fit."""
+        if self.len_bound + T <= self.max_len:
+            return
+        if capturing():
+            raise RuntimeError(f"KV cache capacity: {self.len_bound} + {T} rows may exceed "
+                               f"max_len {self.max_len} (cannot check exactly under capture)")
+        self.len_bound = int(self.lengths.max()) if self.batch else 0
+        if self.len_bound + T > self.max_len:
+            raise RuntimeError(f"KV cache capacity exceeded: a sequence holds {self.len_bound} "
+                               f"tokens, {T} more do not fit max_len {self.max_len}")
+
+    def grew(self, T: int):
+        """Record that a call may have added up to T tokens to every sequence."""
+        self.len_bound += T
 
     # -- bookkeeping used by the model's forward -------------------------------------
     def commit_all(self, T: int):
@@ -71,6 +98,7 @@ class Qwen3_5Cache:
         self.rec_slot.copy_(torch.where(self.rec_slot >= S, 0, S) + (T - 1 if snap else 0))
         self.conv_off.copy_(torch.where(self.conv_off >= W, 0, W) + (T if full else 0))
         self.lengths.add_(T)
+        self.grew(T)
 
     def rollback(self, n_accepted: torch.Tensor):
         """After commit_all(T) with T <= spec_slots: keep n_accepted[b] + 1 tokens."""
@@ -94,7 +122,9 @@ class Qwen3_5Cache:
         return self._uniform_length()
 
     def advance(self, n):
+        self.reserve(n)
         self.lengths.add_(n)
+        self.grew(n)
 
     def append_kv(self, layer, k, v):
         """Write k, v (B, n_kv, t, D) at the current length; return the full (K, V)."""

@@ -66,7 +66,7 @@ class Qwen3_5Model:
                              for i in range(cfg.num_hidden_layers)]
         self.model.norm = RMSNorm(W["model.norm.weight"], cfg.rms_norm_eps)
         self.lm_head = Projection(W["lm_head.weight"])
-        self.attn_grid = 0          # attention workgroups (0: two per CU)
+        self.attn_grid = 0          # attention workgroups (0: one per CU)
         ops.gemm_workspace(max(p.workspace_bytes() for p in self.projections()), self.device)
         self._ws = {}
         self.default_extra_capacity = 4096
@@ -98,6 +98,7 @@ class Qwen3_5Model:
     def forward(self, input_ids, past=None, return_hidden=False, logits="all"):
         B, T = input_ids.shape
         cache = past if past is not None else self.new_cache(B, T + self.default_extra_capacity)
+        cache.reserve(T)                  # raise before any KV row could land past max_len
         x, normed = self.hidden_states(input_ids, cache)
         if logits == "last":
             out = self.lm_head(normed[:, -1:])
@@ -110,7 +111,8 @@ class Qwen3_5Model:
 
     def hidden_states(self, input_ids, cache):
         """The decoder stack; returns (pre-norm hidden, final-normed hidden).  Writes
-        the KV rows / GDN snapshots of the T new tokens but does not commit them."""
+        the KV rows / GDN snapshots of the T new tokens but does not commit them.  The
+        caller has checked the capacity (cache.reserve(T))."""
         B, T = input_ids.shape
         cfg = self.cfg
         x = self.model.embed_tokens(input_ids.to(self.device))

@@ -27,7 +27,8 @@ from __future__ import annotations
 import torch
 
 from .. import ops
-from .blocks import Projection, RMSNorm, _cus
+from .blocks import Projection, RMSNorm
+from .kv import capturing
 from .modeling_qwen3_5 import DecoderLayer, Qwen3_5Model
 from .random_init import weight_shapes
 from .weights import take_weights, to_raw
@@ -126,16 +127,30 @@ class SpecDecoder:
     rejection sampling with p = sample_next's distribution (temperature, top-k,
     top-p) and q one-hot at the argmax draft (draft="argmax", the reference's
     drafting rule, mtp.py:138) or q = the MTP head's own distribution with sampled
-    drafts (draft="sample")."""
+    drafts (draft="sample").
+
+    repetition_penalty != 1 applies sample_next's penalty (src/generate.py:18-22) to
+    every verified position before acceptance, over each sequence's context as the
+    reference keeps it (prompt, emitted tokens, the pending token, and the drafts
+    verified before the position, mtp.py:108,129,150); argmax drafts are taken from the
+    unpenalised MTP logits as in mtp.py:138, sampled drafts from penalised ones.
+
+    Capacity: a step adds at most k + 1 tokens to a sequence; step() and replay() raise
+    RuntimeError before a step whose tokens might not fit the cache (max_len) or the
+    output buffer (out_capacity), from host-side upper bounds (exact values are read
+    from the device only when a bound says the step might not fit)."""
 
     def __init__(self, model: Qwen3_5Model, mtp: MTP, batch: int, max_len: int, k: int = 3,
                  temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0, seed: int = 0,
-                 draft: str = "argmax", out_capacity: int = 4096):
+                 draft: str = "argmax", out_capacity: int = 4096, repetition_penalty: float = 1.0):
         if draft not in ("argmax", "sample"):
             raise ValueError("draft must be 'argmax' or 'sample'")
+        if not repetition_penalty or repetition_penalty <= 0:
+            raise ValueError("repetition_penalty must be positive")
         self.model, self.mtp, self.k = model, mtp, k
         self.B = batch
         self.temperature, self.top_k, self.top_p, self.seed = temperature, top_k, top_p, seed
+        self.penalty = float(repetition_penalty)
         self.draft_mode = draft if temperature > 0 else "argmax"
         cfg, dev = model.cfg, model.device
         self.cache = model.new_cache(batch, max_len, spec_slots=k + 1)
@@ -146,10 +161,13 @@ class SpecDecoder:
         self.drafts = torch.zeros(batch, k, **i32)
         self.n_acc = torch.zeros(batch, **i32)
         self.next_tok = torch.zeros(batch, **i32)
+        self.out_capacity = out_capacity
         self.out_tokens = torch.zeros(batch, out_capacity, **i32)
         self.out_count = torch.zeros(batch, **i32)
+        self.out_bound = 0                                  # host upper bound of max(out_count)
         self.offset = torch.zeros(1, dtype=torch.int64, device=dev)
         self.accept_hist = torch.zeros(k + 1, **i32)       # accepted-length histogram
+        self.seen = (ops.new_seen(batch, cfg.vocab_size, dev) if self.penalty != 1.0 else None)
         self.spec_ws = torch.empty(max(ops._lib.lib().lollm_spec_workspace_bytes(batch, k, 1), 16),
                                    dtype=torch.uint8, device=dev)
         self.row_ws = torch.empty(ops.sample_workspace_bytes(batch), dtype=torch.uint8, device=dev)
@@ -165,13 +183,23 @@ class SpecDecoder:
     @torch.no_grad()
     def prefill(self, prompts):
         """prompts (B, L) long, equal lengths.  Runs the prompt through the model
-        (mtp.py:120-122) and samples the first pending token."""
+        (mtp.py:120-122) and samples the first pending token (penalised by the prompt,
+        mtp.py:122)."""
+        V = self.model.cfg.vocab_size
         logits, _, hidden = self.model(prompts, self.cache, return_hidden=True, logits="last")
-        self.pending.copy_(ops.sample_rows(logits[:, -1].contiguous(), self.temperature,
-                                           self.top_k, self.top_p, self.seed, 0,
-                                           slot=2 * self.k + 2, workspace=self.row_ws))
+        last = logits[:, -1].contiguous()
+        if self.seen is not None:
+            self.seen.zero_()
+            ops.seen_mark(self.seen, prompts.to(self.model.device), V)
+            ops.repetition_penalty(last, self.seen, self.penalty)
+        self.pending.copy_(ops.sample_rows(last, self.temperature, self.top_k, self.top_p,
+                                           self.seed, 0, slot=2 * self.k + 2,
+                                           workspace=self.row_ws))
+        if self.seen is not None:
+            ops.seen_mark(self.seen, self.pending, V)
         self.h_last.copy_(hidden[:, -1])
         self.out_count.zero_()
+        self.out_bound = 0
         self.offset.fill_(1)
 
     def _draft_chain(self):
@@ -184,44 +212,68 @@ class SpecDecoder:
             lm = model.lm_head
             if self.draft_mode == "sample":
                 lg = lm(normed).view(B, -1)
+                if self.seen is not None:
+                    # the context of draft j holds the drafts before it
+                    ops.repetition_penalty(lg, self.seen, self.penalty, extra=self.drafts,
+                                           n_extra0=j - 1)
                 self.draft_logits[:, j - 1].copy_(lg)
                 d = ops.sample_rows(lg, self.temperature, self.top_k, self.top_p, self.seed, 0,
                                     slot=k + 1 + j, offset_dev=self.offset, workspace=self.row_ws)
                 self.drafts[:, j - 1].copy_(d)
             elif lm.tiled is not None and B <= ops.GEMM_MAX_ROWS:
-                # greedy draft straight from the lm_head GEMM (no logits), into its column;
-                # the grid (two workgroups per CU or one) timed once per shape like the
-                # projections' paths
+                # greedy draft straight from the lm_head GEMM (no logits), into its column
                 x2 = normed.reshape(B, -1)
                 col = self.drafts[:, j - 1]
-                g1 = _cus()
-                key = ("argmax", B)
-                choice = lm.choice.get(key) or lm._pick(key, {
-                    "gemm": lambda: ops.gemm_argmax(x2, lm.tiled, lm.N, lm.K, out=col),
-                    "gemm1": lambda: ops.gemm_argmax(x2, lm.tiled, lm.N, lm.K, out=col, grid=g1)})
                 d = ops.gemm_argmax(x2, lm.tiled, lm.N, lm.K, out=col,
-                                    grid=g1 if choice == "gemm1" else 0)
+                                    grid=lm.argmax_grid(B))
             else:
                 d = ops.sample_rows(lm(normed).view(B, -1), 0.0, workspace=self.row_ws)
                 self.drafts[:, j - 1].copy_(d)
             tok, h = d, m
 
+    def _reserve(self):
+        """Raise before a step whose k + 1 tokens might not fit (see the class doc)."""
+        T = self.k + 1
+        self.cache.reserve(T)
+        if self.out_bound + T > self.out_capacity:
+            if capturing():
+                raise RuntimeError("output capacity may be exceeded (cannot check under capture)")
+            self.out_bound = int(self.out_count.max())
+            if self.out_bound + T > self.out_capacity:
+                raise RuntimeError(f"output capacity exceeded: a sequence holds {self.out_bound} "
+                                   f"tokens, a step may add {T}, out_capacity {self.out_capacity}")
+
+    def _grew(self):
+        self.cache.grew(self.k + 1)
+        self.out_bound += self.k + 1
+
     @torch.no_grad()
     def step(self):
         """One speculative step: k drafts, one verify pass over 1 + k positions, accept,
         commit.  Device-only (no host sync)."""
+        live = not capturing()
+        if live:
+            self._reserve()
+        self._step_kernels()
+        if live:
+            self._grew()
+
+    def _step_kernels(self):
         B, k, model, cache = self.B, self.k, self.model, self.cache
         self._draft_chain()
         verify_ids = torch.cat([self.pending.view(B, 1), self.drafts], 1)
         hidden, normed = model.hidden_states(verify_ids, cache)   # int32 ids: no widening copy
         logits = model.lm_head(normed)
+        if self.seen is not None:
+            # position t's context holds the pending token and the drafts before t
+            ops.repetition_penalty(logits, self.seen, self.penalty, extra=self.drafts)
         ops.spec_accept(logits, self.draft_logits, self.drafts, self.temperature, self.top_k,
                         self.top_p, self.seed, 0, offset_dev=self.offset,
                         workspace=self.spec_ws, n_accepted=self.n_acc, next_token=self.next_tok)
         ops.spec_commit(verify_ids, self.n_acc, self.next_tok, cache.lengths, cache.rec_slot,
                         cache.conv_off, self.pending, self.out_tokens, self.out_count,
                         hidden.contiguous(), self.h_last, self.offset, cache.spec_slots,
-                        cache.win_rows, self.accept_hist)
+                        cache.win_rows, self.accept_hist, seen=self.seen)
         cache.fresh = False
 
     def capture(self):
@@ -230,10 +282,12 @@ class SpecDecoder:
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.step()
+            self._step_kernels()
 
     def replay(self):
+        self._reserve()
         self.graph.replay()
+        self._grew()
 
     @torch.no_grad()
     def generate(self, n_steps, use_graph=False):
@@ -256,14 +310,13 @@ def generate_mtp(model, mtp: MTP, ids, decode, stop_ids, device="cuda", *, max_n
                  temperature=0.7, top_k=20, top_p=0.8, repetition_penalty=1.1, k=1, seed=0):
     """Drop-in for the reference's generate_mtp (mtp.py:92-162): yields text pieces.
     Runs the batched decoder with B = 1 and k drafts (k = 1 by default, as the
-    reference).  A repetition penalty other than 1.0 is not implemented by the
-    on-device sampler and raises."""
-    if repetition_penalty not in (None, 1.0):
-        raise NotImplementedError("repetition_penalty != 1.0 is not supported by the on-device sampler")
+    reference), with the reference's sampling arguments (run.py passes the family
+    defaults, repetition_penalty 1.05 included)."""
     eos = set(stop_ids)
+    pen = 1.0 if repetition_penalty is None else float(repetition_penalty)
     dec = SpecDecoder(model, mtp, 1, len(ids) + max_new_tokens + 2 * k + 8, k=k,
                       temperature=temperature, top_k=top_k, top_p=top_p, seed=seed,
-                      out_capacity=max_new_tokens + 2 * k + 2)
+                      out_capacity=max_new_tokens + 2 * k + 2, repetition_penalty=pen)
     dec.prefill(torch.tensor([ids], device=model.device))
     generated, prev = [], ""
     while True:

@@ -16,11 +16,14 @@ How each piece is pinned (see tests/test_oracle_*.py):
     offset-causal rule; decode (q_len == 1) and plain-causal special cases.
   * model_forward (+ RefCache): transformers Qwen3_5ForCausalLM logits on the same
     random weights (prefill and cached decode), and prefill == incremental.
-  * mtp_forward: L=1 closed form (softmax over one key => attention output = v),
-    and mtp_chain_draft == the full-recompute form.  Beyond that: parity unpinned
-    (no third-party implementation of the MTP head exists).
-  * sample_next: temperature->0 == argmax, top_p/top_k keep-set rules on
-    hand-built distributions.
+  * mtp_forward / speculate / generate_mtp_greedy / generate_greedy: vectors written by
+    tests/golden/make_golden_ref.py from the reference itself (MTP.forward at L = 1..4 and
+    explicit positions, speculate, and the greedy generate_mtp / generate trajectories
+    with and without a repetition penalty on the tiny and micro models), plus the L=1
+    closed form (softmax over one key => attention output = v).
+  * sample_next: the reference's own greedy picks under a repetition penalty
+    (tests/golden/ref_mtp.safetensors), temperature->0 == argmax, top_p/top_k keep-set
+    rules on hand-built distributions.
 """
 
 from __future__ import annotations
@@ -452,6 +455,15 @@ def mtp_forward(W, cfg, hidden, next_emb, positions=None):
 
 
 @torch.no_grad()
+def speculate(W, cfg, ids):
+    """mtp.py:76-89 -- MTP logits (B, T-1, V): row i scores the token at i + 2 from the
+    main model's hidden state at i and the embedding of token i + 1."""
+    _, _, hidden = model_forward(W, cfg, ids, return_hidden=True)
+    emb = W["model.embed_tokens.weight"][ids]
+    return linear(mtp_forward(W, cfg, hidden[:, :-1], emb[:, 1:]), W["lm_head.weight"])
+
+
+@torch.no_grad()
 def mtp_chain_draft(W, cfg, hidden_last, pending, k, forced=None):
     """The build's k-step draft chain restated in the reference's own no-cache form
     (mtp.py:61-73 with cache=None): draft j runs the MTP block over the whole draft
@@ -511,32 +523,43 @@ def sample_next(logits, temperature, top_k, top_p, repetition_penalty=1.0, prev_
     return int(torch.multinomial(F.softmax(logits, dim=-1), 1, generator=generator))
 
 
+def _greedy_pick(logits, penalty=1.0, context=None):
+    """generate.py:18-24 at temperature 0: argmax after the repetition penalty over
+    set(context), in the logits' dtype."""
+    return sample_next(logits, 0.0, 0, 1.0, penalty, context)
+
+
 @torch.no_grad()
-def generate_greedy(W, cfg, ids, n_new):
+def generate_greedy(W, cfg, ids, n_new, repetition_penalty=1.0):
     """generate.py:40-62 at temperature 0 (token ids only, no text)."""
+    context = list(ids)
     logits, past = model_forward(W, cfg, torch.tensor([ids]))
     out = []
-    nxt = int(logits[0, -1].argmax())
+    nxt = _greedy_pick(logits[0, -1], repetition_penalty, context)
     for _ in range(n_new):
         out.append(nxt)
+        context.append(nxt)
         logits, past = model_forward(W, cfg, torch.tensor([[nxt]]), past)
-        nxt = int(logits[0, -1].argmax())
+        nxt = _greedy_pick(logits[0, -1], repetition_penalty, context)
     return out
 
 
 @torch.no_grad()
-def generate_mtp_greedy(W, cfg, ids, n_new):
-    """mtp.py:92-162 at temperature 0 with k = 1: draft by MTP argmax, snapshot,
-    verify [pending, draft], accept iff draft == argmax(logits[0]); on reject
-    restore the snapshot and re-run the pending token alone.  Returns the token ids
-    and the per-step accepted-draft counts."""
+def generate_mtp_greedy(W, cfg, ids, n_new, repetition_penalty=1.0):
+    """mtp.py:92-162 at temperature 0 with k = 1: draft by MTP argmax (no penalty,
+    mtp.py:138), snapshot, verify [pending, draft], accept iff draft == the penalised
+    argmax of logits[0]; on reject restore the snapshot and re-run the pending token
+    alone.  The penalty context is the prompt plus every emitted token
+    (mtp.py:108,129,150).  Returns the token ids and the per-step accepted-draft counts."""
+    context = list(ids)
     logits, past, hidden = model_forward(W, cfg, torch.tensor([ids]), return_hidden=True)
     h_last = hidden[:, -1:]
-    pending = int(logits[0, -1].argmax())
+    pending = _greedy_pick(logits[0, -1], repetition_penalty, context)
     out, accepts = [], []
     emb_w = W["model.embed_tokens.weight"]
     while len(out) < n_new:
         out.append(pending)
+        context.append(pending)
         if len(out) >= n_new:
             break
         x = mtp_forward(W, cfg, h_last, emb_w[torch.tensor([[pending]])])
@@ -544,13 +567,14 @@ def generate_mtp_greedy(W, cfg, ids, n_new):
         snap = past.clone()
         lg2, past, hid2 = model_forward(W, cfg, torch.tensor([[pending, draft]]), past,
                                         return_hidden=True)
-        true_next = int(lg2[0, 0].argmax())
+        true_next = _greedy_pick(lg2[0, 0], repetition_penalty, context)
         if draft == true_next:
             accepts.append(1)
             out.append(draft)
+            context.append(draft)
             if len(out) >= n_new:
                 break
-            pending = int(lg2[0, 1].argmax())
+            pending = _greedy_pick(lg2[0, 1], repetition_penalty, context)
             h_last = hid2[:, 1:2]
         else:
             accepts.append(0)

@@ -317,3 +317,33 @@ int oracle_spec_accept(const uint16_t* target, const uint16_t* draft, const int3
   free(counts);
   return 0;
 }
+
+/* ------------------------------------------------------------ repetition penalty */
+/* generate.py:18-22 on one bf16 row: every distinct id of ids[0..n) in [0, V) becomes
+ * bf16(x / penalty) if x > 0 else bf16(x * penalty), each computed in fp32 and rounded
+ * to bf16 once, to nearest even -- what torch does for `s / p` and `s * p` on a bf16
+ * tensor with a Python float (the fp32 opmath of its CPU kernels). */
+static uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+int oracle_repetition_penalty(uint16_t* row, int V, const int32_t* ids, int n, float penalty) {
+  unsigned char* mark = (unsigned char*)calloc((size_t)V, 1);
+  if (!mark) return 1;
+  for (int i = 0; i < n; ++i)
+    if (ids[i] >= 0 && ids[i] < V) mark[ids[i]] = 1;
+  for (int v = 0; v < V; ++v) {
+    if (!mark[v]) continue;
+    uint32_t bits = (uint32_t)row[v] << 16;
+    float x;
+    memcpy(&x, &bits, 4);
+    float y = x > 0.0f ? x / penalty : x * penalty;
+    row[v] = f32_to_bf16_rne(y);
+  }
+  free(mark);
+  return 0;
+}

@@ -45,6 +45,7 @@ def lib():
         L.oracle_spec_accept.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                          ctypes.c_float, ctypes.c_int, ctypes.c_float,
                                          ctypes.c_uint64, ctypes.c_uint64, P, P]
+        L.oracle_repetition_penalty.argtypes = [P, ctypes.c_int, P, ctypes.c_int, ctypes.c_float]
         _lib = L
     return _lib
 
@@ -126,3 +127,14 @@ def spec_accept(target, draft, drafts, inv_temp, top_k, top_p, seed, offset):
     if rc:
         raise RuntimeError(f"oracle_spec_accept failed ({rc})")
     return na, nt
+
+
+def repetition_penalty(row, ids, penalty):
+    """generate.py:18-22 on one bf16 row (uint16 bits or a torch bf16 tensor): returns the
+    penalised row as uint16 bits.  ids: the context token ids (duplicates allowed)."""
+    xb = _bits(row).reshape(-1).copy()
+    ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int64).reshape(-1), dtype=np.int32)
+    rc = lib().oracle_repetition_penalty(_ptr(xb), xb.size, _ptr(ids), ids.size, penalty)
+    if rc:
+        raise RuntimeError("oracle_repetition_penalty failed")
+    return xb

@@ -146,3 +146,21 @@ def test_attn_small_equals_prologue_then_verify(B, Hq, Hkv, rd, lens, rope):
     assert (g32 != r32).float().mean().item() <= 0.02
     o = oracle(q.cpu(), kc2.cpu(), vc2.cpu(), kv_len.cpu(), gate.cpu())
     torch.testing.assert_close(g32.view(B, -1), o.view(B, -1), **TOL)
+
+
+def test_attn_verify_c3_full_batch():
+    """The isolated verify workload at full size: B = 16, 1 + k = 4 queries, 16 q / 2 kv
+    heads of 256, contexts U[1024, 32768] (seeded).  Four sequences spread over the batch
+    against the oracle; all 16 through split invariance (the balanced split deals the
+    blocks of all sequences out together, so a grid change moves every cut)."""
+    from lollm_amd import ops
+    gen = torch.Generator().manual_seed(33)
+    lens = torch.randint(1024, 32769, (16,), generator=gen).tolist()
+    q, kc, vc, kl, gate = make_case(16, 4, 16, 2, lens, seed=33, max_len=32768)
+    qd, kd, vd, ld, gd = q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda()
+    outs = [ops.attn_verify(qd, kd, vd, ld, gd, grid=g).float().cpu() for g in (0, 37, 1024)]
+    for o in outs[1:]:
+        torch.testing.assert_close(o, outs[0], rtol=1e-2, atol=1e-2)
+    pick = [0, 5, 10, 15]
+    ref = oracle(q[pick], kc[pick], vc[pick], kl[pick], gate[pick])
+    torch.testing.assert_close(outs[0][pick], ref, **TOL)

@@ -1,0 +1,182 @@
+"""The end-to-end speculative workload at full size: a seeded random-init dense 8B-class
+qwen3_5 (hidden 4096, 32 layers 3:1 GDN:attention, GDN 16 qk / 32 v heads of 128,
+attention 32 q / 4 kv heads of 256, SwiGLU 12288, vocab 151936) with a 1-layer MTP head,
+B = 16 sequences of 2048-token prompts, k = 3 drafts.
+
+Checked here (the benchmark only times this workload):
+  * one Gated DeltaNet layer and one gated-attention layer of the verify pass, on the
+    prefilled cache (context 2048), against the CPU oracle at the bf16 bar;
+  * graph replay == eager steps, token for token, with temperature 0.7 / top-p 0.95;
+  * rollback == a shorter history: verify 4 tokens, keep a + 1 (a = 0..3 over the
+    batch), then the next token's logits equal those of a cache that only saw the kept
+    tokens;
+  * accepted drafts at this shape: drafts forced to the verify pass's own greedy fixed
+    point are all accepted (the a = k commit, the bonus token, the last snapshot slot).
+"""
+
+import pytest
+import torch
+
+from oracle import qwen3_5_ref as R
+
+pytestmark = pytest.mark.gpu
+B, L, K = 16, 2048, 3
+
+
+@pytest.fixture(scope="module")
+def dense8b():
+    from lollm_amd.qwen3_5 import load, load_mtp
+    from lollm_amd.qwen3_5.config import Qwen3_5Config, dense_8b_config_dict
+    from lollm_amd.qwen3_5.random_init import random_weights
+    print("case C5 build dense 8B", flush=True)
+    raw = dense_8b_config_dict()
+    cfg = Qwen3_5Config.from_hf(raw)
+    W = random_weights(cfg, seed=5, dtype=torch.bfloat16, device="cuda")
+    # the oracle needs only layers 0 (GDN) and 3 (attention)
+    keep = {k: v.float().cpu() for k, v in W.items()
+            if ".layers.0." in k or ".layers.3." in k}
+    model = load(raw, W, "hf", device="cuda")
+    mtp = load_mtp(model, W, "hf", device="cuda")
+    del W
+    g = torch.Generator(device="cuda").manual_seed(5)
+    prompts = torch.randint(0, cfg.vocab_size, (B, L), device="cuda", generator=g)
+    W_ref = {k.replace("model.language_model.", "model."): v for k, v in keep.items()}
+    return model, mtp, W_ref, R.RefConfig.from_dict(raw), prompts
+
+
+def _bf16_bar(got, ref32, ref16, what):
+    got = got.float().cpu()
+    err = (got - ref32).abs().max().item()
+    budget = 2 * (ref16.float() - ref32).abs().max().item() + 1e-3 * ref32.abs().max().item()
+    assert err <= budget, f"{what}: max err {err:.4g} > budget {budget:.4g}"
+
+
+def test_c5_verify_layers_match_oracle(dense8b):
+    model, _, W, cfg, prompts = dense8b
+    print("case C5 layers 0 and 3 vs oracle", flush=True)
+    cache = model.new_cache(B, L + 8, spec_slots=K + 1)
+    model(prompts, cache, logits="last")
+    g = torch.Generator().manual_seed(50)
+    x = torch.randn(B, K + 1, cfg.hidden_size, generator=g).bfloat16()
+    W16 = {k: v.to(torch.bfloat16) for k, v in W.items()}
+    # GDN layer 0: conv window + recurrent state from the prefilled cache
+    conv, rec = cache.linear_state(0)
+    gdn = model.model.layers[0].linear_attn
+    got = gdn.out_proj(gdn.core(x.cuda(), cache, 0))
+    p = "model.layers.0.linear_attn."
+    r32, _, _ = R.gated_deltanet(W, p, cfg, x.float(), conv.float().cpu(), rec.cpu(), True)
+    r16, _, _ = R.gated_deltanet(W16, p, cfg, x, conv.cpu(), rec.cpu(), True)
+    _bf16_bar(got, r32, r16, "GDN layer 0")
+    # attention layer 3: the cache's post-RoPE K / V rows, queries at positions L..L+3
+    st = cache.layers[3]
+    attn = model.model.layers[3].self_attn
+    lengths = cache.lengths.clone()
+    ref_k = st["k"][:, :, :L].float().cpu()
+    ref_v = st["v"][:, :, :L].float().cpu()
+    ws = model.attn_workspace(B, K + 1, cache.max_len)
+    got = attn(x.cuda(), st["k"], st["v"], lengths, lengths + K + 1, workspace=ws)
+    pos = torch.arange(L, L + K + 1)
+    outs = []
+    for Wd, dt in ((W, torch.float32), (W16, torch.bfloat16)):
+        c = R.RefCache(cfg.num_hidden_layers)
+        c.append_kv(3, ref_k.to(dt), ref_v.to(dt))
+        cos, sin = R.rope_tables(pos, cfg.rotary_dim, cfg.rope_theta, dt)
+        outs.append(R.gated_attention(Wd, "model.layers.3.self_attn.", cfg, x.to(dt), cos, sin,
+                                      c, 3))
+    _bf16_bar(got, outs[0], outs[1], "attention layer 3")
+
+
+def test_c5_graph_replay_equals_eager(dense8b):
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    model, mtp, _, cfg, prompts = dense8b
+    print("case C5 graph vs eager", flush=True)
+    toks = []
+    for use_graph in (False, True):
+        dec = SpecDecoder(model, mtp, B, L + 6 * (K + 1) + 8, k=K, temperature=0.7, top_p=0.95,
+                          seed=5, out_capacity=6 * (K + 1) + 4)
+        dec.prefill(prompts)
+        dec.step()
+        if use_graph:
+            dec.capture()
+        for _ in range(4):
+            if use_graph:
+                dec.replay()
+                torch.cuda.synchronize()
+            else:
+                dec.step()
+        toks.append(dec.tokens())
+        del dec
+    assert toks[0] == toks[1]
+    assert all(len(t) == 5 for t in toks[0])       # random weights accept nothing here
+
+
+def test_c5_rollback_equals_shorter_history(dense8b):
+    """Verify 4 tokens, keep a + 1 (a = 0..3 over the batch), then one more token: each
+    sequence's logits must match the history that only ever saw its a + 1 kept tokens.
+    The verify pass (64 GEMM rows) and the shorter forwards (16..48 rows) round
+    differently, which 32 random layers amplify to a few percent of the logit range, so
+    the check is discriminative: every sequence must be much closer to its own history
+    (1 - cosine < 1e-2, against about 0.95 for a wrong history) than to the history of
+    any other accepted length."""
+    model, _, _, cfg, prompts = dense8b
+    print("case C5 rollback", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(51)
+    blk = torch.randint(0, cfg.vocab_size, (B, K + 1), device="cuda", generator=g)
+    nxt = torch.randint(0, cfg.vocab_size, (B, 1), device="cuda", generator=g)
+    acc = (torch.arange(B, device="cuda") % (K + 1)).int()
+    cache = model.new_cache(B, L + 16, spec_slots=K + 1)
+    model(prompts, cache, logits="last")
+    short = cache.clone()
+    model(blk, cache)
+    cache.rollback(acc)
+    got, _ = model(nxt, cache)
+    got = got.float().view(B, -1)
+    hist = []
+    for a in range(K + 1):
+        c = short.clone()
+        model(blk[:, :a + 1], c)
+        lg, _ = model(nxt, c)
+        hist.append(lg.float().view(B, -1))
+        del c
+    cs = torch.nn.functional.cosine_similarity
+    for b in range(B):
+        a = int(acc[b])
+        d = [1 - cs(got[b], h[b], dim=0).item() for h in hist]
+        print(f"b={b} a={a} 1-cos to each history: " + " ".join(f"{x:.2e}" for x in d), flush=True)
+        assert d[a] < 1e-2
+        assert all(d[a] < 0.05 * d[o] for o in range(K + 1) if o != a)
+
+
+def test_c5_accepted_drafts_commit(dense8b):
+    """Accepted drafts at full size (random weights accept nothing on their own): each
+    step's drafts are forced to the verify pass's own greedy fixed point (k rounds of the
+    verify forward, so position i's argmax already follows drafts 1..i), so at
+    temperature 0 all k are accepted -- the a = k commit, the bonus token and the last
+    snapshot slot -- and the emitted tokens are exactly those drafts."""
+    from lollm_amd import ops
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    model, mtp, _, cfg, prompts = dense8b
+    print("case C5 accepted drafts", flush=True)
+    steps = 3
+    n = steps * (K + 1)
+    dec = SpecDecoder(model, mtp, B, L + n + 8, k=K, temperature=0.0, out_capacity=n + 8)
+    dec.prefill(prompts)
+    expect = [[] for _ in range(B)]
+
+    def fixed_point_chain():
+        d = torch.zeros(B, K, dtype=torch.int32, device="cuda")
+        for _ in range(K):
+            ids = torch.cat([dec.pending.view(B, 1), d], 1)
+            _, normed = model.hidden_states(ids, dec.cache)
+            am = ops.sample_rows(model.lm_head(normed).view(B * (K + 1), -1), 0.0)
+            d = am.view(B, K + 1)[:, :K].contiguous()
+        dec.drafts.copy_(d)
+        for b in range(B):
+            expect[b] += [int(dec.pending[b])] + d[b].tolist()
+    dec._draft_chain = fixed_point_chain
+    for _ in range(steps):
+        dec.step()
+    hist = dec.accept_hist.cpu().tolist()
+    print(f"accept histogram {hist}", flush=True)
+    assert hist[K] == steps * B
+    assert dec.tokens() == expect

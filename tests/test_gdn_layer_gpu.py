@@ -204,3 +204,37 @@ def test_gdn_layer_chunked_precision_long(B, T, S, seed):
         assert err <= 5e-5 * scale, f"state err {err:.3g} > 5e-5 x {scale:.3g}"
     assert (oc != orr).float().mean().item() <= 1e-2
     assert (~torch.isclose(oc, orr, rtol=1e-2, atol=1e-2)).float().mean().item() <= 1e-5
+
+
+@pytest.mark.parametrize("B,T,S", [(3, 4, 4), (2, 1, 4)])
+def test_gdn_layer_verify_fresh_call(B, T, S):
+    """fresh = 1 (a cache's first call): the recurrent state starts at zero whatever the
+    committed slot holds (the kernel reads it through an empty buffer descriptor); the
+    committed half is still untouched and the snapshots land in the other half."""
+    from lollm_amd import ops
+    print(f"case gdn_layer fresh B={B} T={T} S={S}", flush=True)
+    proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, W = make(B, T, S, 77 + T)
+    rec = rec + 1.0                                   # non-zero garbage the call must ignore
+    zero = rec.clone()
+    for b in range(B):
+        zero[b, int(rec_slot[b])] = 0
+    ref_o, _ = oracle(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, zero, rec_slot, T)
+    r32_o, ref_s = oracle(proj.float(), conv_w.float(), A_log, dt_bias, norm_w.float(),
+                          win.float(), conv_off, zero, rec_slot, T)
+    rec_d = rec.cuda()
+    out = ops.gdn_layer(proj.cuda(), conv_w.cuda(), A_log.cuda(), dt_bias.cuda(), norm_w.cuda(),
+                        win.cuda(), conv_off.cuda(), rec_d, rec_slot.cuda(), True, B, T, Hk, Hv, D,
+                        K, 1e-6)
+    torch.cuda.synchronize()
+    got = out.cpu().float()
+    err = (got - r32_o).abs().max().item()
+    budget = 2 * (ref_o.float() - r32_o).abs().max().item() + 1e-3 * r32_o.abs().max().item()
+    assert err <= budget, f"max err {err:.4g} > budget {budget:.4g}"
+    rec_o = rec_d.cpu()
+    for b in range(B):
+        slot = int(rec_slot[b])
+        rbase = 0 if slot >= S else S
+        scale = ref_s[b].abs().max().item()
+        torch.testing.assert_close(rec_o[b, rbase:rbase + T], ref_s[b], rtol=2e-2, atol=2e-2 * scale)
+        keep = slice(S - rbase, 2 * S - rbase)
+        assert torch.equal(rec_o[b, keep], rec[b, keep])

@@ -89,21 +89,19 @@ def test_gemm_rejects_bad_shapes_and_workspace():
 
 
 def test_projection_paths_agree():
-    """Projection: every path for <= 64 rows (the timed choice and the forced others:
-    lollm_gemm at two grids, hipBLASLt) and hipBLASLt for more rows all match the
-    oracle."""
-    from lollm_amd.qwen3_5.blocks import Projection, _cus
+    """Projection: lollm_gemm (the fixed path for <= 64 rows), lollm_gemm at the default
+    grid, hipBLASLt, and hipBLASLt for more rows all match the oracle."""
+    from lollm_amd import ops as O
+    from lollm_amd.qwen3_5.blocks import Projection, gemm_path
     x, W = case(80, 256, 512, seed=5)
     p = Projection(W.cuda())
     assert p.tiled is not None
     ref = R.linear(x.float(), W.float())
+    assert gemm_path(256, 512, 0, 64) == "gemm" and gemm_path(256, 512, 0, 80) == "blas"
     close(p(x[:64].cuda()), ref[:64])
-    assert p.choice[64] in ("gemm", "gemm1", "blas")
-    close(p._gemm(x[:64].cuda()), ref[:64])
-    close(p._gemm(x[:64].cuda(), _cus()), ref[:64])
+    close(O.gemm(x[:64].cuda(), p.tiled, p.N, p.K), ref[:64])
     close(p._blas(x[:64].cuda()), ref[:64])
     close(p(x.cuda()), ref)
-
 
 
 @pytest.mark.parametrize("M,N,K,grid", [(64, 4096, 4096, 0), (16, 4096, 12288, 0), (5, 512, 128, 4),

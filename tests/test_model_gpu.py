@@ -14,7 +14,7 @@ decoding, where ties are the only legitimate source of disagreement.
 import pytest
 import torch
 
-from lollm_amd.qwen3_5.config import Qwen3_5Config, micro_config_dict, tiny_config_dict
+from lollm_amd.qwen3_5.config import Qwen3_5Config, micro_config_dict
 from lollm_amd.qwen3_5.random_init import random_weights
 from oracle import qwen3_5_ref as R
 
@@ -120,22 +120,33 @@ def test_mtp_forward_and_chain(micro):
     assert bool(((lg.float().argmax(-1) == got) | tie).all())
 
 
-def _check_greedy_trajectory(model, prompts, toks, margin=0.05):
-    """Every emitted token must be the argmax of the model's own logits given the
-    emitted prefix (teacher forcing), except where the top-2 gap is within `margin`."""
-    full = torch.cat([prompts, toks], 1)
-    lg, _ = model(full.cuda(), model.new_cache(full.shape[0], full.shape[1] + 4))
-    lg = lg.float().cpu()[:, prompts.shape[1] - 1:-1]
-    top2 = lg.topk(2, -1).values
-    am = lg.argmax(-1)
-    bad = (am != toks) & ((top2[..., 0] - top2[..., 1]) > margin)
-    assert not bad.any(), f"{int(bad.sum())} non-tie disagreements"
+def _oracle_trajectory(W, W16, cfg, prompt, n):
+    """The oracle's greedy tokens (generate.py:40-62, fp32) and, along them, its top-16
+    logits and the bf16 oracle's largest logit deviation (the near-tie tolerance)."""
+    toks = R.generate_greedy(W, cfg, prompt, n)
+    full = torch.tensor([prompt + toks])
+    lg = R.model_forward(W, cfg, full)[0][0, len(prompt) - 1:-1].float()
+    lg16 = R.model_forward(W16, cfg, full)[0][0, len(prompt) - 1:-1].float()
+    v, i = lg.topk(16, -1)
+    return toks, i, v, (lg16 - lg).abs().max().item()
+
+
+def _agreed_prefix(got, want, top_idx, top_vals, tol):
+    for i, (a, b) in enumerate(zip(got, want)):
+        if a != b:
+            idx = top_idx[i].tolist()
+            assert a in idx and float(top_vals[i, 0] - top_vals[i, idx.index(a)]) <= tol, \
+                f"step {i}: token {a} is not a near-tie of the oracle's {b}"
+            return i
+    return len(want)
 
 
 @pytest.mark.parametrize("k", [1, 3])
-def test_greedy_spec_decode_is_greedy(micro, k):
-    model, mtp, _, cfg = micro
-    from lollm_amd.generate import greedy_tokens
+def test_greedy_spec_decode_matches_oracle(micro, k):
+    """Greedy speculative decoding (B = 4, k drafts) emits the oracle's greedy
+    autoregressive tokens (mtp.py:101-103); a difference is allowed only at a near-tie of
+    the oracle's own logits, where the comparison stops."""
+    model, mtp, (W, W16), cfg = micro
     from lollm_amd.qwen3_5.mtp import SpecDecoder
     print(f"case greedy spec k={k}", flush=True)
     g = torch.Generator().manual_seed(5)
@@ -145,21 +156,26 @@ def test_greedy_spec_decode_is_greedy(micro, k):
     dec.prefill(prompts.cuda())
     while int(dec.out_count.min()) < n:
         dec.step()
-    spec = torch.tensor([t[:n] for t in dec.tokens()])
-    ar = greedy_tokens(model, prompts, n)
-    agree = (spec == ar).float().mean().item()
-    _check_greedy_trajectory(model, prompts, spec)
-    assert agree > 0.9, f"spec vs AR agreement {agree:.3f}"
+    got = dec.tokens()
+    agreed = 0
+    for b in range(4):
+        want, ti, tv, dev = _oracle_trajectory(W, W16, cfg, prompts[b].tolist(), n)
+        agreed += _agreed_prefix(got[b][:n], want, ti, tv, 2 * dev)
+    print(f"agreed {agreed} of {4 * n} steps", flush=True)
+    assert agreed >= 2 * n              # near-ties are rare on this model
 
 
-def test_graph_replay_matches_eager(micro):
+@pytest.mark.parametrize("pen,draft", [(1.0, "argmax"), (1.05, "argmax"), (1.3, "sample")])
+def test_graph_replay_matches_eager(micro, pen, draft):
     model, mtp, _, cfg = micro
     from lollm_amd.qwen3_5.mtp import SpecDecoder
+    print(f"case graph replay pen={pen} draft={draft}", flush=True)
     g = torch.Generator().manual_seed(6)
     prompts = torch.randint(0, cfg.vocab_size, (3, 10), generator=g)
     outs = []
     for use_graph in (False, True):
-        dec = SpecDecoder(model, mtp, 3, 80, k=3, temperature=0.7, top_p=0.95, seed=9)
+        dec = SpecDecoder(model, mtp, 3, 80, k=3, temperature=0.7, top_p=0.95, seed=9,
+                          repetition_penalty=pen, draft=draft)
         dec.prefill(prompts.cuda())
         dec.step()
         if use_graph:
@@ -173,22 +189,3 @@ def test_graph_replay_matches_eager(micro):
                 dec.step()
         outs.append(dec.tokens())
     assert outs[0] == outs[1]
-
-
-def test_tiny_config_greedy_spec_k1():
-    """The tiny CPU-runnable config (hidden 1024, 8 layers): 64 greedy tokens from a
-    128-token prompt with k = 1, checked as a greedy trajectory of the model."""
-    from lollm_amd.qwen3_5.mtp import SpecDecoder
-    model, mtp, (W, W16), cfg = build(tiny_config_dict(), seed=0)
-    g = torch.Generator().manual_seed(1)
-    prompts = torch.randint(0, cfg.vocab_size, (1, 128), generator=g)
-    dec = SpecDecoder(model, mtp, 1, 128 + 64 + 8, k=1, temperature=0.0)
-    dec.prefill(prompts.cuda())
-    while int(dec.out_count.min()) < 64:
-        dec.step()
-    toks = torch.tensor([dec.tokens()[0][:64]])
-    _check_greedy_trajectory(model, prompts, toks)
-    lg, _ = model(prompts.cuda(), model.new_cache(1, 140), logits="last")
-    ref, _ = R.model_forward(W, cfg, prompts)
-    r16, _ = R.model_forward(W16, cfg, prompts)
-    close_logits(lg[0, -1], ref[0, -1], r16[0, -1])
