@@ -118,6 +118,20 @@ int lollm_spec_accept(const void* target, const void* draft, const int32_t* draf
                       int32_t* next_token, void* workspace, long long workspace_bytes,
                       void* stream);
 
+/* lollm_spec_accept with no workspace argument and no device allocation, for callers that
+ * cannot allocate: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  No counterpart in the reference.  The workspace is a fixed array inside the
+ * library, LOLLM_SPEC_SCRATCH_BYTES on each device it runs on, held until the process
+ * ends; a shape whose lollm_spec_workspace_bytes exceeds it returns LOLLM_EUNSUPPORTED
+ * (1 MiB covers, e.g., B = 256 with k = 8 and sampled drafts).  Every call on one device
+ * uses that device's array: calls that overlap in time on one device race.  Same
+ * arguments, results and errors as lollm_spec_accept otherwise. */
+#define LOLLM_SPEC_SCRATCH_BYTES (1 << 20)
+int lollm_spec_accept_noalloc(const void* target, const void* draft, const int32_t* drafts, int B,
+                              int k, int V, float inv_temperature, int top_k, float top_p,
+                              uint64_t seed, uint64_t offset, const uint64_t* offset_dev,
+                              int32_t* n_accepted, int32_t* next_token, void* stream);
+
 /* One draw per row from its temperature / top-k / top-p distribution (the
  * multinomial of src/generate.py:37 on explicit uniforms); greedy rows return the
  * first argmax (generate.py:24).  Row r uses Philox row row_base + r and `slot`.

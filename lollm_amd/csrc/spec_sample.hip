@@ -48,6 +48,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace lollm {
 
@@ -1055,6 +1056,49 @@ LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int
                      (const uint16_t*)draft, drafts, k, V, inv_temperature, seed, offset, offset_dev,
                      st_t, draft ? st_d : nullptr, ns, (const u128*)apart, n_accepted, next_token);
   return launch_status();
+}
+
+// ---------------------------------------------------------------- allocation-free
+// lollm_spec_accept for callers that cannot allocate: its workspace (row statistics and
+// draw partials, every byte written before it is read, so nothing needs clearing) lives
+// in this fixed per-device array.  The host never uses the array's name as an address:
+// each device's copy is located once with hipGetSymbolAddress, with that device current.
+static __device__ __attribute__((aligned(256))) unsigned char scratch[LOLLM_SPEC_SCRATCH_BYTES];
+
+static void* g_scratch_ptr[64];
+static std::mutex g_scratch_mu;
+
+static int scratch_for_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return LOLLM_EHIP_BASE + (int)e;
+  if (dev < 0 || dev >= 64) return LOLLM_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return LOLLM_EHIP_BASE + (int)e;
+    if (!p) return LOLLM_EHIP_BASE + (int)hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LOLLM_OK;
+}
+
+LOLLM_API int lollm_spec_accept_noalloc(const void* target, const void* draft,
+                                        const int32_t* drafts, int B, int k, int V,
+                                        float inv_temperature, int top_k, float top_p,
+                                        uint64_t seed, uint64_t offset, const uint64_t* offset_dev,
+                                        int32_t* n_accepted, int32_t* next_token, void* stream) {
+  const long long need = lollm_spec_workspace_bytes(B, k, draft != nullptr);
+  if (need < 0) return LOLLM_EINVAL;
+  if (need > (long long)LOLLM_SPEC_SCRATCH_BYTES) return LOLLM_EUNSUPPORTED;
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  return lollm_spec_accept(target, draft, drafts, B, k, V, inv_temperature, top_k, top_p, seed,
+                           offset, offset_dev, n_accepted, next_token, ws,
+                           (long long)LOLLM_SPEC_SCRATCH_BYTES, stream);
 }
 
 LOLLM_API int lollm_sample_rows(const void* logits, int rows, int V, float inv_temperature,
