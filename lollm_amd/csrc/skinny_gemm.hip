@@ -9,26 +9,22 @@
 // Weight layout (tiled once at load by lollm_gemm_tile_weights): 1 KB blocks in the
 // order the 16x16x32 bf16 MFMA consumes them.  Block (t, s) -- n-tile t (16 rows),
 // k-step s (32 k) -- sits at element offset (t * K / 32 + s) * 512, and lane L = 16 g + r
-// of the block holds row 16 t + r, k = 32 s + 8 g .. + 8.  A wave's load of one block
-// is one coalesced 1 KB read straight into the MFMA A operand: no LDS for weights.
-// The SwiGLU layout interleaves gate and up rows 8 by 8 (tile t = gate rows 8t..8t+7,
-// then up rows 8t..8t+7) so a lane and its partner 32 lanes away hold gate and up of
-// the same output columns.
+// of the block holds row 16 t + r, k = 32 s + 8 g .. + 8, so a block is one coalesced
+// 1 KB read that lands exactly as a wave's MFMA A operand.  The SwiGLU layout interleaves
+// gate and up rows 8 by 8 (tile t = gate rows 8t..8t+7, then up rows 8t..8t+7) so a lane
+// and its partner 32 lanes away hold gate and up of the same output columns.
 //
-// Work decomposition: a group = 64 output columns (4 n-tiles, one per wave), a unit =
-// (group, 128-k stage).  Units are laid end to end group-major and dealt out in equal
-// contiguous ranges to a fixed grid (two workgroups per CU), so every workgroup streams
-// the same number of weight bytes whatever N is (N / 64 groups over 256 CUs would run
-// uneven rounds).  The activation tile of each stage (M x 128) is staged in LDS and
-// shared by the 4 waves, two stages per workgroup barrier (four LDS slots: a barrier
-// makes every wave wait for its oldest loads, so halving the barriers measured 2-6%
-// faster at M = 64); weight loads run 4 units ahead in a register ring, activation
-// loads 2 units ahead (for at most 32 rows gemm_ksplit_kernel splits each unit's k over
-// the waves instead, see there).  A group one workgroup covers whole is stored directly (with
-// the epilogue); a group cut between workgroups leaves an fp32 piece in slot
-// w + group: in accumulator order (each wave's store one contiguous 1 KB) when
-// gemm_fixup_kernel merges it with one float4 per thread over a (group, m-tile) grid,
-// row major when gemm_norm_kernel merges it row by row.  (Merging
+// Work decomposition: a group = 64 output columns (4 n-tiles), a unit = (group, 128-k
+// stage).  Units are laid end to end group-major and dealt out in equal contiguous ranges
+// to a fixed grid (one workgroup per CU), so every workgroup streams the same number of
+// weight bytes whatever N is (N / 64 groups over 256 CUs would run uneven rounds).  Two
+// kernels: gemm_ksplit_kernel for at most 32 rows (operands straight to registers, each
+// wave one k-step of every unit), gemm_stream_kernel for 33..64 rows (warp-specialised:
+// DMA loader waves stream weights and activations into LDS rings, MFMA waves consume
+// them; see each).  A group one workgroup covers whole is stored directly (with the
+// epilogue); a group cut between workgroups leaves an fp32 piece in slot w + group: in
+// accumulator order when gemm_fixup_kernel merges it with one float4 per thread over a
+// (group, m-tile) grid, row major when gemm_norm_kernel merges it row by row.  (Merging
 // in the last-arriving workgroup instead would need device-scope release / acquire
 // fences, which write back and invalidate the XCD's L2 -- measured 3-10x slower here
 // than the second launch.)
@@ -168,108 +164,182 @@ __device__ __forceinline__ void gm_emit(const GemmArgs& a, const gm_f32x4 (&v)[M
   }
 }
 
-template <int MT>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
-  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-  constexpr int CPR = GM_KC / 8;                          // 16 B chunks per activation row
-  constexpr int ACH = (MT * 16 * CPR + 255) / 256;        // activation chunks per thread
-  // every thread stages exactly ACH chunks, so the staging needs no row test: such a
-  // test (always true) made the compiler wait for all staging loads at once instead of
-  // each one in turn, which measured 5-11% slower at 48-64 rows
-  static_assert(ACH * 256 == MT * 16 * CPR, "the staging covers the tile exactly");
-  // activation stages of units ub + j in slot j & 3, written two at a time
-  __shared__ __attribute__((aligned(16))) unsigned char al[4][MT * 16 * GM_PITCH];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// The product for 33..64 rows, warp-specialised.  Waves 4 and 5 only stream weights:
+// each copies its half of a unit's 16 weight blocks (2 n-tiles x 4 k-steps, 1 KB each)
+// straight into LDS with 16-byte DMA loads (global_load_lds_dwordx4, non-temporal) into a
+// ring of GS_WSLOTS slots, GS_WSLOTS - 1 units ahead; wave 6 copies the unit's 64-row
+// activation tile (128 k) the same way into a ring of GS_ASLOTS slots.  Only these
+// three waves wait on vmcnt, each for its own oldest unit with a fixed count, so the
+// weight stream never waits for anything else (in the register-ring kernel every wait
+// for an activation or a weight also waited for all older loads, in issue order, and
+// the compiler added full drains at the loop head).  Waves 0-3 read both MFMA operands
+// from LDS in a 2 x 2 arrangement -- wave (wn, wm) owns n-tiles 2 wn, 2 wn + 1 and m-tiles
+// 2 wm, 2 wm + 1 of the group -- accumulating each tile over the unit's k-steps in order,
+// as the register-ring kernel it replaced did, so results and pieces kept their bits.  One barrier per unit: past it the unit has
+// landed and every consumer has finished the previous unit, whose slots the loaders
+// refill.  Activation rows sit in LDS without padding, the 16-byte chunk c of row r at
+// chunk position c ^ (r & 15) (the DMA writes a wave's 1 KB contiguously, so the loaders
+// pick each lane's source chunk to produce that layout; the consumers' 16 rows of one
+// chunk then hit 16 different bank groups).  Rows past M re-read the last row.  Past
+// the range's end the loaders refetch its last unit into the free slot, so their wait
+// counts stay exact.  Measured 3-8% faster at 64 rows than that register-ring kernel
+// (weights and activations in a 4-unit register ring, activations staged into LDS by
+// the MFMA waves) on every projection shape of the 8B-class verify pass.
+typedef __attribute__((address_space(1))) void gs_global_t;
+typedef __attribute__((address_space(3))) void gs_lds_t;
+constexpr int GS_WSLOTS = 5;
+constexpr int GS_ASLOTS = 3;
+constexpr int GS_SLOT = 16384;
+constexpr int GS_THREADS = 448;
+constexpr int GS_NT = 2;                    // cache policy of the weight DMA: non-temporal
+
+__device__ __forceinline__ void gs_emit_tile(const GemmArgs& a, const gm_f32x4& v, int i, int j,
+                                             int g, bool whole, int w, int lane) {
   const int l16 = lane & 15, g4 = lane >> 4;
+  const int m = 16 * i + l16;
+  if (whole) {
+    if (a.epi == GM_EPI_ARGMAX) {
+      const int col = GM_COLS * g + 16 * j + 4 * g4;
+      uint64_t best = gm_key(v[0], col);
+#pragma unroll
+      for (int e = 1; e < 4; ++e) {
+        const uint64_t k2 = gm_key(v[e], col + e);
+        best = k2 > best ? k2 : best;
+      }
+      best = gm_max_xor(best, 16);
+      best = gm_max_xor(best, 32);
+      if (g4 == 0 && m < a.M) a.am[(size_t)m * (a.N / 16) + 4 * g + j] = best;
+    } else if (a.epi == GM_EPI_SWIGLU) {
+      float other[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) other[e] = __shfl_xor(v[e], 32, 64);
+      if (g4 < 2 && m < a.M) {
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = round_bf16(gm_silu_bf16(v[e]) * round_bf16(other[e]));
+        const int col = 8 * (4 * g + j) + 4 * g4;
+        *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+            make_uint2((uint32_t)f32_to_bf16(y[0]) | ((uint32_t)f32_to_bf16(y[1]) << 16),
+                       (uint32_t)f32_to_bf16(y[2]) | ((uint32_t)f32_to_bf16(y[3]) << 16));
+      }
+    } else if (m < a.M) {
+      const int col = GM_COLS * g + 16 * j + 4 * g4;
+      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+          make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                     (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+    }
+  } else {
+    // the piece of a cut group in the layout the merge kernels read: (16 mt) x 64 fp32
+    // with mt = ceil(M / 16) m-tiles, so an m-tile made only of padding rows is skipped
+    const int mt = (a.M + 15) / 16;
+    if (i >= mt) return;
+    float* pp = a.part + ((size_t)w + g) * ((size_t)mt * 16 * GM_COLS);
+    const size_t off = a.rowmajor ? (size_t)m * GM_COLS + 16 * j + 4 * g4
+                                  : (((size_t)i * 4 + j) * 64 + lane) * 4;
+    *reinterpret_cast<float4*>(pp + off) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+__global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[(GS_WSLOTS + GS_ASLOTS) * GS_SLOT];
+  unsigned char* wring = lds;
+  unsigned char* aring = lds + GS_WSLOTS * GS_SLOT;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int w = blockIdx.x;
   const int u0 = gm_begin(a.U, w, a.nw), u1 = gm_begin(a.U, w + 1, a.nw);
-  if (u0 >= u1) return;
+  if (u0 >= u1) return;                      // the whole workgroup: no barrier is left waiting
   const int kt = a.K / 32;
-  const uint16_t* wlane = a.Wt + (size_t)wave * kt * 512 + lane * 8;
-
-  v4u wr[GM_P][GM_KS], an[2][ACH];
-  // weights of unit u for this wave: n-tile 4 g + wave, k-steps 4 st .. 4 st + 3
-  auto wload = [&](v4u* dst, int u) {
-    const int g = u / a.SK, st = u - g * a.SK;
-    const uint16_t* p = wlane + ((size_t)4 * g * kt + (size_t)st * GM_KS) * 512;
+  if (wave == 4 || wave == 5) {
+    const int lw = wave - 4;
+    auto issue = [&](int u) {
+      const int uu = u < u1 ? u : u1 - 1;
+      const int g = uu / a.SK, st = uu - g * a.SK;
+      unsigned char* sb = wring + ((u - u0) % GS_WSLOTS) * GS_SLOT;
 #pragma unroll
-    for (int q = 0; q < GM_KS; ++q)
-      dst[q] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p + q * 512));
-  };
-  auto aload = [&](v4u* dst, int u) {
-    const int k0 = (u % a.SK) * GM_KC;
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * lw + jj;
+        const uint16_t* src = a.Wt + ((size_t)(4 * g + j) * kt + (size_t)st * GM_KS) * 512 + lane * 8;
 #pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = i * 256 + tid, row = c / CPR, col = c % CPR;
-      const int rr = row < a.M ? row : a.M - 1;
-      dst[i] = *reinterpret_cast<const v4u*>(a.A + (size_t)rr * a.lda + k0 + col * 8);
+        for (int q = 0; q < GM_KS; ++q)
+          __builtin_amdgcn_global_load_lds((gs_global_t*)(src + q * 512),
+                                           (gs_lds_t*)(sb + (j * GM_KS + q) * 1024), 16, 0, GS_NT);
+      }
+    };
+#pragma unroll
+    for (int p = 0; p < GS_WSLOTS - 1; ++p) issue(u0 + p);
+    for (int u = u0; u < u1; ++u) {
+      // unit u has landed once at most GS_WSLOTS - 2 younger units (8 DMAs each) remain
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"((GS_WSLOTS - 2) * 8) : "memory");
+      issue(u + GS_WSLOTS - 1);
     }
-  };
-
-  gm_f32x4 acc[MT];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+  if (wave == 6) {
+    auto issue = [&](int u) {
+      const int uu = u < u1 ? u : u1 - 1;
+      const int k0 = (uu % a.SK) * GM_KC;
+      unsigned char* sb = aring + ((u - u0) % GS_ASLOTS) * GS_SLOT;
 #pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
-  // Every load is issued unconditionally (units past the range re-read the last one),
-  // so the compiler can count the loads in flight exactly and each staging waits only
-  // for its own unit, never for the ring ahead of it.
-  const int ulast = u1 - 1;
+      for (int d = 0; d < 16; ++d) {
+        const int r = 4 * d + (lane >> 4), p = lane & 15, c = p ^ (r & 15);
+        const int rr = r < a.M ? r : a.M - 1;
+        __builtin_amdgcn_global_load_lds((gs_global_t*)(a.A + (size_t)rr * a.lda + k0 + c * 8),
+                                         (gs_lds_t*)(sb + d * 1024), 16, 0, 0);
+      }
+    };
 #pragma unroll
-  for (int p = 0; p < GM_P; ++p) wload(wr[p], u0 + p < u1 ? u0 + p : ulast);
-  aload(an[0], u0);
-  aload(an[1], u0 + 1 < u1 ? u0 + 1 : ulast);
+    for (int p = 0; p < GS_ASLOTS - 1; ++p) issue(u0 + p);
+    for (int u = u0; u < u1; ++u) {
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"((GS_ASLOTS - 2) * 16) : "memory");
+      issue(u + GS_ASLOTS - 1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+  const int wn = wave & 1, wm = wave >> 1, l16 = lane & 15, g4 = lane >> 4;
+  gm_f32x4 acc[2][2];
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) acc[ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
   bool whole_from_start = (u0 % a.SK) == 0;
-
-  auto finish = [&](int g, bool whole) {
-    gm_emit<MT>(a, acc, g, whole, w, wave, lane);
+  for (int u = u0; u < u1; ++u) {
+    // this wave's reads of the previous unit are complete before the loaders may refill it
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const unsigned char* wb = wring + ((u - u0) % GS_WSLOTS) * GS_SLOT;
+    const unsigned char* ab = aring + ((u - u0) % GS_ASLOTS) * GS_SLOT;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) acc[i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
-  };
-
-  // One unit: stage activations, 4 k-steps of MFMA, refill the rings; at a group's
-  // last unit (or the range's end) write the group's result or piece.
-#define GM_UNIT(J)                                                                            \
-  {                                                                                           \
-    const int u = ub + (J);                                                                   \
-    const bool livej = u < u1;                                                                \
-    constexpr int slot = (J) % GM_P;                                                          \
-    if ((J) % 2 == 0) {                                                                       \
-      /* stage units u and u + 1 (slots J, J + 1) behind one barrier, then load the     */    \
-      /* next pair; the previous writer of these slots was two units before the last    */    \
-      /* barrier, which every wave has passed                                            */    \
-      _Pragma("unroll") for (int h = 0; h < 2; ++h)                                           \
-      _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                       \
-        const int c = i * 256 + tid, row = c / CPR, col = c % CPR;                            \
-        *reinterpret_cast<v4u*>(&al[(J) + h][row * GM_PITCH + col * 16]) = an[h][i]; \
-      }                                                                                       \
-      gm_lds_barrier();                                                                       \
-      aload(an[0], u + 2 < u1 ? u + 2 : ulast);                                               \
-      aload(an[1], u + 3 < u1 ? u + 3 : ulast);                                               \
-    }                                                                                         \
-    if (livej) {                                                                              \
-      _Pragma("unroll") for (int q = 0; q < GM_KS; ++q) {                                     \
-        _Pragma("unroll") for (int i = 0; i < MT; ++i) {                                      \
-          const gm_bf16x8 ab = *reinterpret_cast<const gm_bf16x8*>(                           \
-              &al[(J)][(16 * i + l16) * GM_PITCH + q * 64 + g4 * 16]);                        \
-          acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                                   \
-              __builtin_bit_cast(gm_bf16x8, wr[slot][q]), ab, acc[i], 0, 0, 0);               \
-        }                                                                                     \
-      }                                                                                       \
-    }                                                                                         \
-    wload(wr[slot], u + GM_P < u1 ? u + GM_P : ulast);                                        \
-    if (livej) {                                                                              \
-      const int st = u % a.SK;                                                                \
-      if (st == a.SK - 1 || u == ulast) {                                                     \
-        finish(u / a.SK, whole_from_start && st == a.SK - 1);                                 \
-        whole_from_start = true;                                                              \
-      }                                                                                       \
-    }                                                                                         \
+    for (int q = 0; q < GM_KS; ++q) {
+      gm_bf16x8 wf[2], af[2];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+        wf[jj] = *reinterpret_cast<const gm_bf16x8*>(wb + ((2 * wn + jj) * GM_KS + q) * 1024 + lane * 16);
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const int row = 16 * (2 * wm + ii) + l16, c = q * 4 + g4;
+        af[ii] = *reinterpret_cast<const gm_bf16x8*>(ab + row * 256 + ((c ^ (row & 15)) * 16));
+      }
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          acc[ii][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[jj], af[ii], acc[ii][jj], 0, 0, 0);
+    }
+    const int st = u % a.SK;
+    if (st == a.SK - 1 || u == u1 - 1) {
+      const int g = u / a.SK;
+      const bool whole = whole_from_start && st == a.SK - 1;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          gs_emit_tile(a, acc[ii][jj], 2 * wm + ii, 2 * wn + jj, g, whole, w, lane);
+          acc[ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      whole_from_start = true;
+    }
   }
-
-  static_assert(GM_P == 4, "the unit loop is unrolled by 4");
-  for (int ub = u0; ub < u1; ub += 4) {
-    GM_UNIT(0) GM_UNIT(1) GM_UNIT(2) GM_UNIT(3)
-  }
-#undef GM_UNIT
 }
 
 
@@ -647,8 +717,9 @@ static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, 
   switch ((M + 15) / 16) {
     case 1: hipLaunchKernelGGL(gemm_ksplit_kernel<1>, dim3(nw), dim3(256), 0, st, a); break;
     case 2: hipLaunchKernelGGL(gemm_ksplit_kernel<2>, dim3(nw), dim3(256), 0, st, a); break;
-    case 3: hipLaunchKernelGGL(gemm_kernel<3>, dim3(nw), dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL(gemm_kernel<4>, dim3(nw), dim3(256), 0, st, a); break;
+    default:   // 33..64 rows: the warp-specialised stream (64-row tiles, rows past M clamped)
+      hipLaunchKernelGGL(gemm_stream_kernel, dim3(nw), dim3(GS_THREADS), 0, st, a);
+      break;
   }
   return launch_status();
 }

@@ -30,7 +30,6 @@ def _cat_rows(*ws):
 #   (N, K, epilogue, rows) -> "blas"
 BLAS_SHAPES = {
     (12352, 4096, 0, 64),      # GDN in_proj of the 4096-hidden model, verify pass
-    (151936, 4096, 0, 64),     # lm_head of the 151936-vocabulary model, verify pass
 }
 
 
