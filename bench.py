@@ -198,7 +198,7 @@ def gdn_layer_roofline(model, dec, iters=50):
 # ------------------------------------------------------------------------------------
 # isolated kernel workloads
 # ------------------------------------------------------------------------------------
-def isolated_gdn(B, kd):
+def isolated_gdn(B, kd, cpu=False):
     import torch
     from lollm_amd import ops
     Hk, Hv, D, T = 16, 32, 128, 1 + kd
@@ -214,8 +214,18 @@ def isolated_gdn(B, kd):
     snaps = torch.empty(B, T, Hv, D, D, device="cuda")
     us = time_fn(lambda: ops.gdn_verify(q, k, v, gg, beta, s0, out=out, snap_out=snaps), 50)
     byt = B * Hv * (1 + T) * D * D * 4 + B * T * (2 * Hk * D * 2 + 2 * Hv * D * 2 + Hv * 6)
-    return {"B": B, "T": T, "us": round(us, 2), "MB": round(byt / 1e6, 1),
-            "GBs": round(byt / us / 1e3, 1), "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
+    row = {"B": B, "T": T, "us": round(us, 2), "MB": round(byt / 1e6, 1),
+           "GBs": round(byt / us / 1e3, 1), "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
+    if cpu:
+        # the reference's T > 1 path: repeat_interleave to the v-heads, then the chunked
+        # delta rule (blocks.py:309-322), bf16 inputs computed as the reference does
+        from oracle import qwen3_5_ref as R
+        qc, kc, vc = (t.cpu() for t in (q, k, v))
+        gc, bc, sc = gg.cpu(), beta.cpu(), s0.cpu()
+        rep = Hv // Hk
+        row["_cpu"] = lambda: time_cpu(lambda: R.gdn_scan_chunked(
+            qc.repeat_interleave(rep, 2), kc.repeat_interleave(rep, 2), vc, gc, bc, state=sc))
+    return row
 
 
 PEAK_FP32_MFMA_TFLOPS = 157.3
@@ -268,7 +278,7 @@ def isolated_gdn_prefill(B=16, T=2048):
             "peak": PEAK_BF16_MFMA_TFLOPS, "frac": round(mf / PEAK_BF16_MFMA_TFLOPS, 3)}
 
 
-def isolated_attn():
+def isolated_attn(cpu=False):
     import torch
     from lollm_amd import ops
     g = torch.Generator().manual_seed(3)
@@ -283,13 +293,31 @@ def isolated_attn():
     out = torch.empty(B, T, Hq * D, dtype=torch.bfloat16, device="cuda")
     us = time_fn(lambda: ops.attn_verify(q, kc, vc, kl, gate, workspace=ws, out=out), 20)
     byt = int(lens.sum()) * Hkv * D * 2 * 2 + 3 * B * T * Hq * D * 2
+    row = {"B": B, "T": T, "sum_ctx": int(lens.sum()), "us": round(us, 2),
+           "MB": round(byt / 1e6, 1), "GBs": round(byt / us / 1e3, 1),
+           "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
+    if cpu:
+        # one sequence at a time, as the reference's cache holds one length:
+        # repeat_kv (blocks.py:152-156), SDPA with the offset-causal bool mask
+        # (attention.py:43-51), sigmoid gate (blocks.py:235); bf16
+        from oracle import qwen3_5_ref as R
+        qc, gc = q.cpu(), gate.cpu()
+        ks = [kc[b, :, :int(lens[b])].cpu() for b in range(B)]
+        vs = [vc[b, :, :int(lens[b])].cpu() for b in range(B)]
+
+        def ref():
+            for b in range(B):
+                qq = qc[b].transpose(0, 1)[None]                          # (1, Hq, T, D)
+                kk = R.repeat_kv(ks[b][None], Hq // Hkv)
+                vv = R.repeat_kv(vs[b][None], Hq // Hkv)
+                o = R.sdpa_offset_causal(qq, kk, vv).transpose(1, 2).reshape(T, Hq * D)
+                o * torch.sigmoid(gc[b])
+        row["_cpu"] = lambda: time_cpu(ref)
     del kc, vc
-    return {"B": B, "T": T, "sum_ctx": int(lens.sum()), "us": round(us, 2),
-            "MB": round(byt / 1e6, 1), "GBs": round(byt / us / 1e3, 1),
-            "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
+    return row
 
 
-def isolated_sampler():
+def isolated_sampler(cpu=False):
     import torch
     from lollm_amd import ops
     g = torch.Generator(device="cuda")
@@ -306,13 +334,101 @@ def isolated_sampler():
     us = time_fn(lambda: ops.spec_accept(tgt, drf, drafts, 0.7, 0, 0.95, 7, 0, workspace=ws,
                                          n_accepted=na, next_token=nt), 20)
     byt = B * (2 * k + 1) * V * 2
-    return {"B": B, "k": k, "V": V, "us": round(us, 2), "MB": round(byt / 1e6, 1),
-            "GBs": round(byt / us / 1e3, 1), "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
+    row = {"B": B, "k": k, "V": V, "us": round(us, 2), "MB": round(byt / 1e6, 1),
+           "GBs": round(byt / us / 1e3, 1), "frac": round(byt / us / 1e3 / PEAK_HBM_GBS, 3)}
+    if cpu:
+        # the reference's sampler arithmetic (generate.py:23-36: sort, softmax, cumsum)
+        # with the rejection rule, on the same logits and Philox uniforms
+        from oracle import qwen3_5_ref as R
+        from oracle import sampler_ref as S
+        tc, dc, dr = tgt.float().cpu(), drf.float().cpu(), drafts.long().cpu()
+        U = torch.tensor([[S.uniform_u24(7, 0, b, i) for i in range(k + 1)] for b in range(B)],
+                         dtype=torch.float64) / 2 ** 24
+        row["_cpu"] = lambda: time_cpu(lambda: R.spec_accept_sorted(tc, dr, 0.7, 0, 0.95, U, draft=dc))
+    return row
 
 
 # ------------------------------------------------------------------------------------
 # CPU baseline: the oracle (torch-on-CPU restatement of the reference path)
 # ------------------------------------------------------------------------------------
+def time_cpu(fn, warm=3, reps=20, budget_s=30.0):
+    """Median ms of fn() on the host: `warm` untimed runs, then up to `reps` timed runs
+    within about budget_s seconds (at least 3).  Returns (median ms, runs)."""
+    for _ in range(warm):
+        fn()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < reps and (len(ts) < 3 or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return sorted(ts)[len(ts) // 2], len(ts)
+
+
+def cpu_info():
+    import torch
+    model_name = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model_name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model_name, "os_cpu_count": os.cpu_count(),
+            "torch_threads": torch.get_num_threads()}
+
+
+def tiny_e2e(n_new=64):
+    """The tiny CPU-runnable config: hidden 1024, 8 layers, vocab 32768, 1 MTP layer,
+    seeded weights; B = 1, a 128-token prompt (seed 1), 64 greedy tokens with k = 1,
+    prefill included.  GPU: SpecDecoder on the kernels (bf16, eager steps).  CPU: the
+    oracle's generate_mtp loop in fp32 (mtp.py:92-162 with the reference's chunked GDN,
+    masked SDPA and deep-copy rollback)."""
+    import torch
+    from lollm_amd.qwen3_5 import load, load_mtp
+    from lollm_amd.qwen3_5.config import Qwen3_5Config, tiny_config_dict
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    from lollm_amd.qwen3_5.random_init import random_weights
+    from oracle import qwen3_5_ref as R
+    raw = tiny_config_dict()
+    cfg = Qwen3_5Config.from_hf(raw)
+    W = random_weights(cfg, seed=0)
+    Wb = {n: t.to(torch.bfloat16) for n, t in W.items()}
+    prompt = torch.randint(0, cfg.vocab_size, (128,), generator=torch.Generator().manual_seed(1))
+    weights = dict(Wb)
+    model = load(raw, weights, "hf", device="cuda")
+    mtp = load_mtp(model, weights, "hf", device="cuda")
+
+    def gpu_run():
+        dec = SpecDecoder(model, mtp, 1, 128 + n_new + 8, k=1, temperature=0.0, out_capacity=n_new + 4)
+        dec.prefill(prompt.view(1, -1).cuda())
+        while True:
+            for _ in range(8):
+                dec.step()
+            if int(dec.out_count[0]) >= n_new:
+                return
+    gpu_run()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        gpu_run()
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    g_s = sorted(ts)[2]
+    Wr = R.canonical_weights({n: t.float() for n, t in Wb.items()})
+    rcfg = R.RefConfig.from_dict(raw)
+    t0 = time.perf_counter()
+    R.generate_mtp_greedy(Wr, rcfg, prompt.tolist(), n_new)
+    c_s = time.perf_counter() - t0
+    return {"gpu_tok_s": round(n_new / g_s, 1), "gpu_s": round(g_s, 4),
+            "cpu_tok_s": round(n_new / c_s, 2), "cpu_s": round(c_s, 2),
+            "sample": f"{n_new} greedy tokens after a 128-token prompt, k=1, B=1, prefill included "
+                      "(GPU bf16 eager steps; CPU the oracle in fp32, 1 run)"}
+
+
 def cpu_baseline(raw, cfg, keep, dec, k, temperature, top_p, seed):
     """One speculative step of the reference algorithm on the host cores, from the GPU
     run's committed state: the k-step MTP draft chain, the deep-copy snapshot of the
@@ -344,33 +460,35 @@ def cpu_baseline(raw, cfg, keep, dec, k, temperature, top_p, seed):
     h_last = dec.h_last.float().cpu()[:, None]
     log(f"cpu baseline setup {time.time() - t_setup:.1f} s (threads {torch.get_num_threads()})")
     B = pending.shape[0]
+    steps, toks = 2, 0
+    inv = S.inv_temperature(temperature)
     t0 = time.perf_counter()
     with torch.no_grad():
-        drafts, _ = R.mtp_chain_draft(W, rcfg, h_last, pending, k)
-        snap = past.clone()
-        ids = torch.cat([pending[:, None], drafts], 1)
-        logits, past, _ = R.model_forward(W, rcfg, ids, past, return_hidden=True)
-        inv = S.inv_temperature(temperature)
-        na, nt = S.spec_accept(logits.bfloat16(), None, drafts.numpy().astype(np.int32), inv, 0,
-                               top_p, seed, 1)
-        past = snap
-        R.model_forward(W, rcfg, pending[:, None], past, return_hidden=True)
-    step_s = time.perf_counter() - t0
-    toks = int(na.sum()) + B
-    model_name = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model_name = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": round(toks / step_s, 3), "unit": "tok/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": (f"1 speculative step (k={k}, B={B}, context {L}) of the CPU restatement "
-                       f"(oracle/) in fp32 on {os.cpu_count()} host CPUs ({model_name}): "
-                       f"{step_s:.2f} s/step, {toks} tokens; extrapolated to tok/s"),
+        for step in range(steps):
+            drafts, _ = R.mtp_chain_draft(W, rcfg, h_last, pending, k)
+            snap = past.clone()
+            ids = torch.cat([pending[:, None], drafts], 1)
+            logits, past, hid = R.model_forward(W, rcfg, ids, past, return_hidden=True)
+            na, nt = S.spec_accept(logits.bfloat16(), None, drafts.numpy().astype(np.int32), inv,
+                                   0, top_p, seed, 1 + step)
+            if int(na.min()) == k:                   # every draft accepted (not with random weights)
+                h_last = hid[:, k:]
+            else:
+                # reject: restore the snapshot and re-run the pending token (mtp.py:156-162);
+                # the batch re-runs together, as the reference does for its one sequence
+                past = snap
+                _, past, hid1 = R.model_forward(W, rcfg, pending[:, None], past, return_hidden=True)
+                h_last = hid1[:, -1:]
+            toks += int(na.sum()) + B
+            pending = torch.from_numpy(nt.astype(np.int64))
+    step_s = (time.perf_counter() - t0) / steps
+    info = cpu_info()
+    return {"value": round(toks / (step_s * steps), 3), "unit": "tok/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"{steps} speculative steps (k={k}, B={B}, context {L}) of the CPU "
+                       f"restatement (oracle/) in fp32 on {info['os_cpu_count']} host CPUs "
+                       f"({info['cpu_model']}): {step_s:.2f} s/step, {toks} tokens; "
+                       "extrapolated to tok/s"),
             "step_seconds": round(step_s, 3)}
 
 
@@ -467,11 +585,25 @@ def main():
     roof = gdn_layer_roofline(model, dec)
     log(f"gdn_layer: {roof['avg_us']} us, {roof['achieved']} GB/s")
     kernels = {"gdn_layer_verify": roof}
+    cpu_legs = not args.no_cpu
+    if cpu_legs:
+        torch.set_num_threads(os.cpu_count())
     if not args.no_isolated:
-        kernels["gdn_verify_isolated"] = [isolated_gdn(B, kd) for B in (1, 8, 32) for kd in (1, 2, 4)]
-        kernels["attn_verify_isolated"] = isolated_attn()
-        kernels["spec_accept_isolated"] = isolated_sampler()
+        kernels["gdn_verify_isolated"] = [isolated_gdn(B, kd, cpu=cpu_legs)
+                                          for B in (1, 8, 32) for kd in (1, 2, 4)]
+        kernels["attn_verify_isolated"] = isolated_attn(cpu=cpu_legs)
+        kernels["spec_accept_isolated"] = isolated_sampler(cpu=cpu_legs)
         kernels["gdn_prefill_chunked"] = isolated_gdn_prefill()
+        kernels["tiny_e2e"] = tiny_e2e() if cpu_legs else None
+        # the CPU legs of the isolated workloads, after every GPU timing (a GPU left idle
+        # through seconds of host work clocks down and would time its next kernels slow)
+        for row in kernels["gdn_verify_isolated"] + [kernels["attn_verify_isolated"],
+                                                     kernels["spec_accept_isolated"]]:
+            leg = row.pop("_cpu", None)
+            if leg is not None:
+                ms, n = leg()
+                row.update(cpu_ms=round(ms, 2), cpu_runs=n,
+                           gpu_speedup=round(ms * 1e3 / row["us"], 1))
     cpu = None
     if not args.no_cpu:
         try:
@@ -497,6 +629,7 @@ def main():
         "projection_paths": projection_paths(model, mtp, args.batch, args.k),
         "kernels": kernels,
         "cpu_baseline": cpu,
+        "cpu_host": cpu_info() if cpu_legs else None,
     }
     print(json.dumps(line), flush=True)
 

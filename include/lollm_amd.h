@@ -278,8 +278,10 @@ int lollm_gdn_layer(const void* proj, long long proj_stride, const void* conv_w,
 /* The same layer for long calls (prefill) with the delta rule in its chunked parallel
  * form: torch_chunk_gated_delta_rule (src/qwen3_5/blocks.py:59-113), which the reference
  * runs for every T > 1 call (blocks.py:316-322), fused with the conv / gating / norm of
- * lollm_gdn_layer.  Chunks of 64 tokens, all products fp32 MFMA; the L2 norm of q and
- * k (blocks.py:124-127) is applied as fp32 scales, as the recurrent kernels do.  Same
+ * lollm_gdn_layer.  Chunks of 64 tokens on bf16 MFMA, each fp32 operand entering as a
+ * hi + lo pair of bf16 values (relative error near 2^-17), the triangular solve's
+ * off-diagonal blocks on fp32 MFMA; the L2 norm of q and k (blocks.py:124-127) is
+ * applied as fp32 scales, as the recurrent kernels do.  Same
  * arguments and the same long-call placement as lollm_gdn_layer: the final state in
  * slot 0 of the half not holding rec_slot[b], the final K-1 raw inputs in rows 0 .. K-2
  * of the window half not holding conv_off[b].  Supported: conv_kernel 4, T > slots,

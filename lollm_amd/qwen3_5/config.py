@@ -98,8 +98,8 @@ class Qwen3_5Config:
 def build_config(raw: dict, fmt: str) -> Qwen3_5Config:
     if fmt != "hf":
         raise NotImplementedError(
-            "qwen3_5: only safetensors (hf) supported; GGUF for Gated DeltaNet is not "
-            "standardized (fail loud rather than guess)")
+            f"qwen3_5 loads checkpoints in the hf (safetensors) format only, not {fmt!r}: "
+            "there is no agreed GGUF tensor layout for the Gated DeltaNet layers")
     return Qwen3_5Config.from_hf(raw)
 
 

@@ -22,7 +22,8 @@ def to_raw(canonical: str, fmt: str):
         if canonical.startswith("model."):
             return "model.language_model." + canonical[len("model."):]
         return canonical
-    raise NotImplementedError("qwen3_5: only hf (safetensors) supported; GGUF not implemented")
+    raise NotImplementedError(f"qwen3_5 has no tensor-name map for the {fmt!r} format "
+                              "(hf safetensors checkpoints only)")
 
 
 def to_canonical(raw: str) -> str:

@@ -584,3 +584,66 @@ def generate_mtp_greedy(W, cfg, ids, n_new, repetition_penalty=1.0):
             pending = true_next
             h_last = hid1[:, -1:]
     return out[:n_new], accepts
+
+
+# ---------------------------------------------------------------------------------
+# acceptance in the reference's own arithmetic (the CPU baseline of the sampler)
+# ---------------------------------------------------------------------------------
+def sample_next_probs(logits, temperature, top_k, top_p):
+    """generate.py:23-36 batched over rows: the distribution sample_next draws from
+    (temperature, top-k keeping logits >= the k-th, top-p by a descending sort with the
+    cumulative mass shifted one place), in float32; greedy rows are one-hot at the first
+    argmax.  logits (R, V) -> probabilities (R, V)."""
+    x = logits.float()
+    if temperature <= 0.0:
+        return F.one_hot(x.argmax(-1), x.shape[-1]).float()
+    x = x / temperature
+    if top_k and top_k > 0:
+        kth = torch.topk(x, top_k, dim=-1).values[:, -1:]
+        x = x.masked_fill(x < kth, float("-inf"))
+    if top_p and 0.0 < top_p < 1.0:
+        sl, si = torch.sort(x, dim=-1, descending=True)
+        cum = torch.softmax(sl, -1).cumsum(-1)
+        drop = torch.zeros_like(cum, dtype=torch.bool)
+        drop[:, 1:] = cum[:, :-1] > top_p
+        sl = sl.masked_fill(drop, float("-inf"))
+        x = torch.empty_like(x).scatter_(-1, si, sl)
+    return torch.softmax(x, -1)
+
+
+def spec_accept_sorted(target, drafts, temperature, top_k, top_p, uniforms, draft=None):
+    """Speculative acceptance with the reference's sampler arithmetic: p_i =
+    sample_next_probs(target[:, i]); q_i = sample_next_probs(draft[:, i]) for sampled
+    drafts, or one-hot at the draft for argmax drafts (draft None, mtp.py:138); accept
+    d_i iff u_i q_i(d_i) < p_i(d_i); at the first rejection draw from
+    norm(max(0, p_i - q_i)), if all k are accepted draw the bonus from p_k, each by
+    inverse CDF over token order with uniform u_k.  target (B, k+1, V); drafts (B, k)
+    long; uniforms (B, k+1) in [0, 1).  Returns (n_accepted (B,), next_token (B,))."""
+    B, T, V = target.shape
+    k = T - 1
+    p = sample_next_probs(target.reshape(B * T, V), temperature, top_k, top_p).view(B, T, V)
+    q = None
+    if draft is not None:
+        q = sample_next_probs(draft.reshape(B * k, V), temperature, top_k, top_p).view(B, k, V)
+    na = torch.zeros(B, dtype=torch.long)
+    nt = torch.zeros(B, dtype=torch.long)
+    for b in range(B):
+        a = 0
+        while a < k:
+            d = drafts[b, a]
+            qd = 1.0 if q is None else float(q[b, a, d])
+            if not float(uniforms[b, a]) * qd < float(p[b, a, d]):
+                break
+            a += 1
+        w = p[b, a].clone()
+        if a < k:
+            if q is None:
+                w[drafts[b, a]] = max(0.0, float(w[drafts[b, a]]) - 1.0)
+            else:
+                w = (w - q[b, a]).clamp_min(0.0)
+            if float(w.sum()) <= 0.0:
+                w = p[b, a].clone()
+        cdf = w.double().cumsum(0)
+        tok = int(torch.searchsorted(cdf, uniforms[b, k].double() * cdf[-1], right=True))
+        na[b], nt[b] = a, min(tok, V - 1)
+    return na, nt

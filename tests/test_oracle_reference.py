@@ -240,3 +240,29 @@ def test_spec_step_capacity_raises():
     d.cache.len_bound = 9
     with pytest.raises(RuntimeError, match="capacity"):
         d._reserve()
+
+
+def test_sorted_acceptance_agrees_with_exact_oracle():
+    """The float restatement of acceptance (the CPU baseline's algorithm, sort-based as
+    generate.py:26-36) against the exact integer C oracle on the same rows and uniforms:
+    identical at temperature 0; with sampling, identical except where a uniform falls
+    within float rounding of a CDF boundary (a few rows at most)."""
+    g = torch.Generator().manual_seed(40)
+    B, k, V = 32, 3, 4096
+    tgt = (torch.randn(B, k + 1, V, generator=g) * 3).bfloat16()
+    drafts = tgt[:, :k].float().argmax(-1)
+    drafts[::2, 1] = torch.randint(0, V, (B // 2,), generator=g)     # some rejections
+    seed, off = 5, 2
+    U = torch.tensor([[S.uniform_u24(seed, off, b, s) for s in range(k + 1)] for b in range(B)],
+                     dtype=torch.float64) / 2 ** 24
+    drf = (tgt[:, :k].float() + torch.randn(B, k, V, generator=g)).bfloat16()
+    for temp, top_p, dl in ((0.0, 1.0, None), (0.7, 0.95, None), (1.0, 0.8, None), (0.7, 0.95, drf)):
+        inv = S.inv_temperature(temp)
+        na_c, nt_c = S.spec_accept(tgt, dl, drafts.numpy().astype(np.int32), inv, 0, top_p, seed, off)
+        na_f, nt_f = R.spec_accept_sorted(tgt.float(), drafts, temp, 0, top_p, U,
+                                          None if dl is None else dl.float())
+        agree = (torch.from_numpy(na_c.astype(np.int64)) == na_f) & (torch.from_numpy(nt_c.astype(np.int64)) == nt_f)
+        if temp == 0.0:
+            assert bool(agree.all())
+        else:
+            assert int(agree.sum()) >= B - 2, (temp, int(agree.sum()))
