@@ -278,12 +278,20 @@ def isolated_gdn_prefill(B=16, T=2048):
             "peak": PEAK_BF16_MFMA_TFLOPS, "frac": round(mf / PEAK_BF16_MFMA_TFLOPS, 3)}
 
 
-def isolated_attn(cpu=False):
+def isolated_attn(cpu=False, step_shape=False):
+    """The gated-attention verify kernel alone: the isolated shape (16 q / 2 kv heads,
+    contexts U[1024, 32768]) or, with step_shape, the shape the dense 8B-class step runs
+    (32 q / 4 kv heads, contexts U[2052, 2308]: a 2048-token prompt plus up to 256
+    decoded tokens)."""
     import torch
     from lollm_amd import ops
     g = torch.Generator().manual_seed(3)
-    B, T, Hq, Hkv, D, max_len = 16, 4, 16, 2, 256, 32768
-    lens = torch.randint(1024, 32769, (B,), generator=g)
+    if step_shape:
+        B, T, Hq, Hkv, D, max_len = 16, 4, 32, 4, 256, 2312
+        lens = torch.randint(2052, 2309, (B,), generator=g)
+    else:
+        B, T, Hq, Hkv, D, max_len = 16, 4, 16, 2, 256, 32768
+        lens = torch.randint(1024, 32769, (B,), generator=g)
     q = torch.randn(B, T, Hq, D, device="cuda").bfloat16()
     kc = torch.randn(B, Hkv, max_len, D, device="cuda").bfloat16()
     vc = torch.randn(B, Hkv, max_len, D, device="cuda").bfloat16()
@@ -592,6 +600,7 @@ def main():
         kernels["gdn_verify_isolated"] = [isolated_gdn(B, kd, cpu=cpu_legs)
                                           for B in (1, 8, 32) for kd in (1, 2, 4)]
         kernels["attn_verify_isolated"] = isolated_attn(cpu=cpu_legs)
+        kernels["attn_verify_step_shape"] = isolated_attn(step_shape=True)
         kernels["spec_accept_isolated"] = isolated_sampler(cpu=cpu_legs)
         kernels["gdn_prefill_chunked"] = isolated_gdn_prefill()
         kernels["tiny_e2e"] = tiny_e2e() if cpu_legs else None

@@ -11,53 +11,41 @@
 // block); its 32 MFMA rows pack n_rep q-heads x QB queries, so every K/V byte read
 // from HBM serves all the q-heads that share it.  A pair's context is cut into
 // 128-key blocks ("units"), and the units of all pairs, laid end to end (pair-major),
-// are dealt out in equal contiguous ranges to a fixed grid of one 8-wave workgroup per
+// are dealt out in equal contiguous ranges to a fixed grid of one 4-wave workgroup per
 // CU.  Every workgroup therefore streams the same number of bytes whatever the context
 // lengths, and no CU idles while another finishes a long sequence.  Each workgroup
 // leaves one partial (m, l, O) per pair it touched; a combine kernel merges the pieces
 // of every pair and applies the gate.
 //
-// Inside a workgroup, two units are in flight ahead of the one computed (256 KB per
-// CU), all their loads issued unconditionally through buffer descriptors (a unit past
-// the range reads through an empty descriptor: zeros, no traffic), so the compiler's
-// vmcnt waits only ever wait for the unit about to be used:
-//   - K: wave w loads its own 16 keys straight into the S MFMA A operand;
-//   - V: coalesced non-temporal loads into registers, staged in LDS (padded rows);
-//   - Q: one unit ahead, staged in LDS (two buffers) at the pair's first unit;
-// and each unit is:
-//   - S^T for keys [16w, 16w+16) x 32 rows on wave w (16x16x32 MFMA, Q^T from LDS);
-//     P^T to LDS as bf16 against a per-row reference max shared by all waves, with the
-//     masked row maxima to LDS, then one barrier: only when a block's maximum exceeds
-//     the reference by 16 in the exponent (and at a pair's first block) do all waves
-//     move the reference, rescale l and O and rewrite P^T behind a second barrier;
-//   - O^T[32w, 32w+32) += V^T P^T on wave w (32x32x16 MFMA, A = V^T read from LDS).
+// Inside a workgroup the four waves split every unit by keys (wave w: keys 32 w ..
+// 32 w + 31) and run independent online softmaxes over them, so the main loop has no
+// barrier and no exchange between waves:
+//   - K: each wave loads its 32 keys straight into the S MFMA A operand (registers,
+//     two units ahead);
+//   - V: each wave's 32 rows arrive by LDS DMA (buffer_load ... lds, two units ahead)
+//     into its own part of the unit's LDS set, and are read back as the A operand of
+//     O^T += V^T P^T with the transposing LDS read (ds_read_b64_tr_b16), which hands
+//     each lane 4 consecutive keys of one column;
+//   - Q: the pair's 32 rows are staged in LDS at the pair's first unit and read as the
+//     S MFMA B operand;
+//   - S^T (32 keys x 32 rows) and O^T (256 columns x 32 rows) are 32x32x16 MFMAs; the
+//     S^T accumulator already holds P^T in the order the O^T MFMA consumes it, so P
+//     never leaves registers;
+//   - the running max of a row only moves (and l, O are rescaled) when a block's
+//     maximum exceeds it by more than 16 in the exponent.
+// At the end of a pair the four waves' (m, l, O) are merged through the free LDS set
+// into the workgroup's piece.
 #include "common.h"
 
 namespace lollm {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int AT_D = 256;            // head dim
 constexpr int AT_ROWS = 32;          // MFMA rows per pair (n_rep x QB)
 constexpr int AT_BLOCK = 128;        // keys per block
-constexpr int AT_WAVES = 8;
-constexpr int AT_THREADS = 64 * AT_WAVES;
 constexpr int AT_MAXB = 512;         // sequences per call (prefix table in LDS)
-constexpr int AT_KROW = AT_D * 2 + 16;        // padded bytes per K / V row in LDS
-constexpr int AT_PROW = AT_BLOCK * 2 + 16;    // padded bytes per P^T row in LDS
-constexpr int AT_OROW = AT_D + 1;             // padded floats per O row in LDS
 constexpr int AT_PART = 2 * AT_ROWS + AT_ROWS * AT_D;  // floats per partial
-constexpr int AT_LDS_V = 0;                                 // V block; O at a pair's end
-constexpr int AT_LDS_Q = AT_LDS_V + AT_BLOCK * AT_KROW;     // two Q buffers
-constexpr int AT_LDS_P = AT_LDS_Q + 2 * AT_ROWS * AT_KROW;
-constexpr int AT_LDS_M = AT_LDS_P + AT_ROWS * AT_PROW;
-constexpr int AT_LDS_PRE = AT_LDS_M + 2 * AT_WAVES * AT_ROWS * 4;
-constexpr int AT_LDS_LEN = AT_LDS_PRE + (AT_MAXB + 1) * 4;
-constexpr int AT_LDS_BYTES = AT_LDS_LEN + AT_MAXB * 4 + 64;
-static_assert(AT_ROWS * AT_OROW * 4 <= AT_BLOCK * AT_KROW, "O of a pair is staged in the V region");
-static_assert(AT_LDS_BYTES <= 160 * 1024, "one workgroup per CU");
 
 struct AttnArgs {
   const uint16_t* q;       // (B, T, Hq, D)
@@ -66,7 +54,7 @@ struct AttnArgs {
   const int32_t* kv_len;   // (B) keys per sequence, the T new ones included
   const uint16_t* gate;    // (B, T, Hq * D) or null
   uint16_t* out;           // (B, T, Hq * D)
-  float* ws;               // partials: (nw + pairs) x AT_PART
+  float* ws;               // partials: (nw + pairs) x AT_PART, then the combine table
   long long seq_stride, head_stride;  // cache strides in elements
   int B, T, Hq, Hkv, n_rep, QB, qblocks, max_len, nw;
   float cl2;               // scale * log2(e)
@@ -76,27 +64,59 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
 
-// Workgroup barrier that orders LDS only: global loads stay in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 __device__ __forceinline__ int seq_len(const AttnArgs& a, int b) {
   return min(max(a.kv_len[b], 0), a.max_len);  // never past the cache capacity
 }
 
 __device__ __forceinline__ int nblk_of(int L) { return (L + AT_BLOCK - 1) / AT_BLOCK; }
 
+// First unit of workgroup w and the workgroup that owns unit u, for U units dealt
+// out to nw workgroups in equal contiguous ranges: w owns [U w / nw, U (w+1) / nw).
+__device__ __forceinline__ long long unit_begin(long long U, int w, int nw) {
+  return U * w / nw;
+}
+__device__ __forceinline__ int unit_owner(long long U, long long u, int nw) {
+  return (int)(((u + 1) * nw - 1) / U);
+}
+
+// Buffer loads through a descriptor over [base, base + bytes): offsets past the end read
+// zeros without touching memory.  AUX = 2 is the non-temporal hint.
+template <int AUX>
+__device__ __forceinline__ u32x4_t at_bload(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, AUX));
+}
+
+// Position of a unit in the pair-major block order: sequence b, pair ph of it, block j
+// of the pair's nb blocks.
+struct AtCursor {
+  int b, ph, j, nb;
+};
+
+constexpr int AW_WAVES = 4;
+constexpr int AW_THREADS = 64 * AW_WAVES;
+constexpr int AW_WKEYS = AT_BLOCK / AW_WAVES;        // 32 keys of each block per wave
+constexpr int AW_VPAIR = 2 * AT_D * 2 + 64;          // two V rows (one DMA) + 64 bytes of padding
+constexpr int AW_VWAVE = AW_WKEYS / 2 * AW_VPAIR;     // 17 KB: one wave's V rows of a block
+constexpr int AW_VSET = AW_WAVES * AW_VWAVE;          // the V rows of one block
+constexpr int AW_QROW = AT_D * 2 + 16;                // padded Q row in LDS
+constexpr int AW_OROW = AT_D / 2 + 4;                 // padded floats per row of an O half-dump
+static_assert(AW_WAVES * AT_ROWS * AW_OROW * 4 <= AW_VSET, "the O dump fits a V set");
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
+
 // pre[b] = blocks of sequences 0..b-1 (pre[0] = 0), for b = 0..B, and len[b] = the
 // clamped key count of sequence b, built in LDS by the whole workgroup (so the main
 // loop never waits on a global load to address the next block).  Returns pre[B].
 __device__ int build_prefix(const AttnArgs& a, int* pre, int* len, int* tmp) {
+  constexpr int WAVES = AW_WAVES;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int carry = 0;
   if (tid == 0) pre[0] = 0;
-  for (int base = 0; base < a.B; base += AT_THREADS) {
+  for (int base = 0; base < a.B; base += AW_THREADS) {
     const int b = base + tid;
     const int Lb = b < a.B ? seq_len(a, b) : 0;
     if (b < a.B) len[b] = Lb;
@@ -110,7 +130,7 @@ __device__ int build_prefix(const AttnArgs& a, int* pre, int* len, int* tmp) {
     __syncthreads();
     int before = carry, all = carry;
 #pragma unroll
-    for (int w = 0; w < AT_WAVES; ++w) {
+    for (int w = 0; w < WAVES; ++w) {
       if (w < wave) before += tmp[w];
       all += tmp[w];
     }
@@ -121,55 +141,28 @@ __device__ int build_prefix(const AttnArgs& a, int* pre, int* len, int* tmp) {
   return carry;
 }
 
-// First unit of workgroup w and the workgroup that owns unit u, for U units dealt
-// out to nw workgroups in equal contiguous ranges: w owns [U w / nw, U (w+1) / nw).
-__device__ __forceinline__ long long unit_begin(long long U, int w, int nw) {
-  return U * w / nw;
-}
-__device__ __forceinline__ int unit_owner(long long U, long long u, int nw) {
-  return (int)(((u + 1) * nw - 1) / U);
-}
+// Workgroup barrier after this wave's LDS accesses complete; the compiler sees a memory
+// clobber (no LDS access moves across it) but no fence, so global loads and LDS DMA in
+// flight are not drained.
+__device__ __forceinline__ void aw_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t at_rsrc(const void* base, uint32_t bytes) {
-  return buf_rsrc(base, bytes);
-}
-// AUX = 2: the non-temporal hint (K and V are read once per launch and should not
-// displace reusable lines; measured 9% faster than the default policy on the C3 shape)
-template <int AUX>
-__device__ __forceinline__ u32x4_t at_bload(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, AUX));
-}
-
-// Position of a unit in the pair-major block order: sequence b, pair ph of it, block j
-// of the pair's nb blocks.
-struct AtCursor {
-  int b, ph, j, nb;
-};
-
-__global__ __launch_bounds__(AT_THREADS, 1) void attn_verify_kernel(AttnArgs a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  unsigned char* v_lds = smem + AT_LDS_V;
-  unsigned char* q_lds = smem + AT_LDS_Q;   // two buffers of AT_ROWS rows
-  unsigned char* p_lds = smem + AT_LDS_P;
-  float* m_lds = reinterpret_cast<float*>(smem + AT_LDS_M);    // [wave][row]
-  float* l_lds = m_lds + AT_WAVES * AT_ROWS;
-  int* pre = reinterpret_cast<int*>(smem + AT_LDS_PRE);
-  int* len = reinterpret_cast<int*>(smem + AT_LDS_LEN);
-  int* tmp = len + AT_MAXB;
+__global__ __launch_bounds__(AW_THREADS, 1) void attn_verify_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char vs0[AW_VSET];   // V of even units
+  __shared__ __attribute__((aligned(16))) unsigned char vs1[AW_VSET];   // V of odd units
+  __shared__ __attribute__((aligned(16))) unsigned char qs[AT_ROWS * AW_QROW];   // Q of the pair
+  __shared__ float mx[AW_WAVES][32], lx[AW_WAVES][32];
+  __shared__ int pre[AT_MAXB + 1], len[AT_MAXB], tmp[AW_WAVES];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l16 = lane & 15, g4 = lane >> 4, l32 = lane & 31, h2 = lane >> 5;
+  const int l32 = lane & 31, h = lane >> 5;
   const int w = blockIdx.x;
-  const int PH = a.Hkv * a.qblocks;  // pairs per sequence
+  const int PH = a.Hkv * a.qblocks;
 
   const long long U = (long long)PH * build_prefix(a, pre, len, tmp);
   {
-    // the combine's table: per pair, the first and last workgroup whose range touches it
-    // (-1 for a pair with no keys) and the unit count, so the combine reads one entry
-    // instead of rebuilding the block prefix
     const int npairs = a.B * PH;
     int4* tab = reinterpret_cast<int4*>(a.ws + (size_t)(a.nw + npairs) * AT_PART);
-    for (int p = w * AT_THREADS + tid; p < npairs; p += a.nw * AT_THREADS) {
+    for (int p = w * AW_THREADS + tid; p < npairs; p += a.nw * AW_THREADS) {
       const int pb = p / PH, pph = p % PH, pnb = pre[pb + 1] - pre[pb];
       int wf = -1, wl = -1;
       if (pnb > 0) {
@@ -183,7 +176,6 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
   const long long u0 = unit_begin(U, w, a.nw), u1 = unit_begin(U, w + 1, a.nw);
   if (u0 >= u1) return;
 
-  // locate the first unit: the last sequence whose first unit is <= u0 (never empty)
   AtCursor C;
   {
     int lo = 0, hi = a.B - 1;
@@ -197,7 +189,6 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
     C.ph = (int)(r / C.nb);
     C.j = (int)(r % C.nb);
   }
-  // (cursor fields are the same in every lane: kept in scalar registers)
   auto uni = [](AtCursor X) {
     X.b = __builtin_amdgcn_readfirstlane(X.b);
     X.ph = __builtin_amdgcn_readfirstlane(X.ph);
@@ -220,267 +211,239 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
     return uni(Y);
   };
 
-  // The loads of a unit (all unconditional: a unit past the range, or Q of a unit that
-  // does not start its pair, gets an empty descriptor and reads zeros without traffic).
-  //   V: cooperative, chunk c = 512 i + tid holds key 16 i + tid / 32, bytes 16 (tid % 32)
-  //   K: wave w's own 16 keys straight into the S MFMA A operand (lane: key 16 w + l16,
-  //      bytes 64 s + 16 g4 for k-step s); keys past the sequence read zero.  Default
-  //      cache policy: each load reads half of 16 lines, and L2 merges the two halves
-  //      (with the non-temporal hint they were fetched separately: 10% slower)
-  //   Q: cooperative rows r = 16 it + tid / 32 (r = hr QB + i), staged at the pair's start;
-  //      one unit ahead, issued first in its unit's loads so waiting for it never waits
-  //      for the later K/V loads
-  u32x4_t vr[2][8], kr[2][8], qr[2];
-  auto issue_v = [&](int set, const AtCursor& X, bool live) {
+  // zero both V sets once: rows past a sequence's end are never loaded, and what they
+  // hold must stay finite (their P is 0)
+  for (int i = tid; i < AW_VSET / 16; i += AW_THREADS) {
+    *reinterpret_cast<uint4*>(vs0 + 16 * i) = make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(vs1 + 16 * i) = make_uint4(0, 0, 0, 0);
+  }
+  __syncthreads();
+
+  // Loads of a unit (all unconditional; a unit past the range gets an empty descriptor).
+  //   K: wave w's 32 keys straight into the S MFMA A operand (lane: key 32 w + l32,
+  //      16 bytes at d chunk 2 ks + h for k-step ks)
+  //   V: wave w's 32 rows by LDS DMA into its part of the unit's set, 2 rows (1 KB)
+  //      per instruction, 64 bytes of padding after each pair of rows (so that the
+  //      transposing reads of 8 consecutive rows hit every bank at most twice)
+  //   Q: the next pair's 32 rows into registers one unit ahead (thread t: row t / 32 + 8 i,
+  //      chunk t % 32), staged in LDS (padded rows) at the pair's first unit and read as
+  //      the S MFMA B operand (lane: row l32, d chunk 2 ks + h)
+  u32x4_t kr[2][16], qr[4];
+  auto rsrc_of = [&](const uint16_t* cache, const AtCursor& X, bool live) {
     const int kvh = live ? X.ph / a.qblocks : 0;
     const uint32_t bytes = live ? (uint32_t)__builtin_amdgcn_readfirstlane(len[X.b]) * (AT_D * 2) : 0u;
-    const uint16_t* base = a.vc + (live ? (size_t)X.b * a.seq_stride + (size_t)kvh * a.head_stride : 0);
-    const __amdgpu_buffer_rsrc_t rs = at_rsrc(base, bytes);
-    const uint32_t vo = (uint32_t)(X.j * AT_BLOCK + (tid >> 5)) * (AT_D * 2) + (uint32_t)(tid & 31) * 16u;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) vr[set][i] = at_bload<2>(rs, vo, (uint32_t)i * 16u * (AT_D * 2));
+    const uint16_t* base = cache + (live ? (size_t)X.b * a.seq_stride + (size_t)kvh * a.head_stride : 0);
+    return buf_rsrc(base, bytes);
   };
   auto issue_k = [&](int set, const AtCursor& X, bool live) {
-    const int kvh = live ? X.ph / a.qblocks : 0;
-    const uint32_t bytes = live ? (uint32_t)__builtin_amdgcn_readfirstlane(len[X.b]) * (AT_D * 2) : 0u;
-    const uint16_t* base = a.kc + (live ? (size_t)X.b * a.seq_stride + (size_t)kvh * a.head_stride : 0);
-    const __amdgpu_buffer_rsrc_t rs = at_rsrc(base, bytes);
-    const uint32_t ko = (uint32_t)(X.j * AT_BLOCK + 16 * wave + l16) * (AT_D * 2) + (uint32_t)g4 * 16u;
+    const __amdgpu_buffer_rsrc_t rs = rsrc_of(a.kc, X, live);
+    const uint32_t ko = (uint32_t)(X.j * AT_BLOCK + AW_WKEYS * wave + l32) * (AT_D * 2) + 16u * h;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) kr[set][s] = at_bload<0>(rs, ko + (uint32_t)s * 64u, 0u);
+    for (int ks = 0; ks < 16; ++ks) kr[set][ks] = at_bload<0>(rs, ko + 32u * ks, 0u);
+  };
+  auto issue_v = [&](unsigned char* vset, const AtCursor& X, bool live) {
+    const __amdgpu_buffer_rsrc_t rs = rsrc_of(a.vc, X, live);
+    unsigned char* dst = vset + wave * AW_VWAVE;
+    const uint32_t vo = (uint32_t)(X.j * AT_BLOCK + AW_WKEYS * wave) * (AT_D * 2) + 16u * lane;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + AW_VPAIR * i), 16, vo, 1024u * i, 0, 2);
   };
   auto issue_q = [&](const AtCursor& X, bool load) {
     const int kvh = load ? X.ph / a.qblocks : 0, qb = load ? X.ph % a.qblocks : 0;
     const int q0_ = qb * a.QB, QB_ = min(a.QB, a.T - q0_), rows_ = a.n_rep * QB_;
     const uint32_t bytes = load ? (uint32_t)a.T * (uint32_t)a.Hq * (AT_D * 2) : 0u;
     const uint16_t* base = a.q + (load ? (size_t)X.b * a.T * a.Hq * AT_D : 0);
-    const __amdgpu_buffer_rsrc_t rs = at_rsrc(base, bytes);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(base, bytes);
 #pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int r = 16 * it + (tid >> 5);
+    for (int ii = 0; ii < 4; ++ii) {
+      const int r = (tid >> 5) + 8 * ii, c = tid & 31;
       const int hr = r / QB_, i = r % QB_;
       const uint32_t qo = r < rows_ ? ((uint32_t)(q0_ + i) * (uint32_t)a.Hq + (uint32_t)(kvh * a.n_rep + hr)) *
-                                          (AT_D * 2) + (uint32_t)(tid & 31) * 16u
-                                    : 0xFFFFFFF0u;
-      qr[it] = at_bload<0>(rs, qo, 0u);
+                                          (AT_D * 2) + 16u * c
+                                    : 0x80000000u;
+      qr[ii] = at_bload<0>(rs, qo, 0u);
     }
   };
 
   AtCursor X1 = advance(C), X2 = advance(X1);
   issue_q(C, true);
-  issue_v(0, C, true);
   issue_k(0, C, true);
-  issue_v(1, X1, u0 + 1 < u1);
+  issue_v(vs0, C, true);
   issue_k(1, X1, u0 + 1 < u1);
+  issue_v(vs1, X1, u0 + 1 < u1);
 
-  f32x16 O;   // O^T of this wave's 32 value columns
-  float m_s[2], l_s[2], m_o;
-  int qpos_s0 = 0, qpos_s1 = 0, L = 0, QB = 1, q0 = 0, rows = 0, qbuf = 1;
+  f32x16 O[8];            // O^T: d-tile dt (32 columns) x the 32 rows; lane row = l32
+  float m_ref = -INFINITY, l_s = 0.f;
+  int qpos = 0, L = 0;
 
   for (long long ub = u0; ub < u1; ub += 2) {
 #pragma unroll
     for (int set = 0; set < 2; ++set) {
+      unsigned char* vset = set ? vs1 : vs0;
       const long long u = ub + set;
-      {
-        // the second unit of the last pair of units may lie past the range: it issues
-        // its (empty) loads like every other, so the loads in flight are the same on
-        // every path and the compiler's waits stay exact, but computes nothing
-        const bool live = u < u1;
-        const int b = C.b, ph = C.ph, j = C.j, nb = C.nb;
-        const bool seg_first = live && ((u == u0) || (j == 0));
-        const bool seg_last = live && ((u == u1 - 1) || (j == nb - 1));
+      const bool live = u < u1;
+      const int b = C.b, ph = C.ph, j = C.j, nb = C.nb;
+      const bool seg_first = live && ((u == u0) || (j == 0));
+      const bool seg_last = live && ((u == u1 - 1) || (j == nb - 1));
+      if (seg_first) {
         const int qb = ph % a.qblocks;
-        if (seg_first) {
-          L = __builtin_amdgcn_readfirstlane(len[b]);
-          q0 = qb * a.QB;
-          QB = min(a.QB, a.T - q0);
-          rows = a.n_rep * QB;
-          qpos_s0 = L - a.T + q0 + l16 % QB;
-          qpos_s1 = L - a.T + q0 + (16 + l16) % QB;
+        L = __builtin_amdgcn_readfirstlane(len[b]);
+        const int q0 = qb * a.QB, QB = min(a.QB, a.T - q0);
+        qpos = L - a.T + q0 + l32 % QB;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) O[r] = 0.f;
-          m_s[0] = m_s[1] = -INFINITY;
-          l_s[0] = l_s[1] = 0.f;
-          m_o = -INFINITY;
-          // this pair's Q into the other buffer (its last reader was two pairs ago)
-          qbuf ^= 1;
+        for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-          for (int it = 0; it < 2; ++it) {
-            const int c = it * AT_THREADS + tid;
-            *reinterpret_cast<u32x4_t*>(q_lds + qbuf * (AT_ROWS * AT_KROW) + (c >> 5) * AT_KROW + (c & 31) * 16) =
-                qr[it];
-          }
-        }
-        const int key0 = j * AT_BLOCK;
-
-        // 1. stage V, then Q of unit u + 1 and V of unit u + 2 into the registers just freed
+          for (int r = 0; r < 16; ++r) O[dt][r] = 0.f;
+        m_ref = -INFINITY;
+        l_s = 0.f;
+        // (the previous pair's last unit ended with barriers: no wave still reads qs)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int c = i * AT_THREADS + tid;
-          *reinterpret_cast<u32x4_t*>(v_lds + (c >> 5) * AT_KROW + (c & 31) * 16) = vr[set][i];
-        }
-        const bool live2 = u + 2 < u1;
-        issue_q(X1, u + 1 < u1 && X1.j == 0);
-        issue_v(set, X2, live2);
-        lds_barrier();
-
-        // 2. S^T for keys [16 w, 16 w + 16) x rows [0, 32): K from registers, Q^T from LDS
-        f32x4 S[2];
-#pragma unroll
-        for (int r2 = 0; r2 < 2; ++r2)
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) S[r2][jj] = 0.f;
-        if (live) {
-          const unsigned char* qrow = q_lds + qbuf * (AT_ROWS * AT_KROW) + l16 * AT_KROW + 16 * g4;
-#pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            const bf16x8 kA = __builtin_bit_cast(bf16x8, kr[set][s]);
-            const bf16x8 q0B = *reinterpret_cast<const bf16x8*>(qrow + 64 * s);
-            const bf16x8 q1B = *reinterpret_cast<const bf16x8*>(qrow + 16 * AT_KROW + 64 * s);
-            S[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kA, q0B, S[0], 0, 0, 0);
-            S[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kA, q1B, S[1], 0, 0, 0);
-          }
-        }
-        // the K loads of unit u + 2 into the registers S just consumed
-        issue_k(set, X2, live2);
-
-        if (live) {
-          // 3. mask (key < L and <= the row's query position); this wave's row maxima to
-          //    LDS, and P^T against the reference max m_s (the running max as of the last
-          //    rescale, the same in every wave), written before the one barrier
-          float mx[2], ps[2];
-#pragma unroll
-          for (int r2 = 0; r2 < 2; ++r2) {
-            const int qp = r2 ? qpos_s1 : qpos_s0;
-            const int kbase = key0 + 16 * wave + 4 * g4;
-            const int lim = min(L - 1, qp) - kbase;   // keys kbase + jj allowed iff jj <= lim
-            mx[r2] = -INFINITY;
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-              S[r2][jj] = jj <= lim ? S[r2][jj] : -INFINITY;
-              mx[r2] = fmaxf(mx[r2], S[r2][jj]);
-            }
-            mx[r2] = fmaxf(mx[r2], __shfl_xor(mx[r2], 16, 64));
-            mx[r2] = fmaxf(mx[r2], __shfl_xor(mx[r2], 32, 64));
-            if (lane < 16) m_lds[wave * AT_ROWS + 16 * r2 + lane] = mx[r2];
-            const int row = 16 * r2 + l16;
-            const float base = m_s[r2] == -INFINITY ? 0.f : m_s[r2] * a.cl2;
-            float p[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) p[jj] = fast_exp2(__builtin_fmaf(S[r2][jj], a.cl2, -base));
-            ps[r2] = (p[0] + p[1]) + (p[2] + p[3]);
-            const uint32_t lo = (uint32_t)f32_to_bf16(p[0]) | ((uint32_t)f32_to_bf16(p[1]) << 16);
-            const uint32_t hi = (uint32_t)f32_to_bf16(p[2]) | ((uint32_t)f32_to_bf16(p[3]) << 16);
-            *reinterpret_cast<uint2*>(p_lds + row * AT_PROW + (16 * wave + 4 * g4) * 2) = make_uint2(lo, hi);
-          }
-          lds_barrier();
-          // 4. the block maxima of all waves.  While no row's maximum exceeds its reference
-          //    by more than 16 in the exponent (weights up to 2^16, safe in bf16 P and fp32
-          //    sums), P^T stands and nothing is rescaled; otherwise (always at a pair's first
-          //    block) every wave moves the references to the running maxima, rescales l and
-          //    O, and rewrites its P^T.  Every wave evaluates all 32 rows from the same LDS
-          //    maxima and references, so all take the same branch.
-          float mb[2];
-          bool big = false;
-#pragma unroll
-          for (int r2 = 0; r2 < 2; ++r2) {
-            const int row = 16 * r2 + l16;
-            mb[r2] = m_lds[row];
-#pragma unroll
-            for (int ww = 1; ww < AT_WAVES; ++ww) mb[r2] = fmaxf(mb[r2], m_lds[ww * AT_ROWS + row]);
-            big = big || (mb[r2] - m_s[r2]) * a.cl2 > 16.f;   // false when both are -inf
-          }
-          float mbo = m_lds[l32];
-#pragma unroll
-          for (int ww = 1; ww < AT_WAVES; ++ww) mbo = fmaxf(mbo, m_lds[ww * AT_ROWS + l32]);
-          big = big || (mbo - m_o) * a.cl2 > 16.f;
-          if (__builtin_amdgcn_readfirstlane((int)(__ballot(big) != 0))) {
-#pragma unroll
-            for (int r2 = 0; r2 < 2; ++r2) {
-              const int row = 16 * r2 + l16;
-              const float mn = fmaxf(m_s[r2], mb[r2]);
-              const bool live = mn != -INFINITY;
-              const float alpha = live ? fast_exp2((m_s[r2] - mn) * a.cl2) : 1.f;
-              const float base = live ? mn * a.cl2 : 0.f;
-              float p[4];
-#pragma unroll
-              for (int jj = 0; jj < 4; ++jj) p[jj] = fast_exp2(__builtin_fmaf(S[r2][jj], a.cl2, -base));
-              l_s[r2] = l_s[r2] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-              m_s[r2] = mn;
-              const uint32_t lo = (uint32_t)f32_to_bf16(p[0]) | ((uint32_t)f32_to_bf16(p[1]) << 16);
-              const uint32_t hi = (uint32_t)f32_to_bf16(p[2]) | ((uint32_t)f32_to_bf16(p[3]) << 16);
-              *reinterpret_cast<uint2*>(p_lds + row * AT_PROW + (16 * wave + 4 * g4) * 2) = make_uint2(lo, hi);
-            }
-            const float mn = fmaxf(m_o, mbo);
-            const float alpha = mn == -INFINITY ? 1.f : fast_exp2((m_o - mn) * a.cl2);
-            m_o = mn;
-            O *= alpha;
-            lds_barrier();
-          } else {
-            l_s[0] += ps[0];
-            l_s[1] += ps[1];
-          }
-          // 5. O^T[32 w .. 32 w + 32) += V^T P^T over the 128 keys
-#pragma unroll
-          for (int ks = 0; ks < AT_BLOCK / 16; ++ks) {
-            const bf16x8 pB = *reinterpret_cast<const bf16x8*>(p_lds + l32 * AT_PROW + (16 * ks + 8 * h2) * 2);
-            const unsigned char* vcol = v_lds + (16 * ks + 8 * h2) * AT_KROW + (32 * wave + l32) * 2;
-            bf16x8 vA;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) vA[e] = *reinterpret_cast<const __bf16*>(vcol + e * AT_KROW);
-            O = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vA, pB, O, 0, 0, 0);
-          }
-          lds_barrier();
-
-          if (seg_last) {
-            // thread-derived addresses are recomputed from an opaque copy of the thread
-            // index here, not hoisted out of the unit loop (where they would not fit the
-            // registers next to the two K/V units in flight)
-            int t = tid;
-            asm volatile("" : "+v"(t));
-            const int tl = t & 63, tw = t >> 6, t32 = tl & 31, th2 = tl >> 5;
-            // ---- row sums: lanes sharing a row, then waves ----
-#pragma unroll
-            for (int r2 = 0; r2 < 2; ++r2) {
-              float l = l_s[r2];
-              l += __shfl_xor(l, 16, 64);
-              l += __shfl_xor(l, 32, 64);
-              if (tl < 16) l_lds[tw * AT_ROWS + 16 * r2 + tl] = l;
-            }
-            // O^T -> LDS as O[row][d] (the V block region is free until the next staging)
-            float* o_lds = reinterpret_cast<float*>(v_lds);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int d = 32 * tw + 8 * (r >> 2) + 4 * th2 + (r & 3);
-              o_lds[t32 * AT_OROW + d] = O[r];
-            }
-            if (th2 == 0 && tw == 0) m_lds[t32] = m_o;
-            lds_barrier();
-            const int pair = b * PH + ph;
-            // this workgroup's piece of the pair, in slot w + pair (unique: pieces are ordered
-            // in both w and pair).  The combine kernel finishes every pair, so no gate load
-            // here: waiting on a late load would drain the K/V loads in flight.
-            float* part = a.ws + ((size_t)w + pair) * AT_PART;
-            if (t < AT_ROWS) {
-              float l = 0.f;
-#pragma unroll
-              for (int ww = 0; ww < AT_WAVES; ++ww) l += l_lds[ww * AT_ROWS + t];
-              part[t] = m_lds[t];
-              part[AT_ROWS + t] = l;
-            }
-            for (int c = t; c < rows * (AT_D / 4); c += AT_THREADS) {
-              const int r = c / (AT_D / 4), d0 = (c % (AT_D / 4)) * 4;
-              const float* src = o_lds + r * AT_OROW + d0;
-              *reinterpret_cast<float4*>(part + 2 * AT_ROWS + r * AT_D + d0) =
-                  make_float4(src[0], src[1], src[2], src[3]);
-            }
-            lds_barrier();  // o_lds / l_lds / m_lds read before the next staging overwrites them
-          }
-        }
-        C = X1;
-        X1 = X2;
-        X2 = advance(X2);
+        for (int ii = 0; ii < 4; ++ii)
+          *reinterpret_cast<u32x4_t*>(qs + ((tid >> 5) + 8 * ii) * AW_QROW + 16 * (tid & 31)) = qr[ii];
+        aw_barrier();
       }
+      const bool live2 = u + 2 < u1;
+      // Q of the next unit's pair (staged at that unit's start)
+      issue_q(X1, u + 1 < u1 && (X1.j == 0));
+
+      // S^T (32 keys x 32 rows) = K Q^T
+      f32x16 S;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) S[r] = 0.f;
+      if (live) {
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) {
+          const bf16x8 qb = *reinterpret_cast<const bf16x8*>(qs + l32 * AW_QROW + 16 * h + 32 * ks);
+          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[set][ks]), qb, S, 0, 0, 0);
+        }
+      }
+      issue_k(set, X2, live2);
+
+      if (live) {
+        // mask: acc r holds key 32 wave + 8 (r / 4) + 4 h + r % 4 of the block
+        const int kb = j * AT_BLOCK + AW_WKEYS * wave + 4 * h;
+        const int lim = min(L - 1, qpos) - kb;
+        float bm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = 8 * (r >> 2) + (r & 3);
+          S[r] = kk <= lim ? S[r] : -INFINITY;
+          bm = fmaxf(bm, S[r]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        // the reference max moves (and l, O are rescaled) only when a row's block max
+        // exceeds it by more than 16 in the exponent (always at a pair's first block)
+        const bool big = (bm - m_ref) * a.cl2 > 16.f;
+        if (__builtin_amdgcn_readfirstlane((int)(__ballot(big) != 0))) {
+          const float mn = fmaxf(m_ref, bm);
+          const float alpha = mn == -INFINITY ? 1.f : fast_exp2((m_ref - mn) * a.cl2);
+          m_ref = mn;
+          l_s *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) O[dt] *= alpha;
+        }
+        const float base = m_ref == -INFINITY ? 0.f : m_ref * a.cl2;
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(S[r], a.cl2, -base));
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ps += p[r];
+        l_s += ps;
+        bf16x8 P[2];
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          u32x4_t pw;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            pw[e] = (uint32_t)f32_to_bf16(p[8 * k2 + 2 * e]) | ((uint32_t)f32_to_bf16(p[8 * k2 + 2 * e + 1]) << 16);
+          P[k2] = __builtin_bit_cast(bf16x8, pw);
+        }
+
+        // O^T += V^T P^T: A = V^T from LDS by transposing reads (lane: column 32 dt + l32,
+        // keys 16 ks + 4 h + 0..3 and 16 ks + 8 + 4 h + 0..3, the order P holds them in)
+        // lane's rows 16 ks + 8 q + x (x = 4 h + (lane % 16) / 4), columns 32 dt +
+        // 16 ((lane / 16) % 2) + 4 (lane % 4): a per-lane base plus constant offsets
+        const int x = 4 * h + ((lane & 15) >> 2);
+        const unsigned char* vw = vset + wave * AW_VWAVE + (x >> 1) * AW_VPAIR + (x & 1) * (AT_D * 2) +
+                                  32 * ((lane >> 4) & 1) + 8 * (lane & 3);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4_t*)(vw + 8 * ks * AW_VPAIR + 64 * dt));
+            const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4_t*)(vw + (8 * ks + 4) * AW_VPAIR + 64 * dt));
+            const u32x2_t w0 = __builtin_bit_cast(u32x2_t, v0), w1 = __builtin_bit_cast(u32x2_t, v1);
+            const u32x4_t wa = {w0.x, w0.y, w1.x, w1.y};
+            const bf16x8 vA = __builtin_bit_cast(bf16x8, wa);
+            O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vA, P[ks], O[dt], 0, 0, 0);
+          }
+        }
+      }
+
+      if (seg_last) {
+        // merge the four waves' (m, l, O) of this pair into the workgroup's piece, in two
+        // halves of d through the free V set: each wave dumps its O (straight from the
+        // accumulators), then every thread sums one row's 16 columns with the waves'
+        // weights exp(m_w - M)
+        const float lrow = l_s + __shfl_xor(l_s, 32, 64);
+        aw_barrier();   // every wave is done reading this set
+        if (h == 0) {
+          mx[wave][l32] = m_ref;
+          lx[wave][l32] = lrow;
+        }
+        const int pair = b * PH + ph;
+        float* part = a.ws + ((size_t)w + pair) * AT_PART;
+        float* dump = reinterpret_cast<float*>(vset);
+        const int srow = tid >> 3, sc8 = tid & 7;
+        float wgt[AW_WAVES];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              *reinterpret_cast<float4*>(dump + (wave * AT_ROWS + l32) * AW_OROW + 32 * dt + 8 * q + 4 * h) =
+                  make_float4(O[4 * half + dt][4 * q], O[4 * half + dt][4 * q + 1], O[4 * half + dt][4 * q + 2],
+                              O[4 * half + dt][4 * q + 3]);
+          aw_barrier();
+          if (half == 0) {
+            float M = mx[0][srow];
+#pragma unroll
+            for (int ww = 1; ww < AW_WAVES; ++ww) M = fmaxf(M, mx[ww][srow]);
+            float Lsum = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < AW_WAVES; ++ww) {
+              const float mw = mx[ww][srow];
+              wgt[ww] = mw == -INFINITY ? 0.f : fast_exp2((mw - M) * a.cl2);
+              Lsum += lx[ww][srow] * wgt[ww];
+            }
+            if (sc8 == 0) {
+              part[srow] = M;
+              part[AT_ROWS + srow] = Lsum;
+            }
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int ww = 0; ww < AW_WAVES; ++ww) {
+              const float4 v = *reinterpret_cast<const float4*>(dump + (ww * AT_ROWS + srow) * AW_OROW + 16 * sc8 + 4 * k);
+              acc.x += wgt[ww] * v.x; acc.y += wgt[ww] * v.y; acc.z += wgt[ww] * v.z; acc.w += wgt[ww] * v.w;
+            }
+            *reinterpret_cast<float4*>(part + 2 * AT_ROWS + srow * AT_D + 128 * half + 16 * sc8 + 4 * k) = acc;
+          }
+          aw_barrier();   // the dump is read before it is overwritten (and the set refilled)
+        }
+      }
+      // V of unit u + 2 into this set
+      issue_v(vset, X2, live2);
+      C = X1;
+      X1 = X2;
+      X2 = advance(X2);
     }
   }
 }
@@ -629,16 +592,7 @@ LOLLM_API int lollm_attn_verify(const void* q, const void* k_cache, const void* 
   a.max_len = max_len; a.nw = nw;
   a.cl2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
-  static bool lds_set[64] = {};   // per device: the attribute is set on the current device
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return LOLLM_EUNSUPPORTED;
-  if (!lds_set[dev]) {
-    hipError_t e = hipFuncSetAttribute((const void*)attn_verify_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, AT_LDS_BYTES);
-    if (e != hipSuccess) return LOLLM_EHIP_BASE + (int)e;
-    lds_set[dev] = true;
-  }
-  hipLaunchKernelGGL(attn_verify_kernel, dim3(nw), dim3(AT_THREADS), AT_LDS_BYTES, st, a);
+  hipLaunchKernelGGL(attn_verify_kernel, dim3(nw), dim3(AW_THREADS), 0, st, a);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(AT_ROWS, B * Hkv * qblocks), dim3(256), 0, st, a);
   return launch_status();
