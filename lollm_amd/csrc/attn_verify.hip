@@ -21,7 +21,8 @@
 // 32 w + 31) and run independent online softmaxes over them, so the main loop has no
 // barrier and no exchange between waves:
 //   - K: each wave loads its 32 keys straight into the S MFMA A operand (registers,
-//     two units ahead);
+//     one unit ahead: with V two units ahead that keeps a wave's loads in flight under
+//     the 63 that vmcnt counts, so issuing a load never stalls the wave);
 //   - V: each wave's 32 rows arrive by LDS DMA (buffer_load ... lds, two units ahead)
 //     into its own part of the unit's LDS set, and are read back as the A operand of
 //     O^T += V^T P^T with the transposing LDS read (ds_read_b64_tr_b16), which hands
@@ -221,25 +222,25 @@ __global__ __launch_bounds__(AW_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
 
   // Loads of a unit (all unconditional; a unit past the range gets an empty descriptor).
   //   K: wave w's 32 keys straight into the S MFMA A operand (lane: key 32 w + l32,
-  //      16 bytes at d chunk 2 ks + h for k-step ks)
+  //      16 bytes at d chunk 2 ks + h for k-step ks), one unit ahead
   //   V: wave w's 32 rows by LDS DMA into its part of the unit's set, 2 rows (1 KB)
   //      per instruction, 64 bytes of padding after each pair of rows (so that the
   //      transposing reads of 8 consecutive rows hit every bank at most twice)
   //   Q: the next pair's 32 rows into registers one unit ahead (thread t: row t / 32 + 8 i,
   //      chunk t % 32), staged in LDS (padded rows) at the pair's first unit and read as
   //      the S MFMA B operand (lane: row l32, d chunk 2 ks + h)
-  u32x4_t kr[2][16], qr[4];
+  u32x4_t kr[16], qr[4];
   auto rsrc_of = [&](const uint16_t* cache, const AtCursor& X, bool live) {
     const int kvh = live ? X.ph / a.qblocks : 0;
     const uint32_t bytes = live ? (uint32_t)__builtin_amdgcn_readfirstlane(len[X.b]) * (AT_D * 2) : 0u;
     const uint16_t* base = cache + (live ? (size_t)X.b * a.seq_stride + (size_t)kvh * a.head_stride : 0);
     return buf_rsrc(base, bytes);
   };
-  auto issue_k = [&](int set, const AtCursor& X, bool live) {
+  auto issue_k = [&](const AtCursor& X, bool live) {
     const __amdgpu_buffer_rsrc_t rs = rsrc_of(a.kc, X, live);
     const uint32_t ko = (uint32_t)(X.j * AT_BLOCK + AW_WKEYS * wave + l32) * (AT_D * 2) + 16u * h;
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) kr[set][ks] = at_bload<0>(rs, ko + 32u * ks, 0u);
+    for (int ks = 0; ks < 16; ++ks) kr[ks] = at_bload<0>(rs, ko + 32u * ks, 0u);
   };
   auto issue_v = [&](unsigned char* vset, const AtCursor& X, bool live) {
     const __amdgpu_buffer_rsrc_t rs = rsrc_of(a.vc, X, live);
@@ -268,9 +269,8 @@ __global__ __launch_bounds__(AW_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
 
   AtCursor X1 = advance(C), X2 = advance(X1);
   issue_q(C, true);
-  issue_k(0, C, true);
+  issue_k(C, true);
   issue_v(vs0, C, true);
-  issue_k(1, X1, u0 + 1 < u1);
   issue_v(vs1, X1, u0 + 1 < u1);
 
   f32x16 O[8];            // O^T: d-tile dt (32 columns) x the 32 rows; lane row = l32
@@ -315,10 +315,10 @@ __global__ __launch_bounds__(AW_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
 #pragma unroll
         for (int ks = 0; ks < 16; ++ks) {
           const bf16x8 qb = *reinterpret_cast<const bf16x8*>(qs + l32 * AW_QROW + 16 * h + 32 * ks);
-          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[set][ks]), qb, S, 0, 0, 0);
+          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[ks]), qb, S, 0, 0, 0);
         }
       }
-      issue_k(set, X2, live2);
+      issue_k(X1, u + 1 < u1);   // K of the next unit into the registers S consumed
 
       if (live) {
         // mask: acc r holds key 32 wave + 8 (r / 4) + 4 h + r % 4 of the block
