@@ -113,8 +113,8 @@ def run_e2e(model, mtp, cfg, B, prompt_len, k, steps, warmup, temperature, top_p
 
 
 def projection_paths(model, mtp, B, k):
-    """The path of each projection shape of the step ("gemm" = lollm_gemm, "blas" =
-    hipBLASLt; a fixed function of the shape), keyed "NxK M=rows"."""
+    """The path of each projection shape of the step ("gemm grid g" = lollm_gemm on g
+    workgroups, "blas" = hipBLASLt; a fixed function of the shape), keyed "NxK M=rows"."""
     out = {}
     layers = list(model.model.layers) + list(mtp.layers)
     projs = [model.lm_head, mtp.fc]
@@ -124,7 +124,8 @@ def projection_paths(model, mtp, B, k):
     for p in projs:
         for rows in (B, B * (k + 1)):
             tag = f"{p.N}x{p.K}{' swiglu' if p.epilogue else ''} M={rows}"
-            out[tag] = p.path(rows)
+            path = p.path(rows)
+            out[tag] = f"gemm grid {p.grid()}" if path == "gemm" else path
     return dict(sorted(out.items()))
 
 
@@ -510,10 +511,21 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 PROBE_COPY_BYTES = 256 << 20
 
 
+PROBE_ORDER = ("gdn_layer", "gemm_qkv", "gemm_gate_up", "gemm_down", "attn_step", "spec_accept_c4")
+
+
 def pmc_probe(B=16, T=4, launches=20):
-    """Launch only the roofline kernel (the fused GDN layer at the step's shape, inputs
-    of the dense 8B-class layer) `launches` times, then torch.neg over 256 MiB (reads
-    and writes PROBE_COPY_BYTES each) 5 times as the counter calibration."""
+    """Launch each hot kernel `launches` times at the dense 8B-class step's shapes, in
+    the order of PROBE_ORDER, then torch.neg over 256 MiB (reads and writes
+    PROBE_COPY_BYTES each) 5 times as the counter calibration:
+      gdn_layer       the fused GDN layer, B=16, T=4, 32 v / 16 qk heads of 128
+      gemm_qkv        lollm_gemm, 64 rows x q|gate|k|v (N=18432) x K=4096
+      gemm_gate_up    lollm_gemm with the SwiGLU epilogue, 64 rows x N=24576 x K=4096
+      gemm_down       lollm_gemm, 64 rows x N=4096 x K=12288
+      attn_step       lollm_attn_verify, B=16, T=4, 32 q / 4 kv heads, contexts U[2052, 2308]
+      spec_accept_c4  lollm_spec_accept, B=64, k=3, V=151936 with sampled drafts
+    Each GEMM rotates over enough weight copies (> 512 MB) that every launch streams its
+    weights from HBM, as a step that walks every layer does."""
     import torch
     from lollm_amd import ops
     Hk, Hv, D, K, S = 16, 32, 128, 4, 4
@@ -535,12 +547,41 @@ def pmc_probe(B=16, T=4, launches=20):
     for _ in range(launches):
         ops.gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, False,
                       B, T, Hk, Hv, D, K, 1e-6, out=out)
+    del rec, win
+    M = B * T
+    for N, Kd, epi in ((18432, 4096, ops.GEMM_NONE), (24576, 4096, ops.GEMM_SWIGLU),
+                       (4096, 12288, ops.GEMM_NONE)):
+        copies = max(2, -(-(512 << 20) // (N * Kd * 2)))
+        Wts = [ops.gemm_tile_weights((0.02 * torch.randn(N, Kd, device="cuda", generator=g)).bfloat16(), epi)
+               for _ in range(copies)]
+        x = torch.randn(M, Kd, device="cuda", generator=g).bfloat16()
+        for i in range(launches):
+            ops.gemm(x, Wts[i % copies], N, Kd, epi)
+        del Wts
+        torch.cuda.empty_cache()
+    kv_len = torch.randint(2052, 2309, (16,), generator=torch.Generator().manual_seed(3)).int().cuda()
+    q = torch.randn(16, 4, 32, 256, device="cuda", generator=g).bfloat16()
+    kc = torch.randn(16, 4, 2312, 256, device="cuda", generator=g).bfloat16()
+    vc = torch.randn(16, 4, 2312, 256, device="cuda", generator=g).bfloat16()
+    gate = torch.randn(16, 4, 32 * 256, device="cuda", generator=g).bfloat16()
+    for _ in range(launches):
+        ops.attn_verify(q, kc, vc, kv_len, gate)
+    del kc, vc
+    Bs, k, V = 64, 3, 151936
+    tgt = torch.randn(Bs, k + 1, V, device="cuda", generator=g) * 3
+    drf = (tgt[:, :k] + torch.randn(Bs, k, V, device="cuda", generator=g)).bfloat16()
+    tgt = tgt.bfloat16()
+    drafts = torch.stack([ops.sample_rows(drf[:, i].contiguous(), 0.7, 0, 0.95, 7, 0, slot=k + 1 + i)
+                          for i in range(k)], 1)
+    for _ in range(launches):
+        ops.spec_accept(tgt, drf, drafts, 0.7, 0, 0.95, 7, 0)
     x = torch.randn(PROBE_COPY_BYTES // 4, device="cuda", generator=g)
     y = torch.empty_like(x)
     for _ in range(5):
         torch.neg(x, out=y)
     torch.cuda.synchronize()
-    log(f"pmc probe: {launches} x gdn_layer B={B} T={T}, 5 x neg over {PROBE_COPY_BYTES} bytes")
+    log(f"pmc probe: {launches} launches each of {', '.join(PROBE_ORDER)}; "
+        f"5 x neg over {PROBE_COPY_BYTES} bytes")
 
 
 def measured_traffic(kernel, shape):

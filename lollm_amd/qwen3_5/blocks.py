@@ -22,30 +22,35 @@ def _cat_rows(*ws):
     return torch.cat([w.reshape(w.shape[0], -1) for w in ws], 0).contiguous()
 
 
-# Fixed GEMM path per projection shape, so a given (weights, inputs) gives the same bits in
-# every process (a timing-based choice could differ between runs and change rounding).
-# Rows <= 64 take lollm_gemm on one workgroup per CU, except the shapes listed here, which
-# measured faster on hipBLASLt at that row count with cold caches (weights streaming
-# from HBM, as in a step that walks every layer):
-#   (N, K, epilogue, rows) -> "blas"
-BLAS_SHAPES = {
-    (12352, 4096, 0, 64),      # GDN in_proj of the 4096-hidden model, verify pass
-}
+# Fixed GEMM path and grid per projection shape, so a given (weights, inputs) gives the
+# same bits in every process (a timing-based choice could differ between runs and
+# change rounding).  Rows <= 64 take lollm_gemm, rows > 64 (the prefill) hipBLASLt.
+# lollm_gemm deals 64-column groups x 128-k stages out to one workgroup per CU; when the
+# groups number between 3/4 of the CUs and the CUs, one workgroup per group instead
+# leaves no group cut between workgroups, so no merge launch follows (the GDN in_proj
+# of the 4096-hidden model, 193 groups: 25.0 us against 30.2 us on 256 workgroups and
+# 25.7 us on hipBLASLt, weights streaming from HBM).
 
 
 def gemm_path(N, K, epilogue, rows, tiled=True):
-    """'gemm' (lollm_gemm, one workgroup per CU) or 'blas' (hipBLASLt) for a projection
-    call; a pure function of the shape."""
-    if not tiled or rows > ops.GEMM_MAX_ROWS:
-        return "blas"
-    return "blas" if (N, K, epilogue, rows) in BLAS_SHAPES else "gemm"
+    """'gemm' (lollm_gemm) or 'blas' (hipBLASLt) for a projection call; a pure function
+    of the shape."""
+    return "gemm" if tiled and rows <= ops.GEMM_MAX_ROWS else "blas"
+
+
+def gemm_grid(N, cus):
+    """Workgroups of a lollm_gemm call with N output columns on a device with `cus`
+    CUs: one per 64-column group when that covers 3/4 of the CUs or more, else one per
+    CU."""
+    groups = N // 64
+    return groups if 4 * groups >= 3 * cus and groups <= cus else cus
 
 
 class Projection:
     """y = x W^T (blocks.py's nn.Linear layers, no bias).  Keeps the row-major weight
     for hipBLASLt (F.linear) and a tiled copy for lollm_gemm (<= 64 rows).
     epilogue=GEMM_SWIGLU: W = [gate; up], y = silu(x gate^T) * x up^T (blocks.py:341-342).
-    The path of each call is gemm_path() of its shape."""
+    The path of each call is gemm_path() of its shape, the grid gemm_grid()."""
 
     def __init__(self, weight, epilogue=ops.GEMM_NONE):
         self.weight = weight.to(torch.bfloat16).contiguous()
@@ -58,8 +63,11 @@ class Projection:
     def workspace_bytes(self, rows=ops.GEMM_MAX_ROWS):
         if self.tiled is None:
             return 0
-        return max(ops.gemm_workspace_bytes(rows, self.N, self.K),
+        return max(ops.gemm_workspace_bytes(rows, self.N, self.K, self.grid()),
                    ops.gemm_workspace_bytes(rows, self.N, self.K, _cus()))
+
+    def grid(self):
+        return gemm_grid(self.N, _cus())
 
     def path(self, rows):
         return gemm_path(self.N, self.K, self.epilogue, rows, self.tiled is not None)
@@ -76,7 +84,7 @@ class Projection:
         rows = x.numel() // self.K
         if self.path(rows) == "blas":
             return self._blas(x)
-        return ops.gemm(x, self.tiled, self.N, self.K, self.epilogue, grid=_cus())
+        return ops.gemm(x, self.tiled, self.N, self.K, self.epilogue, grid=self.grid())
 
     def add_norm(self, x, residual, norm):
         """The projection feeding the residual stream with the add and the next RMSNorm
@@ -85,7 +93,7 @@ class Projection:
         kernel) when the path is lollm_gemm and the shape fits it, else the projection
         followed by lollm_rmsnorm."""
         rows = x.numel() // self.K
-        g1 = _cus()
+        g1 = self.grid()
         if (self.path(rows) == "gemm" and self.epilogue == ops.GEMM_NONE
                 and ops.gemm_rmsnorm_supported(rows, self.N, self.K, g1)):
             return ops.gemm_rmsnorm(x, self.tiled, self.N, self.K, residual, norm.weight, norm.eps,
