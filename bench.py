@@ -38,20 +38,33 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_fn(fn, iters, warm=3):
-    """Average µs per call of fn() with HIP events on torch's current stream (every
-    lollm_amd kernel launches on that stream)."""
+def time_fn(fn, iters, warm=3, replays=5):
+    """Average µs per call of fn(): `iters` calls captured into one HIP graph, replayed
+    `replays` times between HIP events on torch's current stream (the stream the graph
+    replays on).  Launching from Python costs 10-30 µs per call, more than many of
+    these kernels take, so eager back-to-back calls would time the host instead."""
     import torch
-    for _ in range(warm):
-        fn()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(warm):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(iters):
-        fn()
+    for _ in range(replays):
+        graph.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1000.0 / iters
+    del graph
+    return e0.elapsed_time(e1) * 1000.0 / (iters * replays)
 
 
 # ------------------------------------------------------------------------------------
@@ -130,7 +143,8 @@ def projection_paths(model, mtp, B, k):
 
 
 def verify_breakdown(dec, iters=20):
-    """Eager timing of the step's parts (µs): draft chain, verify forward, acceptance."""
+    """The step's parts (µs), each replayed alone from a graph: draft chain, verify
+    forward, acceptance."""
     import torch
     from lollm_amd import ops
     B, k, model = dec.B, dec.k, dec.model

@@ -52,29 +52,39 @@ __device__ __forceinline__ void load_rows<float>(const float* p, float (&x)[GDN_
   }
 }
 
-template <typename T>
-__device__ __forceinline__ void load_cols4(const T* p, float (&x)[4]) {
+// NC consecutive value / output columns of one row (4 per lane in the verify scan)
+template <typename T, int NC>
+__device__ __forceinline__ void load_cols(const T* p, float (&x)[NC]) {
 #pragma unroll
-  for (int c = 0; c < 4; ++c) x[c] = Elt<T>::load(p + c);
+  for (int c = 0; c < NC; ++c) x[c] = Elt<T>::load(p + c);
 }
 
-template <typename T>
-__device__ __forceinline__ void store_cols4(T* p, const float (&x)[4]) {
+template <typename T, int NC>
+__device__ __forceinline__ void store_cols(T* p, const float (&x)[NC]) {
 #pragma unroll
-  for (int c = 0; c < 4; ++c) Elt<T>::store(p + c, x[c]);
+  for (int c = 0; c < NC; ++c) Elt<T>::store(p + c, x[c]);
 }
 
 template <>
-__device__ __forceinline__ void store_cols4<uint16_t>(uint16_t* p, const float (&x)[4]) {
+__device__ __forceinline__ void store_cols<uint16_t, 4>(uint16_t* p, const float (&x)[4]) {
   uint2 w;
   w.x = (uint32_t)f32_to_bf16(x[0]) | ((uint32_t)f32_to_bf16(x[1]) << 16);
   w.y = (uint32_t)f32_to_bf16(x[2]) | ((uint32_t)f32_to_bf16(x[3]) << 16);
   *reinterpret_cast<uint2*>(p) = w;
 }
 
-template <>
-__device__ __forceinline__ void store_cols4<float>(float* p, const float (&x)[4]) {
-  *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+// One lane's 4 state floats of a row: plain loads (the state is read once), streaming
+// stores (a snapshot is read back at most once, by a later launch; sending it straight
+// to HBM spares the end-of-launch write-back of dirty L2 lines)
+__device__ __forceinline__ void load_state(const float* p, float (&x)[4]) {
+  const float4 f = *reinterpret_cast<const float4*>(p);
+  x[0] = f.x; x[1] = f.y; x[2] = f.z; x[3] = f.w;
+}
+
+__device__ __forceinline__ void store_state(float* p, const float (&x)[4]) {
+  const u32x4_t w = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                     __float_as_uint(x[3])};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(p));
 }
 
 template <typename T, bool L2>
@@ -92,39 +102,45 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(
   const int hk = h / (Hv / Hk);
   const int row0 = rg * GDN_ROWS;
   const int col0 = wave * 32 + cg * 4;
+  constexpr int NC = 4;  // state columns per lane
   constexpr size_t SS = (size_t)GDN_DK * GDN_DV;
 
-  float S[GDN_ROWS][4];
+  float S[GDN_ROWS][NC];
   if (state != nullptr) {
     int slot = state_slot ? state_slot[b] : 0;
     slot = slot < 0 ? 0 : (slot >= state_slots ? state_slots - 1 : slot);  // never out of range
     const float* s0 = state + ((size_t)(b * state_slots + slot) * Hv + h) * SS;
 #pragma unroll
-    for (int r = 0; r < GDN_ROWS; ++r) {
-      float4 f = *reinterpret_cast<const float4*>(s0 + (size_t)(row0 + r) * GDN_DV + col0);
-      S[r][0] = f.x; S[r][1] = f.y; S[r][2] = f.z; S[r][3] = f.w;
-    }
+    for (int r = 0; r < GDN_ROWS; ++r) load_state(s0 + (size_t)(row0 + r) * GDN_DV + col0, S[r]);
   } else {
 #pragma unroll
-    for (int r = 0; r < GDN_ROWS; ++r) S[r][0] = S[r][1] = S[r][2] = S[r][3] = 0.f;
+    for (int r = 0; r < GDN_ROWS; ++r)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) S[r][c] = 0.f;
   }
 
   // inputs of position t
   auto qk_ptr = [&](const T* base, int t) {
     return base + (((size_t)b * T_len + t) * Hk + hk) * GDN_DK + row0;
   };
+  auto gi_of = [&](int t) { return ((size_t)b * T_len + t) * Hv + h; };
   float kr[GDN_ROWS], qr[GDN_ROWS];
   load_rows<T>(qk_ptr(k, 0), kr);
   load_rows<T>(qk_ptr(q, 0), qr);
+  // g, beta and this lane's value columns are loaded one position ahead with k and q,
+  // so no wait for them covers the previous position's snapshot stores (the memory
+  // counter retires in issue order, stores included)
+  float graw = g[gi_of(0)], braw = Elt<T>::load(beta + gi_of(0)), vv[NC];
+  load_cols<T, NC>(v + gi_of(0) * GDN_DV + col0, vv);
 
   // partial dot products of the current state with k_t, q_t (this lane's rows)
-  float pa[4], pb[4], pkq = 0.f, pkk = 0.f, pqq = 0.f;
+  float pa[NC], pb[NC], pkq = 0.f, pkk = 0.f, pqq = 0.f;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) pa[c] = pb[c] = 0.f;
+  for (int c = 0; c < NC; ++c) pa[c] = pb[c] = 0.f;
 #pragma unroll
   for (int r = 0; r < GDN_ROWS; ++r) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < NC; ++c) {
       pa[c] = fmaf(S[r][c], kr[r], pa[c]);
       pb[c] = fmaf(S[r][c], qr[r], pb[c]);
     }
@@ -136,24 +152,27 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(
   }
 
   for (int t = 0; t < T_len; ++t) {
-    // prefetch the next position's k, q while this one is reduced
-    float kn[GDN_ROWS], qn[GDN_ROWS];
+    // prefetch the next position's k, q, g, beta, v while this one is reduced
+    float kn[GDN_ROWS], qn[GDN_ROWS], gn = 0.f, bn = 0.f, vn[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) vn[c] = 0.f;
     const bool has_next = t + 1 < T_len;
     if (has_next) {
       load_rows<T>(qk_ptr(k, t + 1), kn);
       load_rows<T>(qk_ptr(q, t + 1), qn);
+      gn = g[gi_of(t + 1)];
+      bn = Elt<T>::load(beta + gi_of(t + 1));
+      load_cols<T, NC>(v + gi_of(t + 1) * GDN_DV + col0, vn);
     }
-    const size_t gi = ((size_t)b * T_len + t) * Hv + h;
-    const float gam = __expf(g[gi]);
-    const float bet = Elt<T>::load(beta + gi);
-    float vv[4];
-    load_cols4<T>(v + gi * GDN_DV + col0, vv);
+    const size_t gi = gi_of(t);
+    const float gam = __expf(graw);
+    const float bet = braw;
 
     // reduce over the 8 row groups (lanes differing in bits 3..5)
 #pragma unroll
     for (int m = 8; m < 64; m <<= 1) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < NC; ++c) {
         pa[c] += wave_xor(pa[c], m);
         pb[c] += wave_xor(pb[c], m);
       }
@@ -166,30 +185,28 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(
     const float rk = L2 ? rsqrtf(pkk + 1e-6f) : 1.f;
     const float rq = (L2 ? rsqrtf(pqq + 1e-6f) : 1.f) * q_scale;
     const float kq = pkq * rk * rq;
-    float d[4], o[4];
+    float d[NC], o[NC];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < NC; ++c) {
       d[c] = (vv[c] - gam * pa[c] * rk) * bet;
       o[c] = gam * pb[c] * rq + d[c] * kq;
     }
-    if (rg == 0) store_cols4<T>(out + gi * GDN_DV + col0, o);
+    if (rg == 0) store_cols<T, NC>(out + gi * GDN_DV + col0, o);
 
     // one pass: decay + rank-1 update, snapshot, next position's partial dots
     float* snap = snapshots ? snapshots + (((size_t)b * T_len + t) * Hv + h) * SS : nullptr;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) pa[c] = pb[c] = 0.f;
+    for (int c = 0; c < NC; ++c) pa[c] = pb[c] = 0.f;
     pkq = pkk = pqq = 0.f;
 #pragma unroll
     for (int r = 0; r < GDN_ROWS; ++r) {
       const float kk_r = kr[r] * rk;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) S[r][c] = fmaf(kk_r, d[c], gam * S[r][c]);
-      if (snap)
-        *reinterpret_cast<float4*>(snap + (size_t)(row0 + r) * GDN_DV + col0) =
-            make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
+      for (int c = 0; c < NC; ++c) S[r][c] = fmaf(kk_r, d[c], gam * S[r][c]);
+      if (snap) store_state(snap + (size_t)(row0 + r) * GDN_DV + col0, S[r]);
       if (has_next) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < NC; ++c) {
           pa[c] = fmaf(S[r][c], kn[r], pa[c]);
           pb[c] = fmaf(S[r][c], qn[r], pb[c]);
         }
@@ -203,15 +220,17 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(
     if (has_next) {
 #pragma unroll
       for (int r = 0; r < GDN_ROWS; ++r) { kr[r] = kn[r]; qr[r] = qn[r]; }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) vv[c] = vn[c];
+      graw = gn;
+      braw = bn;
     }
   }
 
   if (final_state) {
     float* sf = final_state + ((size_t)b * Hv + h) * SS;
 #pragma unroll
-    for (int r = 0; r < GDN_ROWS; ++r)
-      *reinterpret_cast<float4*>(sf + (size_t)(row0 + r) * GDN_DV + col0) =
-          make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
+    for (int r = 0; r < GDN_ROWS; ++r) store_state(sf + (size_t)(row0 + r) * GDN_DV + col0, S[r]);
   }
 }
 

@@ -47,7 +47,9 @@ def to_dev(*ts):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("B,T,Hk,Hv", [(1, 1, 2, 4), (3, 2, 2, 4), (2, 5, 16, 32), (1, 3, 4, 4)])
+# the last two shapes are the isolated workload's head counts at B = 8 and 16
+@pytest.mark.parametrize("B,T,Hk,Hv", [(1, 1, 2, 4), (3, 2, 2, 4), (2, 5, 16, 32), (1, 3, 4, 4),
+                                       (8, 2, 16, 32), (16, 3, 16, 32)])
 @pytest.mark.parametrize("l2", [False, True])
 def test_gdn_verify_matches_oracle(dtype, B, T, Hk, Hv, l2):
     from lollm_amd import ops
@@ -61,6 +63,27 @@ def test_gdn_verify_matches_oracle(dtype, B, T, Hk, Hv, l2):
     torch.testing.assert_close(out.cpu().float(), o_ref.float(), **tol)
     torch.testing.assert_close(snaps.cpu(), snaps_ref, **tol)
     torch.testing.assert_close(fin.cpu(), snaps_ref[:, -1], **tol)
+
+
+def test_gdn_batch_invariant_bits():
+    """The same (sequence, head) computed alone and inside batches of 8 and 16 gives
+    identical bits: a workgroup's sums never depend on the batch around it."""
+    from lollm_amd import ops
+    T, Hk, Hv = 3, 16, 32
+    q, k, v, g, beta, s0 = make_inputs(1, T, Hk, Hv, seed=31, dtype=torch.bfloat16)
+    res = []
+    for B in (1, 8, 16):
+        print(f"batch-invariance case B={B}", flush=True)
+        rep = lambda t: t.expand(B, *t.shape[1:]).contiguous()
+        out, snaps, fin = ops.gdn_verify(*to_dev(*(rep(t) for t in (q, k, v, g, beta, s0))),
+                                         snapshots=True, final_state=True)
+        torch.cuda.synchronize()
+        res.append((out[:1].cpu(), snaps[:1].cpu(), fin[:1].cpu()))
+        assert torch.equal(out[0].cpu(), out[-1].cpu())
+    for r in res[1:]:
+        for a, b in zip(res[0], r):
+            assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a.view(torch.int32),
+                               b.view(torch.int16) if b.dtype == torch.bfloat16 else b.view(torch.int32))
 
 
 def test_gdn_zero_initial_state():
