@@ -351,7 +351,7 @@ def isolated_sampler(cpu=False):
     tgt = tgt.bfloat16()
     drafts = torch.stack([ops.sample_rows(drf[:, i].contiguous(), 0.7, 0, 0.95, 7, 0, slot=k + 1 + i)
                           for i in range(k)], 1)
-    ws = torch.empty(ops._lib.lib().lollm_spec_workspace_bytes(B, k, V, 1), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(ops._lib.lib().lollm_spec_workspace_bytes(B, k, 1), dtype=torch.uint8, device="cuda")
     na = torch.empty(B, dtype=torch.int32, device="cuda")
     nt = torch.empty(B, dtype=torch.int32, device="cuda")
     us = time_fn(lambda: ops.spec_accept(tgt, drf, drafts, 0.7, 0, 0.95, 7, 0, workspace=ws,

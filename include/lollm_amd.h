@@ -108,11 +108,10 @@ int lollm_attn_verify(const void* q, const void* k_cache, const void* v_cache,
  *   seed, offset     Philox4x32-10 key and step counter; offset_dev, if not NULL, is a
  *            device pointer the offset is read from instead (for captured graphs)
  *   n_accepted (B) int32 in 0..k; next_token (B) int32
- *   workspace  lollm_spec_workspace_bytes(B, k, V, draft != NULL) bytes: the row
- *            statistics and each target row's kept set (V / 8 bytes per row)
+ *   workspace  lollm_spec_workspace_bytes(B, k, draft != NULL) bytes
  * Outputs are bit-exact to the integer specification in oracle/sampler_ref.c.
  * Supported: V % 8 == 0, T <= 1000, k <= 64. */
-long long lollm_spec_workspace_bytes(int B, int k, int V, int with_draft);
+long long lollm_spec_workspace_bytes(int B, int k, int with_draft);
 int lollm_spec_accept(const void* target, const void* draft, const int32_t* drafts, int B, int k,
                       int V, float inv_temperature, int top_k, float top_p, uint64_t seed,
                       uint64_t offset, const uint64_t* offset_dev, int32_t* n_accepted,
@@ -124,10 +123,10 @@ int lollm_spec_accept(const void* target, const void* draft, const int32_t* draf
  * hipMalloc.  No counterpart in the reference.  The workspace is a fixed array inside the
  * library, LOLLM_SPEC_SCRATCH_BYTES on each device it runs on, held until the process
  * ends; a shape whose lollm_spec_workspace_bytes exceeds it returns LOLLM_EUNSUPPORTED
- * (8 MiB covers, e.g., B = 64 with k = 4 over a 151936-token vocabulary).  Every call on one device
+ * (1 MiB covers, e.g., B = 256 with k = 8 and sampled drafts).  Every call on one device
  * uses that device's array: calls that overlap in time on one device race.  Same
  * arguments, results and errors as lollm_spec_accept otherwise. */
-#define LOLLM_SPEC_SCRATCH_BYTES (1 << 23)
+#define LOLLM_SPEC_SCRATCH_BYTES (1 << 20)
 int lollm_spec_accept_noalloc(const void* target, const void* draft, const int32_t* drafts, int B,
                               int k, int V, float inv_temperature, int top_k, float top_p,
                               uint64_t seed, uint64_t offset, const uint64_t* offset_dev,

@@ -32,7 +32,7 @@ SIGNATURES = {
     "lollm_attn_workspace_bytes": ([_I, _I, _I, _I, _I, _I, _I], ctypes.c_longlong),
     "lollm_attn_verify": ([_P, _P, _P, _P, _P, _P, _P, ctypes.c_longlong, _I, _I, _I, _I, _I,
                            _I, ctypes.c_longlong, ctypes.c_longlong, _I, _F, _P], _I),
-    "lollm_spec_workspace_bytes": ([_I, _I, _I, _I], ctypes.c_longlong),
+    "lollm_spec_workspace_bytes": ([_I, _I, _I], ctypes.c_longlong),
     "lollm_spec_accept": ([_P, _P, _P, _I, _I, _I, _F, _I, _F, _U64, _U64, _P, _P, _P, _P,
                            ctypes.c_longlong, _P], _I),
     "lollm_spec_accept_noalloc": ([_P, _P, _P, _I, _I, _I, _F, _I, _F, _U64, _U64, _P, _P, _P,

@@ -31,10 +31,10 @@
 //                top-k / top-p cut points and the kept mass Z;
 //   argmax_*     greedy rows: the row split over 16 workgroups, partial maxima
 //                merged by a second tiny kernel (a greedy row needs no histogram);
-//   spec_draw    one workgroup per sequence: the k accept tests in parallel, then the
-//                residual or bonus draw over the kept set of the target row it uses
-//                (row_stats records every target row's kept set as a bitmap; every draw
-//                distribution vanishes outside it);
+//   spec_partial / spec_final  the k accept tests in parallel, then the residual or
+//                bonus draw in two passes: ns workgroups per sequence sum the draw's
+//                weights over ns contiguous vocabulary slices, then one workgroup per
+//                sequence locates the slice holding the target and the token in it;
 //   sample_rows  one draw per row.
 // A draw is an inverse CDF over token ids in three steps: every wave of the block sums
 // the weights of its own contiguous sixteenth of the range (coalesced, exact integers,
@@ -313,23 +313,6 @@ __device__ __forceinline__ void scan_chunk(uint4 u, int c, uint64_t& best, int32
   }
 }
 
-// Bytes between kept-set bitmap rows: V / 8 rounded up to 16.
-__host__ __device__ __forceinline__ int kept_stride(int V) { return ((V >> 3) + 15) & ~15; }
-
-// Kept-set bits of the 8 tokens of a chunk: bit e set iff token e's distance below the
-// maximum key is within the cut.
-__device__ __forceinline__ uint32_t keep_bits(uint4 u, uint32_t km2, int32_t cut) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-  uint32_t bits = 0;
-#pragma unroll
-  for (int h = 0; h < 4; ++h) {
-    const uint32_t dd = dist_pair(w[h], km2);
-    bits |= (uint32_t)((int32_t)(dd & 0xFFFFu) <= cut) << (2 * h);
-    bits |= (uint32_t)((int32_t)(dd >> 16) <= cut) << (2 * h + 1);
-  }
-  return bits;
-}
-
 // Counts of the 8 tokens of a chunk by distance below the maximum key; only distances
 // <= dlim (< SP_NBINS) are counted.
 __device__ __forceinline__ void hist_chunk(uint4 u, uint32_t km2, int32_t dlim, uint32_t* hist) {
@@ -345,15 +328,11 @@ __device__ __forceinline__ void hist_chunk(uint4 u, uint32_t km2, int32_t dlim, 
 
 // Sampled rows only (inv_temp > 0); greedy rows take the split argmax below.  Rows
 // [0, rows0) are read from x0, the rest from x1 (target and draft rows in one launch).
-// With keep non-null, rows [0, rows0) also record their kept set (the tokens within the
-// final cut) as a bitmap: bit e of byte c of row r (rows kept_stride(V) bytes apart) is
-// token 8 c + e.
 __global__ __launch_bounds__(SP_THREADS) void row_stats_kernel(const uint16_t* __restrict__ x0,
                                                                int rows0,
                                                                const uint16_t* __restrict__ x1,
                                                                int V, float inv_temp, int top_k,
-                                                               float top_p, RowStat* stats,
-                                                               uint8_t* __restrict__ keep) {
+                                                               float top_p, RowStat* stats) {
   __shared__ uint32_t hist[SP_NBINS];
   __shared__ uint64_t s64[16];
   __shared__ int32_t shared_cut;
@@ -499,17 +478,6 @@ __global__ __launch_bounds__(SP_THREADS) void row_stats_kernel(const uint16_t* _
     st.Z = z_sh;
   }
   if (tid == 0) stats[row] = st;
-  if (keep && row < rows0) {
-    // the row is still in registers (the tail past them is read again)
-    uint8_t* kb = keep + (size_t)row * kept_stride(V);
-#pragma unroll
-    for (int i = 0; i < SP_REG; ++i) {
-      const int ch = i * SP_THREADS + tid;
-      if (ch < nch) kb[ch] = keep_bits(reg[i], km2, st.cut);
-    }
-    for (int ch = SP_REG * SP_THREADS + tid; ch < nch; ch += SP_THREADS)
-      kb[ch] = keep_bits(x4[ch], km2, st.cut);
-  }
 }
 
 // Greedy rows: 16 workgroups per row each reduce a slice to a packed
@@ -677,8 +645,10 @@ __device__ int32_t draw_refine(int lo, int hi, LD ld, WT wt, Acc* wtot, Acc targ
   return draw_find<Acc>(lo1, hi1, ld, wt, wtot, target - before, V, found);
 }
 
-// chunks in flight per lane in the totals passes
-constexpr int SP_UN64 = 4;
+struct ChunkPair { u32x4_t p, q; };   // vector members: copies stay in registers
+
+// chunks in flight per lane in the totals passes (64-bit and 128-bit masses)
+constexpr int SP_UN64 = 4, SP_UN128 = 2;
 
 __device__ __forceinline__ u128 scaled_target(uint32_t U, u128 M) {
   return (u128)U * (M >> 24) + (((u128)U * (uint64_t)(M & 0xFFFFFFu)) >> 24);
@@ -750,204 +720,114 @@ __device__ AcceptPlan accept_plan(const uint16_t* target, const uint16_t* draft,
   return pl;
 }
 
-// The draw of sequence b's emitted token, one workgroup per sequence, over the kept set
-// of target row a (pl.a) that row_stats recorded: every distribution a draw can use --
-// p of row a, the residual max(0, p - q) (zero wherever p is), p again when the residual
-// is empty -- vanishes outside that set, so the inverse CDF over token ids needs only its
-// tokens.  Thread t owns bitmap bytes [t per, (t + 1) per) (tokens in id order across
-// threads), sums its tokens' weights (loading only the 16-byte chunks that hold kept
-// tokens), a block scan places the target in one thread's range, and that thread walks
-// its tokens again to find it.  Every mass is an exact integer, so the token is the one
-// the full-vocabulary inverse CDF gives.
-// One pass over the kept tokens of bitmap bytes [c0, c1) (c0 a multiple of 4), in id
-// order: 32 bitmap bytes are read at once, then the 16-byte chunks of up to four
-// non-zero bytes are loaded together before their tokens are weighed, so a thread waits
-// on memory once per four chunks that hold kept tokens.  Returns run plus the weights;
-// with find, stops at the first token where that running sum exceeds target (*hit).
-// Weights of a draw at token t, from the bf16 bits pb of row a of the target (and qb of
-// the draft row): p of row a; the residual max(0, p Zq - q Zp) with sampled q; the
-// residual p - [t == d] Zp with q one-hot at d.  Tokens outside p's cut weigh 0.
-struct DrawP {
-  RowStat sp; const uint64_t* tab;
-  template <typename Acc> __device__ Acc weight(uint32_t pb, uint32_t, int) const {
-    const int32_t d = sp.kmax - skey(pb);
-    return (Acc)(d <= sp.cut ? tab[d] : 0);
-  }
-};
-struct DrawResidualQ {
-  RowStat sp, sq; const uint64_t* tp; const uint64_t* tq;
-  template <typename Acc> __device__ Acc weight(uint32_t pb, uint32_t qb, int t) const {
-    const int32_t dp = sp.kmax - skey(pb);
-    const uint64_t wp = dp <= sp.cut ? tp[dp] : 0;
-    if (wp == 0) return 0;
-    uint64_t wq;
-    if (sq.greedy) {
-      wq = t == sq.argmax ? 1u : 0u;
-    } else {
-      const int32_t dq = sq.kmax - skey(qb);
-      wq = dq <= sq.cut ? tq[dq] : 0;
-    }
-    const u128 l = (u128)wp * sq.Z, r = (u128)wq * sp.Z;
-    return l > r ? (Acc)(l - r) : (Acc)0;
-  }
-};
-struct DrawResidualOneHot {
-  RowStat sp; const uint64_t* tab; int d;
-  template <typename Acc> __device__ Acc weight(uint32_t pb, uint32_t, int t) const {
-    const int32_t dp = sp.kmax - skey(pb);
-    const uint64_t wp = dp <= sp.cut ? tab[dp] : 0;
-    const uint64_t r = t == d ? sp.Z : 0;
-    return (Acc)(wp > r ? wp - r : 0);
-  }
-};
-
-// The kept set of a target row, in id order, a round of SP_KLIST tokens at a time.
-// Thread t owns bitmap bytes [t per, (t + 1) per) (per a multiple of 4), so the tokens
-// of consecutive threads are consecutive in id order; a block scan of the threads'
-// counts places each thread's tokens in the kept set, and a round writes the tokens at
-// positions [r SP_KLIST, (r + 1) SP_KLIST) to the LDS list.
-constexpr int SP_KLIST = 7168;
-struct KeptSet {
-  const uint8_t* kb; int kstride, c0, c1;
-  int first;   // this thread's first position in the kept set
-  int n;       // this thread's kept tokens
-  int total;   // kept tokens of the row
-};
-
-__device__ __forceinline__ uint32_t kept_word(const KeptSet& K, int cb) {
-  const uint32_t v = reinterpret_cast<const uint32_t*>(K.kb)[min(cb, K.kstride - 4) >> 2];
-  const int left = K.c1 - cb;
-  return left >= 4 ? v : (left <= 0 ? 0u : v & ((1u << (8 * left)) - 1u));
-}
-
-__device__ KeptSet kept_set(const uint8_t* kb, int nch, int kstride, int* iscratch) {
-  KeptSet K;
-  K.kb = kb;
-  K.kstride = kstride;
-  const int per = ((nch + (int)blockDim.x - 1) / (int)blockDim.x + 3) & ~3;
-  K.c0 = min(nch, (int)threadIdx.x * per);
-  K.c1 = min(nch, K.c0 + per);
-  int n = 0;
-  for (int wb = K.c0; wb < K.c1; wb += 32) {
-    uint32_t w[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = kept_word(K, wb + 4 * i);   // loads in flight together
-#pragma unroll
-    for (int i = 0; i < 8; ++i) n += __popc(w[i]);
-  }
-  int total;
-  const int incl = block_inclusive_scan<int>(n, iscratch, &total);
-  K.first = incl - n;
-  K.n = n;
-  K.total = total;
-  return K;
-}
-
-// Round r of the kept set into list[0, min(SP_KLIST, total - r SP_KLIST)); returns its size.
-__device__ int kept_round(const KeptSet& K, int r, int32_t* list) {
-  const int lo = r * SP_KLIST, hi = min(K.total, lo + SP_KLIST);
-  if (K.n > 0 && K.first < hi && K.first + K.n > lo) {
-    int pos = K.first;
-    for (int wb = K.c0; wb < K.c1 && pos < hi; wb += 4) {
-      uint32_t w = kept_word(K, wb);
-      while (w) {
-        const int bit = __ffs(w) - 1;
-        w &= w - 1;
-        if (pos >= lo && pos < hi) list[pos - lo] = 8 * wb + bit;   // byte bit / 8, bit e
-        ++pos;
-      }
-    }
-  }
-  __syncthreads();
-  return hi - lo;
-}
-
-// The draw over the kept set with weights wf (target_of(total) gives the target mass);
-// returns the token, or -1 when the total is zero (*total_out tells which).  Thread t
-// weighs list entries [t e, (t + 1) e) of each round (their bf16 loads in flight
-// together), a block scan places the target, and the thread holding it walks its entries.
-template <typename Acc, typename WF, typename TG>
-__device__ int32_t kept_draw(const KeptSet& K, int32_t* list, const uint16_t* xp, const uint16_t* xq,
-                             WF wf, TG target_of, Acc* scratch, int32_t* found, Acc* total_out) {
-  constexpr int E = 8;   // entries a thread weighs per step
-  const int rounds = (K.total + SP_KLIST - 1) / SP_KLIST;
-  auto entries = [&](int m, int& e0, int& e1) {
-    const int per = (m + (int)blockDim.x - 1) / (int)blockDim.x;
-    e0 = min(m, (int)threadIdx.x * per);
-    e1 = min(m, e0 + per);
-  };
-  auto weigh = [&](int e0, int e1, Acc base, bool find, Acc tgt, int32_t* hit) {
-    Acc run = base;
-    for (int eb = e0; eb < e1; eb += E) {
-      uint32_t pb[E], qb[E];
-      int tk[E];
-#pragma unroll
-      for (int j = 0; j < E; ++j) {
-        tk[j] = list[min(eb + j, e1 - 1)];
-        pb[j] = xp[tk[j]];
-        qb[j] = xq[tk[j]];
-      }
-#pragma unroll
-      for (int j = 0; j < E; ++j) {
-        if (eb + j >= e1) break;
-        run += wf.template weight<Acc>(pb[j], qb[j], tk[j]);
-        if (find && run > tgt) { *hit = tk[j]; return run; }
-      }
-    }
-    return run;
-  };
-  // pass 1: the total
-  Acc R = 0;
-  int m = 0;
-  for (int r = 0; r < rounds; ++r) {
-    if (rounds > 1 || r == 0) m = kept_round(K, r, list);
-    int e0, e1;
-    entries(m, e0, e1);
-    Acc t;
-    block_inclusive_scan<Acc>(weigh(e0, e1, (Acc)0, false, (Acc)0, nullptr), scratch, &t);
-    R += t;
-  }
-  *total_out = R;
-  if (R == 0) return -1;
-  const Acc tgt = target_of(R);
-  // pass 2: the round and the entry holding the target (the list is still round 0's
-  // when there is one round)
-  if (threadIdx.x == 0) *found = -1;
-  Acc base = 0;
-  for (int r = 0; r < rounds; ++r) {
-    if (rounds > 1) m = kept_round(K, r, list);
-    int e0, e1;
-    entries(m, e0, e1);
-    const Acc mine = weigh(e0, e1, (Acc)0, false, (Acc)0, nullptr);
-    Acc t;
-    const Acc incl = block_inclusive_scan<Acc>(mine, scratch, &t) + base;
-    const Acc before = incl - mine;
-    if (before <= tgt && incl > tgt) {
-      int32_t hit = -1;
-      weigh(e0, e1, before, true, tgt, &hit);
-      *found = hit;
-    }
-    base += t;
+// Runs f(ld, wt, acc_tag) with the chunk loader and weight function of the plan's draw
+// (tables filled and visible on return from the setup).
+template <typename F>
+__device__ void with_draw(const AcceptPlan& pl, const uint16_t* target, const uint16_t* draft,
+                          int k, int V, float c, const RowStat* st_t, const RowStat* st_d, int b,
+                          uint64_t* tab_p, uint64_t* tab_q, F f) {
+  const RowStat sp = st_t[b * (k + 1) + pl.a];
+  const uint16_t* xp = target + ((size_t)b * (k + 1) + pl.a) * V;
+  const u32x4_t* vp = reinterpret_cast<const u32x4_t*>(xp);
+  build_table(sp, c, tab_p);
+  if (pl.kind == 1) {
+    // q a sampled distribution: residual wp Zq - wq Zp in 128 bits
+    const RowStat sq = st_d[b * k + pl.a];
+    const u32x4_t* vq = reinterpret_cast<const u32x4_t*>(draft + ((size_t)b * k + pl.a) * V);
+    const uint64_t Zq = sq.Z;
+    build_table(sq, c, tab_q);
     __syncthreads();
-    if (*found >= 0) break;
+    auto ld = [=](int ch) { return ChunkPair{vp[ch], vq[ch]}; };
+    auto wt = [=](const ChunkPair& r, int ch, u128* w) {
+      const uint32_t pw[4] = {r.p.x, r.p.y, r.p.z, r.p.w}, qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        uint64_t wp[2], wq[2];
+        pair_weights(sp, tab_p, pw[h], ch * 8 + 2 * h, wp[0], wp[1]);
+        pair_weights(sq, tab_q, qw[h], ch * 8 + 2 * h, wq[0], wq[1]);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          u128 v = 0;
+          if (wp[e] != 0) {   // most tokens lie past p's cut: skip the 128-bit products
+            const u128 l = (u128)wp[e] * Zq, rr = (u128)wq[e] * sp.Z;
+            v = l > rr ? l - rr : (u128)0;
+          }
+          w[2 * h + e] = v;
+        }
+      }
+    };
+    f(ld, wt, (u128)0);
+  } else if (pl.kind == 2) {
+    // q one-hot at d: residual wp - [t == d] Zp fits 64 bits
+    __syncthreads();
+    const int d = pl.d;
+    auto ld = [=](int ch) { return vp[ch]; };
+    auto wt = [=](const u32x4_t& up, int ch, uint64_t* w) {
+      uint64_t wp[8];
+      chunk_weights(sp, tab_p, up, ch, wp);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint64_t r = ch * 8 + e == d ? sp.Z : 0;
+        w[e] = wp[e] > r ? wp[e] - r : 0;
+      }
+    };
+    f(ld, wt, (uint64_t)0);
+  } else {
+    // the bonus: p of row k itself
+    __syncthreads();
+    auto ld = [=](int ch) { return vp[ch]; };
+    auto wt = [=](const u32x4_t& u, int ch, uint64_t* w) { chunk_weights(sp, tab_p, u, ch, w); };
+    f(ld, wt, (uint64_t)0);
   }
-  return *found;
 }
 
-// One workgroup per sequence: the accept tests, then the draw of the emitted token.
-__global__ __launch_bounds__(SP_THREADS) void spec_draw_kernel(
+__device__ __forceinline__ void split_range(int nch, int ns, int s, int& lo, int& hi) {
+  const int per = (nch + ns - 1) / ns;
+  lo = min(nch, s * per);
+  hi = min(nch, lo + per);
+}
+
+// Pass 1, grid (ns, B): workgroup (s, b) sums the draw's weights over the s-th of ns
+// contiguous slices of the vocabulary (exact integers, u128 in part[b ns + s]).
+__global__ __launch_bounds__(SP_THREADS) void spec_partial_kernel(
     const uint16_t* __restrict__ target, const uint16_t* __restrict__ draft,
     const int32_t* __restrict__ drafts, int k, int V, float inv_temp, uint64_t seed,
     uint64_t offset_arg, const uint64_t* __restrict__ offset_dev, const RowStat* __restrict__ st_t,
-    const RowStat* __restrict__ st_d, const uint8_t* __restrict__ keep,
+    const RowStat* __restrict__ st_d, int ns, u128* __restrict__ part) {
+  __shared__ u128 wt128[SP_THREADS / 64];
+  __shared__ uint64_t wt64[SP_THREADS / 64];
+  __shared__ int32_t ok[64];
+  extern __shared__ uint64_t sp_tabs[];   // p's table, then q's when drafts are sampled
+  uint64_t* tab_p = sp_tabs;
+  uint64_t* tab_q = sp_tabs + SP_NBINS;
+  const int s = blockIdx.x, b = blockIdx.y;
+  const uint64_t offset = offset_dev ? *offset_dev : offset_arg;
+  const float c = inv_temp * 1.44269504088896341f;
+  const AcceptPlan pl = accept_plan(target, draft, drafts, k, V, c, seed, offset, st_t, st_d, b, ok);
+  int lo, hi;
+  split_range(V >> 3, ns, s, lo, hi);
+  with_draw(pl, target, draft, k, V, c, st_t, st_d, b, tab_p, tab_q, [&](auto ld, auto wt, auto tag) {
+    using Acc = decltype(tag);
+    Acc* wtot;
+    if constexpr (sizeof(Acc) == 16) wtot = wt128; else wtot = wt64;
+    const Acc tot = draw_totals<Acc, sizeof(Acc) == 16 ? SP_UN128 : SP_UN64>(lo, hi, ld, wt, wtot);
+    if (threadIdx.x == 0) part[(size_t)b * ns + s] = (u128)tot;
+  });
+}
+
+// Pass 2, grid (B): the slice holding the target, then the token inside it (the slice
+// summed by the 16 waves, the owning sixteenth summed again, its owning sixteenth walked).
+__global__ __launch_bounds__(SP_THREADS) void spec_final_kernel(
+    const uint16_t* __restrict__ target, const uint16_t* __restrict__ draft,
+    const int32_t* __restrict__ drafts, int k, int V, float inv_temp, uint64_t seed,
+    uint64_t offset_arg, const uint64_t* __restrict__ offset_dev, const RowStat* __restrict__ st_t,
+    const RowStat* __restrict__ st_d, int ns, const u128* __restrict__ part,
     int32_t* __restrict__ n_accepted, int32_t* __restrict__ next_token) {
-  __shared__ u128 s128[SP_THREADS / 64];
-  __shared__ uint64_t s64[SP_THREADS / 64];
-  __shared__ int si[SP_THREADS / 64];
+  __shared__ u128 wt128[SP_THREADS / 64];
+  __shared__ uint64_t wt64[SP_THREADS / 64];
   __shared__ int32_t found;
   __shared__ int32_t ok[64];
-  __shared__ int32_t list[SP_KLIST];
-  extern __shared__ uint64_t sp_tabs[];   // p's table, then q's when drafts are sampled
+  extern __shared__ uint64_t sp_tabs[];
   uint64_t* tab_p = sp_tabs;
   uint64_t* tab_q = sp_tabs + SP_NBINS;
   const int b = blockIdx.x;
@@ -955,46 +835,37 @@ __global__ __launch_bounds__(SP_THREADS) void spec_draw_kernel(
   const float c = inv_temp * 1.44269504088896341f;
   const AcceptPlan pl = accept_plan(target, draft, drafts, k, V, c, seed, offset, st_t, st_d, b, ok);
   const RowStat sp = st_t[b * (k + 1) + pl.a];
-  const uint16_t* xp = target + ((size_t)b * (k + 1) + pl.a) * V;
-  const int ks = kept_stride(V);
-  int32_t tok = -1;
-  if (sp.greedy) {
-    // p one-hot: the bonus is its argmax, and so is every residual draw (max(0, p - q) is
-    // zero or one-hot there) and the fallback to p
+  const int nch = V >> 3;
+  u128 R = 0;
+  for (int s = 0; s < ns; ++s) R += part[(size_t)b * ns + s];
+  int32_t tok;
+  if (sp.greedy && pl.kind == 0) {
     tok = sp.argmax;
-  } else {
-    const KeptSet K = kept_set(keep + ((size_t)b * (k + 1) + pl.a) * ks, V >> 3, ks, si);
+  } else if (pl.kind != 0 && R == 0) {
+    // the residual is empty: draw from p itself (whole row, this workgroup)
     build_table(sp, c, tab_p);
-    const DrawP fp{sp, tab_p};
-    auto bonus = [&](uint64_t) { return (uint64_t)(((u128)pl.U * sp.Z) >> 24); };
-    if (pl.kind == 1) {
-      const RowStat sq = st_d[b * k + pl.a];
-      build_table(sq, c, tab_q);
-      __syncthreads();
-      const uint16_t* xq = draft + ((size_t)b * k + pl.a) * V;
-      u128 R;
-      tok = kept_draw<u128>(K, list, xp, xq, DrawResidualQ{sp, sq, tab_p, tab_q},
-                            [&](u128 t) { return scaled_target(pl.U, t); }, s128, &found, &R);
-      if (R == 0) {   // the residual is empty: draw from p itself
-        uint64_t Z;
-        tok = kept_draw<uint64_t>(K, list, xp, xp, fp, bonus, s64, &found, &Z);
-      }
-    } else if (pl.kind == 2) {
-      __syncthreads();
-      uint64_t R;
-      tok = kept_draw<uint64_t>(K, list, xp, xp, DrawResidualOneHot{sp, tab_p, pl.d},
-                                [&](uint64_t t) { return (uint64_t)scaled_target(pl.U, (u128)t); },
-                                s64, &found, &R);
-      if (R == 0) {
-        uint64_t Z;
-        tok = kept_draw<uint64_t>(K, list, xp, xp, fp, bonus, s64, &found, &Z);
-      }
-    } else {
-      __syncthreads();
-      uint64_t Z;
-      tok = kept_draw<uint64_t>(K, list, xp, xp, fp, bonus, s64, &found, &Z);
+    tok = draw_plain<false>(target + ((size_t)b * (k + 1) + pl.a) * V, sp, tab_p, pl.U, V, wt64, &found);
+  } else {
+    // target: floor(U Z / 2^24) for the bonus (Z = the kept mass of p), U R scaled for
+    // a residual; then the slice whose running total passes it
+    const u128 tgt = pl.kind == 0 ? (u128)(((u128)pl.U * sp.Z) >> 24) : scaled_target(pl.U, R);
+    u128 before = 0;
+    int s_hit = ns - 1;
+    for (int s = 0; s < ns; ++s) {
+      const u128 v = part[(size_t)b * ns + s];
+      if (before + v > tgt) { s_hit = s; break; }
+      before += v;
     }
-    if (tok < 0) tok = V - 1;
+    int lo, hi;
+    split_range(nch, ns, s_hit, lo, hi);
+    with_draw(pl, target, draft, k, V, c, st_t, st_d, b, tab_p, tab_q, [&](auto ld, auto wt, auto tag) {
+      using Acc = decltype(tag);
+      constexpr int UN = sizeof(Acc) == 16 ? SP_UN128 : SP_UN64;
+      Acc* wtot;
+      if constexpr (sizeof(Acc) == 16) wtot = wt128; else wtot = wt64;
+      draw_totals<Acc, UN>(lo, hi, ld, wt, wtot);
+      tok = draw_find<Acc>(lo, hi, ld, wt, wtot, (Acc)(tgt - before), V, &found);
+    });
   }
   if (threadIdx.x == 0) {
     n_accepted[b] = pl.a;
@@ -1095,10 +966,10 @@ static bool sampler_args_ok(int V, float top_p, float inv_temp) {
 // argmax (partials at `part`).
 static int launch_row_stats(const uint16_t* x0, int rows0, const uint16_t* x1, int rows1, int V,
                             float inv_temp, int top_k, float top_p, RowStat* st, uint64_t* part,
-                            uint8_t* keep, hipStream_t s) {
+                            hipStream_t s) {
   if (inv_temp > 0.0f) {
     hipLaunchKernelGGL(row_stats_kernel, dim3(rows0 + rows1), dim3(SP_THREADS), 0, s, x0, rows0,
-                       x1, V, inv_temp, top_k, top_p, st, keep);
+                       x1, V, inv_temp, top_k, top_p, st);
     return launch_status();
   }
   const uint16_t* xs[2] = {x0, x1};
@@ -1123,16 +994,16 @@ static long long stats_bytes(long long rows) {
   return rows * (long long)(sizeof(RowStat) + SP_NSPLIT * sizeof(uint64_t));
 }
 
-// Workspace of lollm_spec_accept: the row statistics (and greedy partials), then the
-// kept-set bitmaps of the B (k + 1) target rows (kept_stride(V) bytes each).
-static long long accept_keep_offset(int B, int k, int with_draft) {
+constexpr int SP_MAXSLICE = 16;   // vocabulary slices of the acceptance draw
+
+static long long accept_part_offset(int B, int k, int with_draft) {
   const long long st = stats_bytes((long long)B * (k + 1) + (with_draft ? (long long)B * k : 0));
-  return (st + 255) / 256 * 256;
+  return (st + 15) / 16 * 16;
 }
 
-LOLLM_API long long lollm_spec_workspace_bytes(int B, int k, int V, int with_draft) {
-  if (B <= 0 || k < 0 || V <= 0 || V % 8) return -1;
-  return accept_keep_offset(B, k, with_draft) + (long long)B * (k + 1) * kept_stride(V);
+LOLLM_API long long lollm_spec_workspace_bytes(int B, int k, int with_draft) {
+  if (B <= 0 || k < 0) return -1;
+  return accept_part_offset(B, k, with_draft) + (long long)B * SP_MAXSLICE * (long long)sizeof(u128);
 }
 
 LOLLM_API long long lollm_sample_workspace_bytes(int rows) {
@@ -1149,31 +1020,41 @@ LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int
   if (k > 0 && !drafts) return LOLLM_EINVAL;
   if (k > 64) return LOLLM_EUNSUPPORTED;
   if (!sampler_args_ok(V, top_p, inv_temperature)) return LOLLM_EUNSUPPORTED;
-  if (workspace_bytes < lollm_spec_workspace_bytes(B, k, V, draft != nullptr)) return LOLLM_EINVAL;
+  if (workspace_bytes < lollm_spec_workspace_bytes(B, k, draft != nullptr)) return LOLLM_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   const int rt = B * (k + 1), rd = draft ? B * k : 0;
   RowStat* st_t = (RowStat*)workspace;
   RowStat* st_d = st_t + rt;
   uint64_t* part = (uint64_t*)(st_d + rd);
-  uint8_t* keep = (uint8_t*)workspace + accept_keep_offset(B, k, draft != nullptr);
   int rc = launch_row_stats((const uint16_t*)target, rt, (const uint16_t*)draft, k > 0 ? rd : 0, V,
-                            inv_temperature, top_k, top_p, st_t, part, keep, st);
+                            inv_temperature, top_k, top_p, st_t, part, st);
   if (rc) return rc;
-  // the draw: one workgroup per sequence over its kept set
+  // the draw: B x ns workgroups sum the draw's weights over ns vocabulary slices (one
+  // round of workgroups: one 1024-thread workgroup fits a CU), then one workgroup per
+  // sequence finds the slice and the token in it
+  const int ns = std::max(1, std::min(SP_MAXSLICE, 256 / B));
+  u128* apart = (u128*)((char*)workspace + accept_part_offset(B, k, draft != nullptr));
   const size_t tabs = (draft ? 2 : 1) * SP_NBINS * sizeof(uint64_t);
   static bool lds_set[64] = {};   // per device: the attribute is set on the current device
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return LOLLM_EUNSUPPORTED;
   if (!lds_set[dev]) {
-    const hipError_t e = hipFuncSetAttribute((const void*)spec_draw_kernel,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             2 * SP_NBINS * (int)sizeof(uint64_t));
+    const int mx = 2 * SP_NBINS * (int)sizeof(uint64_t);
+    hipError_t e = hipFuncSetAttribute((const void*)spec_partial_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, mx);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)spec_final_kernel,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, mx);
     if (e != hipSuccess) return LOLLM_EHIP_BASE + (int)e;
     lds_set[dev] = true;
   }
-  hipLaunchKernelGGL(spec_draw_kernel, dim3(B), dim3(SP_THREADS), tabs, st, (const uint16_t*)target,
+  hipLaunchKernelGGL(spec_partial_kernel, dim3(ns, B), dim3(SP_THREADS), tabs, st,
+                     (const uint16_t*)target, (const uint16_t*)draft, drafts, k, V, inv_temperature,
+                     seed, offset, offset_dev, st_t, draft ? st_d : nullptr, ns, apart);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(spec_final_kernel, dim3(B), dim3(SP_THREADS), tabs, st, (const uint16_t*)target,
                      (const uint16_t*)draft, drafts, k, V, inv_temperature, seed, offset, offset_dev,
-                     st_t, draft ? st_d : nullptr, (const uint8_t*)keep, n_accepted, next_token);
+                     st_t, draft ? st_d : nullptr, ns, (const u128*)apart, n_accepted, next_token);
   return launch_status();
 }
 
@@ -1209,7 +1090,7 @@ LOLLM_API int lollm_spec_accept_noalloc(const void* target, const void* draft,
                                         float inv_temperature, int top_k, float top_p,
                                         uint64_t seed, uint64_t offset, const uint64_t* offset_dev,
                                         int32_t* n_accepted, int32_t* next_token, void* stream) {
-  const long long need = lollm_spec_workspace_bytes(B, k, V, draft != nullptr);
+  const long long need = lollm_spec_workspace_bytes(B, k, draft != nullptr);
   if (need < 0) return LOLLM_EINVAL;
   if (need > (long long)LOLLM_SPEC_SCRATCH_BYTES) return LOLLM_EUNSUPPORTED;
   void* ws = nullptr;
@@ -1240,7 +1121,7 @@ LOLLM_API int lollm_sample_rows(const void* logits, int rows, int V, float inv_t
     return launch_status();
   }
   int rc = launch_row_stats((const uint16_t*)logits, rows, nullptr, 0, V, inv_temperature, top_k,
-                            top_p, stats, part, nullptr, st);
+                            top_p, stats, part, st);
   if (rc) return rc;
   hipLaunchKernelGGL(sample_rows_kernel, dim3(rows), dim3(SP_THREADS), 0, st,
                      (const uint16_t*)logits, V, inv_temperature, seed, offset, offset_dev, row_base,

@@ -338,7 +338,7 @@ def spec_accept(target, draft, drafts, temperature, top_k=0, top_p=1.0, seed=0, 
     _need(drafts, "drafts", torch.int32, (B, k))
     if offset_dev is not None:
         _need(offset_dev, "offset_dev", torch.int64, (1,))
-    need = _lib.lib().lollm_spec_workspace_bytes(B, k, V, int(draft is not None))
+    need = _lib.lib().lollm_spec_workspace_bytes(B, k, int(draft is not None))
     if workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=target.device)
     _need(workspace, "workspace")

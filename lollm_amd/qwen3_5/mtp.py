@@ -168,7 +168,7 @@ class SpecDecoder:
         self.offset = torch.zeros(1, dtype=torch.int64, device=dev)
         self.accept_hist = torch.zeros(k + 1, **i32)       # accepted-length histogram
         self.seen = (ops.new_seen(batch, cfg.vocab_size, dev) if self.penalty != 1.0 else None)
-        self.spec_ws = torch.empty(max(ops._lib.lib().lollm_spec_workspace_bytes(batch, k, cfg.vocab_size, 1), 16),
+        self.spec_ws = torch.empty(max(ops._lib.lib().lollm_spec_workspace_bytes(batch, k, 1), 16),
                                    dtype=torch.uint8, device=dev)
         self.row_ws = torch.empty(ops.sample_workspace_bytes(batch), dtype=torch.uint8, device=dev)
         self.mtp_ws = model.attn_workspace(batch, 1, max(k, 1))
