@@ -169,15 +169,19 @@ def verify_breakdown(dec, iters=20):
 # ------------------------------------------------------------------------------------
 # the dominant hand-written kernel of the verify step: the fused GDN layer
 # ------------------------------------------------------------------------------------
-def gdn_layer_bytes(cfg, B, T):
-    """Algorithmic HBM bytes of one lollm_gdn_layer launch: read the committed state
-    once (B Hv Dk Dv fp32), write T snapshots, read the projections (B T P bf16) and
-    the conv window (K-1 rows), write the window (K-1+T rows) and the output (B T Hv Dv)."""
+def gdn_layer_bytes(cfg, B, T, replayed=None):
+    """Algorithmic HBM bytes of one short lollm_gdn_layer launch: read the committed
+    half's state (B Hv Dk Dv fp32) and the records it replays (`replayed` positions over
+    the batch, default B T; 4 Dk + 16 bytes per head), write the committed state to the
+    other half and the T new records, read the projections (B T P bf16) and the conv
+    window (K-1 rows), write the window (K-1+T rows) and the output (B T Hv Dv)."""
     D, Hv = cfg.linear_key_head_dim, cfg.linear_num_value_heads
     P = cfg.conv_dim + cfg.value_dim + 2 * Hv
     K = cfg.linear_conv_kernel_dim
     state = B * Hv * D * D * 4
-    return (state * (1 + T) + B * T * P * 2 + B * (K - 1) * cfg.conv_dim * 2
+    rec = Hv * (4 * D + 16)
+    replayed = B * T if replayed is None else replayed
+    return (2 * state + (replayed + B * T) * rec + B * T * P * 2 + B * (K - 1) * cfg.conv_dim * 2
             + B * (K - 1 + T) * cfg.conv_dim * 2 + B * T * cfg.value_dim * 2)
 
 
@@ -196,12 +200,12 @@ def gdn_layer_roofline(model, dec, iters=50):
 
     def launch():
         ops.gdn_layer(proj, gdn.conv_w, gdn.A_log, gdn.dt_bias, gdn.norm_w, s["win"],
-                      dec.cache.conv_off, s["rec"], dec.cache.rec_slot, False, B, T,
-                      cfg.linear_num_key_heads, cfg.linear_num_value_heads,
-                      cfg.linear_key_head_dim, cfg.linear_conv_kernel_dim, cfg.rms_norm_eps,
-                      out=out)
-    us = time_fn(launch, iters)
-    byt = gdn_layer_bytes(cfg, B, T)
+                      dec.cache.conv_off, s["rec"], dec.cache.rec_half, s["rep"],
+                      dec.cache.replay, False, B, T, cfg.linear_num_key_heads,
+                      cfg.linear_num_value_heads, cfg.linear_key_head_dim,
+                      cfg.linear_conv_kernel_dim, cfg.rms_norm_eps, out=out)
+    us = time_fn(launch, iters)   # each launch replays the decode's committed records
+    byt = gdn_layer_bytes(cfg, B, T, int(dec.cache.replay.clamp(0, dec.cache.spec_slots).sum()))
     gbs = byt / us / 1e3
     return {"kernel": "lollm::gdn_layer_verify_kernel", "shape": f"B={B} T={T} Hv=32 Hk=16 D=128",
             "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -275,11 +279,13 @@ def isolated_gdn_prefill(B=16, T=2048):
     dt_bias = torch.randn(Hv, device="cuda", generator=g) * 0.5
     norm_w = (1 + 0.1 * torch.randn(D, device="cuda", generator=g)).bfloat16()
     win = torch.zeros(B, 2 * (K - 1 + S), C, device="cuda").bfloat16()
-    rec = torch.zeros(B, 2 * S, Hv, D, D, device="cuda")
+    rec = torch.zeros(B, 2, Hv, D, D, device="cuda")
+    rep = torch.zeros(B, 2, Hv, S, ops.gdn_record_bytes(D), dtype=torch.uint8, device="cuda")
     zero = torch.zeros(B, dtype=torch.int32, device="cuda")
     out = torch.empty(B, T, Hv * D, dtype=torch.bfloat16, device="cuda")
     us = time_fn(lambda: ops.gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, zero, rec, zero,
-                                       True, B, T, Hk, Hv, D, K, 1e-6, out=out, chunked=True), 5)
+                                       rep, zero, True, B, T, Hk, Hv, D, K, 1e-6, out=out,
+                                       chunked=True), 5)
     C64 = 64
     per_chunk = 2 * (2 * C64 * C64 * D + 2 * C64 * D * C64 + 2 * C64 * D * D + C64 * D * C64 + D * D * C64)
     flops = B * Hv * (-(-T // C64)) * per_chunk
@@ -554,14 +560,16 @@ def pmc_probe(B=16, T=4, launches=20):
     dt_bias = torch.randn(Hv, device="cuda", generator=g) * 0.5
     norm_w = torch.ones(D, device="cuda").bfloat16()
     win = torch.zeros(B, 2 * W, C, device="cuda").bfloat16()
-    rec = 0.02 * torch.randn(B, 2 * S, Hv, D, D, device="cuda", generator=g)
+    rec = 0.02 * torch.randn(B, 2, Hv, D, D, device="cuda", generator=g)
+    rep = torch.zeros(B, 2, Hv, S, ops.gdn_record_bytes(D), dtype=torch.uint8, device="cuda")
     conv_off = torch.zeros(B, dtype=torch.int32, device="cuda")
-    rec_slot = torch.zeros(B, dtype=torch.int32, device="cuda")
+    rec_half = torch.zeros(B, dtype=torch.int32, device="cuda")
+    replay = torch.full((B,), T, dtype=torch.int32, device="cuda")   # replays T records
     out = torch.empty(B, T, Hv * D, dtype=torch.bfloat16, device="cuda")
     for _ in range(launches):
-        ops.gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, False,
-                      B, T, Hk, Hv, D, K, 1e-6, out=out)
-    del rec, win
+        ops.gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_half, rep,
+                      replay, False, B, T, Hk, Hv, D, K, 1e-6, out=out)
+    del rec, rep, win
     M = B * T
     for N, Kd, epi in ((18432, 4096, ops.GEMM_NONE), (24576, 4096, ops.GEMM_SWIGLU),
                        (4096, 12288, ops.GEMM_NONE)):

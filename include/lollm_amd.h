@@ -260,10 +260,14 @@ int lollm_gemm_rmsnorm(const void* A, long long lda, const void* Wt, int M, int 
  *             writes the other half (base h = 0 or win_rows): if conv_kernel - 1 + T
  *             <= win_rows the whole window [state | raw x_0..x_{T-1}] at rows h.. (state
  *             after c committed tokens = rows h + c ..), else the final state at rows h..
- *   rec       (B, 2 * slots, Hv, Dk, Dv) fp32, two snapshot halves: the committed state
- *             is slot rec_slot[b] (ignored when fresh: zero state); the call writes the
- *             other half (base s = 0 or slots): the state after position t in slot s + t
- *             if T <= slots, else the final state in slot s
+ *   rec       (B, 2, Hv, Dk, Dv) fp32 and rep (B, 2, Hv, slots, 4 Dk + 16) bytes: two
+ *             halves of recurrent state + replay records.  The committed state is half
+ *             rec_half[b]'s state with its first replay[b] records applied (ignored when
+ *             fresh: zero state).  The call writes only the other half: if T <= slots,
+ *             the committed state and the records of its T positions (k and v after the
+ *             conv as bf16, then fp32 exp(g), beta, 1/|k|), so the state after position t
+ *             is that half with replay = t + 1; else (long call) the final state, with
+ *             replay = 0.  The committed half is never written.
  *   out       (B, T, Hv*Dv) bf16
  * Replaces: GatedDeltaNet._conv, the gating, torch_chunk_gated_delta_rule /
  * torch_recurrent_gated_delta_rule and RMSNormGated (blocks.py:38-51,59-144,268-329),
@@ -271,9 +275,18 @@ int lollm_gemm_rmsnorm(const void* A, long long lda, const void* Wt, int M, int 
  * Supported: Dk == Dv == 128, conv_kernel <= 4. */
 int lollm_gdn_layer(const void* proj, long long proj_stride, const void* conv_w,
                     const float* A_log, const float* dt_bias, const void* norm_w, void* win,
-                    const int32_t* conv_off, int win_rows, float* rec, const int32_t* rec_slot,
-                    int slots, int fresh, void* out, int B, int T, int Hk, int Hv, int Dk, int Dv,
-                    int conv_kernel, float eps, void* stream);
+                    const int32_t* conv_off, int win_rows, float* rec, const int32_t* rec_half,
+                    void* rep, const int32_t* replay, int slots, int fresh, void* out, int B, int T,
+                    int Hk, int Hv, int Dk, int Dv, int conv_kernel, float eps, void* stream);
+
+/* The committed recurrent state of every (sequence, head) of one GDN layer -- half
+ * rec_half[b] of rec with its first replay[b] records of rep applied, as lollm_gdn_layer
+ * lays them out -- into out (B, Hv, Dk, Dv) fp32; with out == NULL, into the other half
+ * of rec instead (after which rec_half[b] ^= 1, replay[b] = 0 names the same state with
+ * no records).  Replaces reading and replacing the recurrent state of the cache
+ * (src/qwen3_5/kv.py:39-44). */
+int lollm_gdn_state(float* rec, const int32_t* rec_half, const void* rep, const int32_t* replay,
+                    int slots, int B, int Hv, int Dk, int Dv, float* out, void* stream);
 
 /* The same layer for long calls (prefill) with the delta rule in its chunked parallel
  * form: torch_chunk_gated_delta_rule (src/qwen3_5/blocks.py:59-113), which the reference
@@ -283,20 +296,21 @@ int lollm_gdn_layer(const void* proj, long long proj_stride, const void* conv_w,
  * off-diagonal blocks on fp32 MFMA; the L2 norm of q and k (blocks.py:124-127) is
  * applied as fp32 scales, as the recurrent kernels do.  Same
  * arguments and the same long-call placement as lollm_gdn_layer: the final state in
- * slot 0 of the half not holding rec_slot[b], the final K-1 raw inputs in rows 0 .. K-2
+ * the half not holding rec_half[b], the final K-1 raw inputs in rows 0 .. K-2
  * of the window half not holding conv_off[b].  Supported: conv_kernel 4, T > slots,
  * K - 1 + T > win_rows (the call does not fit a window half), else LOLLM_EUNSUPPORTED. */
 int lollm_gdn_layer_chunked(const void* proj, long long proj_stride, const void* conv_w,
                             const float* A_log, const float* dt_bias, const void* norm_w,
                             void* win, const int32_t* conv_off, int win_rows, float* rec,
-                            const int32_t* rec_slot, int slots, int fresh, void* out, int B, int T,
-                            int Hk, int Hv, int Dk, int Dv, int conv_kernel, float eps,
-                            void* stream);
+                            const int32_t* rec_half, void* rep, const int32_t* replay, int slots,
+                            int fresh, void* out, int B, int T, int Hk, int Hv, int Dk, int Dv,
+                            int conv_kernel, float eps, void* stream);
 
 /* End of one speculative step, per sequence b with a = n_accepted[b] (of T - 1
- * drafts): keep a + 1 of the T verified positions (lengths += a + 1, GDN snapshot
- * slot = written half + a, conv window offset = written half + a + 1, with the halves
- * of lollm_gdn_layer: slots / win_rows) -- the O(1) form of the snapshot/restore
+ * drafts): keep a + 1 of the T verified positions (lengths += a + 1, GDN state half =
+ * the written half with replay = a + 1 records, conv window offset = written half + a
+ * + 1, with the halves of lollm_gdn_layer: slots / win_rows) -- the O(1) form of the
+ * snapshot/restore
  * of src/qwen3_5/mtp.py:141,156-162), append verify_ids[b, 0..a] to out_tokens (cap
  * columns) at out_count[b], copy hidden[b, a] (B, T, H) to h_last (B, H) (the MTP
  * input, mtp.py:155,162), set pending = next_token, increment *offset (the
@@ -308,8 +322,8 @@ int lollm_gdn_layer_chunked(const void* proj, long long proj_stride, const void*
  * no sync.  The caller guarantees out_count[b] + T <= out_cap and lengths[b] + T <= the
  * cache length before each step (the Python host keeps upper bounds and raises first). */
 int lollm_spec_commit(const int32_t* verify_ids, const int32_t* n_accepted,
-                      const int32_t* next_token, int32_t* lengths, int32_t* rec_slot,
-                      int32_t* conv_off, int32_t* pending, int32_t* out_tokens, int32_t* out_count,
+                      const int32_t* next_token, int32_t* lengths, int32_t* rec_half,
+                      int32_t* replay, int32_t* conv_off, int32_t* pending, int32_t* out_tokens, int32_t* out_count,
                       int out_cap, const void* hidden, void* h_last, int B, int T, int H,
                       int slots, int win_rows, long long* offset, int32_t* accept_hist,
                       uint32_t* seen, int seen_words, void* stream);

@@ -52,18 +52,19 @@ SIGNATURES = {
                           _P], _I),
     "lollm_attn_prologue": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P,
                              _I, _P], _I),
-    "lollm_gdn_layer": ([_P, ctypes.c_longlong, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P,
-                         _I, _I, _I, _I, _I, _I, _I, _F, _P], _I),
-    "lollm_gdn_layer_chunked": ([_P, ctypes.c_longlong, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I,
-                                 _I, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P], _I),
+    "lollm_gdn_layer": ([_P, ctypes.c_longlong, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I,
+                         _I, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P], _I),
+    "lollm_gdn_layer_chunked": ([_P, ctypes.c_longlong, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P,
+                                 _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P], _I),
+    "lollm_gdn_state": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P], _I),
     "lollm_gemm_tile_weights": ([_P, _P, _I, _I, _I, _P], _I),
     "lollm_gemm_workspace_bytes": ([_I, _I, _I, _I], ctypes.c_longlong),
     "lollm_gemm": ([_P, ctypes.c_longlong, _P, _P, ctypes.c_longlong, _I, _I, _I, _I, _P,
                     ctypes.c_longlong, _I, _P], _I),
     "lollm_gemm_rmsnorm": ([_P, ctypes.c_longlong, _P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P,
                             ctypes.c_longlong, _I, _P], _I),
-    "lollm_spec_commit": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P,
-                           _P, _P, _I, _P], _I),
+    "lollm_spec_commit": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I,
+                           _P, _P, _P, _I, _P], _I),
     "lollm_repetition_penalty": ([_P, ctypes.c_longlong, _I, _I, _I, _P, _I, _P, _I, _I, _F, _P],
                                  _I),
     "lollm_seen_mark": ([_P, _I, _I, _P, ctypes.c_longlong, _I, _I, _P], _I),

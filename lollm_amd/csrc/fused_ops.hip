@@ -311,7 +311,8 @@ __global__ __launch_bounds__(256) void attn_small_kernel(
 // One workgroup per sequence: the bookkeeping that ends a speculative step.
 __global__ __launch_bounds__(256) void spec_commit_kernel(
     const int32_t* __restrict__ verify_ids, const int32_t* __restrict__ n_acc,
-    const int32_t* __restrict__ next_tok, int32_t* lengths, int32_t* rec_slot, int32_t* conv_off,
+    const int32_t* __restrict__ next_tok, int32_t* lengths, int32_t* rec_half, int32_t* replay,
+    int32_t* conv_off,
     int32_t* pending, int32_t* out_tokens, int32_t* out_count, int cap,
     const uint16_t* __restrict__ hidden, uint16_t* __restrict__ h_last, int H, int T, int S,
     int W, long long* offset, int* hist, uint32_t* seen, int words) {
@@ -323,7 +324,8 @@ __global__ __launch_bounds__(256) void spec_commit_kernel(
   for (int i = threadIdx.x; i < H / 8; i += 256) dst[i] = src[i];
   if (threadIdx.x == 0) {
     lengths[b] += a + 1;                           // keep a + 1 of the T positions
-    rec_slot[b] = (rec_slot[b] >= S ? 0 : S) + a;  // the half the forward wrote
+    rec_half[b] = (rec_half[b] & 1) ^ 1;            // the half the forward wrote,
+    replay[b] = a + 1;                              // whose first a + 1 records are kept
     conv_off[b] = (conv_off[b] >= W ? 0 : W) + a + 1;
     const int c = out_count[b];
     for (int i = 0; i <= a; ++i)
@@ -420,20 +422,20 @@ LOLLM_API int lollm_attn_small(const void* qkv, const void* q_norm_w, const void
 }
 
 LOLLM_API int lollm_spec_commit(const int32_t* verify_ids, const int32_t* n_accepted,
-                                const int32_t* next_token, int32_t* lengths, int32_t* rec_slot,
-                                int32_t* conv_off, int32_t* pending, int32_t* out_tokens,
+                                const int32_t* next_token, int32_t* lengths, int32_t* rec_half,
+                                int32_t* replay, int32_t* conv_off, int32_t* pending, int32_t* out_tokens,
                                 int32_t* out_count, int out_cap, const void* hidden, void* h_last,
                                 int B, int T, int H, int slots, int win_rows, long long* offset,
                                 int32_t* accept_hist, uint32_t* seen, int seen_words,
                                 void* stream) {
-  if (!verify_ids || !n_accepted || !next_token || !lengths || !rec_slot || !conv_off ||
+  if (!verify_ids || !n_accepted || !next_token || !lengths || !rec_half || !replay || !conv_off ||
       !pending || !out_tokens || !out_count || !hidden || !h_last || !offset)
     return LOLLM_EINVAL;
   if (B <= 0 || T <= 0 || H <= 0 || out_cap <= 0 || slots < T || win_rows <= 0) return LOLLM_EINVAL;
   if (H % 8) return LOLLM_EUNSUPPORTED;
   if (seen && seen_words <= 0) return LOLLM_EINVAL;
   hipLaunchKernelGGL(spec_commit_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, verify_ids,
-                     n_accepted, next_token, lengths, rec_slot, conv_off, pending, out_tokens,
+                     n_accepted, next_token, lengths, rec_half, replay, conv_off, pending, out_tokens,
                      out_count, out_cap, (const uint16_t*)hidden, (uint16_t*)h_last, H, T, slots,
                      win_rows, offset, accept_hist, seen, seen_words);
   return launch_status();

@@ -4,8 +4,9 @@
 // RMSNorm (:38-51,324) -- with the delta rule in its parallel
 // chunked form (torch_chunk_gated_delta_rule, blocks.py:59-113, which the reference
 // runs for every T > 1 call, :316-322), and the same conv-window / state placement as
-// the long-call path of gdn_layer.hip (final state in slot 0 of the half being
-// written, final K-1 raw inputs in rows 0 .. K-2 of the window half being written).
+// the long-call path of gdn_layer.hip (starts from the committed state that the long-call
+// prologue wrote to the state half being written, leaves the final state there and the
+// final K-1 raw inputs in rows 0 .. K-2 of the window half being written).
 //
 // One 256-thread workgroup per (sequence b, v-head h) walks the chunks of 64 tokens in
 // order.  Per chunk, with gc = cumsum(g) and s = Dk^-0.5:
@@ -198,9 +199,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
   int off = a.conv_off[b];
   off = off < 0 ? 0 : (off > 2 * a.W - Km1 ? 2 * a.W - Km1 : off);
   const int wbase = off >= a.W ? 0 : a.W;
-  int slot = a.rec_slot[b];
-  slot = slot < 0 ? 0 : (slot >= 2 * a.S ? 2 * a.S - 1 : slot);
-  const int rbase = slot >= a.S ? 0 : a.S;
+  // the state half written by this call: it already holds the committed state (the
+  // long-call prologue rebuilt it there) and receives the final state
+  float* st_io = a.rec + ((size_t)(b * 2 + ((a.rec_half[b] & 1) ^ 1)) * a.Hv + h) * SS;
   const size_t win_b = (size_t)b * 2 * a.W;
   const float qscale = rsqrtf((float)GL_DK);
   const float a_log = a.A_log[h], dtb = a.dt_bias[h];
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
   // ---- initial state: this wave's 32 value columns, accumulator layout ----
   gc_f32x4 st[8][2];
   {
-    const float* s0 = a.rec + ((size_t)(b * 2 * a.S + slot) * a.Hv + h) * SS;
+    const float* s0 = st_io;
     const float keep = a.fresh ? 0.f : 1.f;   // a fresh sequence starts from S = 0
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb)
@@ -743,9 +744,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnLayerArgs a) {
                                   part * 8) = make_uint4(od[0], od[1], od[2], od[3]);
     }
   }
-  // ---- final state in slot 0 of the written half; final K-1 raw inputs in the window ----
+  // ---- final state in the written half; final K-1 raw inputs in the window ----
   {
-    float* sf = a.rec + ((size_t)(b * 2 * a.S + rbase) * a.Hv + h) * SS;
+    float* sf = st_io;
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb)
 #pragma unroll
@@ -770,11 +771,11 @@ using namespace lollm;
 LOLLM_API int lollm_gdn_layer_chunked(const void* proj, long long proj_stride, const void* conv_w,
                                       const float* A_log, const float* dt_bias, const void* norm_w,
                                       void* win, const int32_t* conv_off, int win_rows, float* rec,
-                                      const int32_t* rec_slot, int slots, int fresh, void* out,
-                                      int B, int T, int Hk, int Hv, int Dk, int Dv, int conv_kernel,
-                                      float eps, void* stream) {
+                                      const int32_t* rec_half, void* rep, const int32_t* replay,
+                                      int slots, int fresh, void* out, int B, int T, int Hk, int Hv,
+                                      int Dk, int Dv, int conv_kernel, float eps, void* stream) {
   if (!proj || !conv_w || !A_log || !dt_bias || !norm_w || !win || !conv_off || !rec ||
-      !rec_slot || !out)
+      !rec_half || !rep || !replay || !out)
     return LOLLM_EINVAL;
   if (B <= 0 || T <= 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return LOLLM_EINVAL;
   if (Dk != GL_DK || Dv != GL_DK || conv_kernel != 4) return LOLLM_EUNSUPPORTED;
@@ -788,10 +789,13 @@ LOLLM_API int lollm_gdn_layer_chunked(const void* proj, long long proj_stride, c
   GdnLayerArgs a;
   a.proj = (const uint16_t*)proj; a.conv_w = (const uint16_t*)conv_w; a.A_log = A_log;
   a.dt_bias = dt_bias; a.norm_w = (const uint16_t*)norm_w; a.win = (uint16_t*)win;
-  a.conv_off = conv_off; a.rec = rec; a.rec_slot = rec_slot; a.out = (uint16_t*)out;
+  a.conv_off = conv_off; a.rec = rec; a.rec_half = rec_half; a.rep = (uint8_t*)rep;
+  a.replay = replay; a.out = (uint16_t*)out;
   a.P = proj_stride; a.T = T; a.Hk = Hk; a.Hv = Hv; a.C = C; a.key_dim = key_dim;
   a.value_dim = value_dim; a.K = conv_kernel; a.W = win_rows; a.S = slots; a.fresh = fresh ? 1 : 0;
   a.eps = eps;
+  const int rc = gdn_long_call_prologue(a, B, (hipStream_t)stream);
+  if (rc != LOLLM_OK) return rc;
   hipLaunchKernelGGL(gdn_chunk_kernel, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);
   return launch_status();
 }

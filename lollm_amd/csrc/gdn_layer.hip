@@ -11,20 +11,25 @@
 //   3. the recurrent delta rule with in-kernel L2 norm of q, k and q scaled by
 //      Dk^-0.5 (blocks.py:116-144), the 128 x 128 fp32 state held in registers exactly
 //      as in gdn_verify.hip (wave = 32-column slab, lane = 16 rows x 4 columns);
-//      the state after every position can be written as a snapshot (O(1) rollback);
 //   4. the gated RMSNorm per v-head (blocks.py:38-51,324) and the bf16 output row.
 // State lives in ping-pong buffers selected per sequence on the device: the conv
-// window buffer has two halves of W rows and the recurrent-state buffer two halves of
-// S snapshot slots; a call reads the half holding the committed state (conv_off[b],
-// rec_slot[b]) and writes the other one, so rolling back to `a` accepted drafts is
-// just new indices (other half + a) and no host-side state changes between steps.
+// window buffer has two halves of W rows, the recurrent state two halves, each with a
+// replay record of up to S positions.  A call reads the half holding the committed
+// state (conv_off[b], rec_half[b]) and writes the other one.  A short call (T <= S,
+// verify / decode) first rebuilds the committed state -- the half's state plus its
+// first replay[b] records -- writes it to the other half, runs its T positions and
+// records them there instead of storing T states; accepting `a` drafts then only sets
+// new indices (other half, replay = a + 1) and no host-side state changes between
+// steps.  Nothing in the committed half is written, so a call that is not committed
+// can simply be run again.
 #include "gdn_common.h"
 
 namespace lollm {
 
-// SNAP: the call writes a snapshot per position (T <= S: verify / decode); otherwise
-// it is a long call (prefill) that writes only the final state.
-template <bool SNAP>
+// SHORT: T <= S, the call rebuilds the committed state and records its positions
+// (verify / decode); otherwise it is a long call (prefill) that starts from the state in
+// the written half (lollm_gdn_layer rebuilds it there first) and stores its final state.
+template <bool SHORT>
 __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
   __shared__ float xin[GL_KMAX - 1 + GL_TC][GL_CH];  // conv inputs (state rows first)
   __shared__ float act[GL_TC][GL_CH];                // q | k | v after conv + SiLU
@@ -38,14 +43,17 @@ __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
   const int row0 = rg * 16, col0 = wave * 32 + cg * 4;
   const int Km1 = a.K - 1;
   const bool full_window = Km1 + a.T <= a.W;
-  constexpr bool snaps = SNAP;
   constexpr size_t SS = (size_t)GL_DK * GL_DK;
   int off = a.conv_off[b];
   off = off < 0 ? 0 : (off > 2 * a.W - Km1 ? 2 * a.W - Km1 : off);  // never out of range
   const int wbase = off >= a.W ? 0 : a.W;          // window half written by this call
-  int slot = a.rec_slot[b];
-  slot = slot < 0 ? 0 : (slot >= 2 * a.S ? 2 * a.S - 1 : slot);
-  const int rbase = slot >= a.S ? 0 : a.S;         // snapshot half written by this call
+  const int half = a.rec_half[b] & 1, other = half ^ 1;
+  int n = a.fresh ? 0 : a.replay[b];
+  n = n < 0 ? 0 : (n > a.S ? a.S : n);
+  float* st_out = a.rec + ((size_t)(b * 2 + other) * a.Hv + h) * SS;
+  const float* st_in = SHORT ? a.rec + ((size_t)(b * 2 + half) * a.Hv + h) * SS : st_out;
+  const uint8_t* rep_in = a.rep + ((size_t)(b * 2 + half) * a.Hv + h) * a.S * GL_REC_BYTES;
+  uint8_t* rep_out = a.rep + ((size_t)(b * 2 + other) * a.Hv + h) * a.S * GL_REC_BYTES;
   const size_t win_b = (size_t)b * 2 * a.W;
 
   auto gchan = [&](int lc) {  // local channel -> global conv channel
@@ -65,15 +73,22 @@ __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
   // ---- recurrent state ----
   float S[16][4];
   if (!a.fresh) {
-    const float* s0 = a.rec + ((size_t)(b * 2 * a.S + slot) * a.Hv + h) * SS;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float4 f = *reinterpret_cast<const float4*>(s0 + (size_t)(row0 + r) * GL_DK + col0);
+      const float4 f = *reinterpret_cast<const float4*>(st_in + (size_t)(row0 + r) * GL_DK + col0);
       S[r][0] = f.x; S[r][1] = f.y; S[r][2] = f.z; S[r][3] = f.w;
     }
   } else {
 #pragma unroll
     for (int r = 0; r < 16; ++r) S[r][0] = S[r][1] = S[r][2] = S[r][3] = 0.f;
+  }
+  if (SHORT) {  // the committed state: replay the accepted records, store it to the other half
+    for (int j = 0; j < n; ++j) gdn_replay_one(S, rep_in + (size_t)j * GL_REC_BYTES, row0, col0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      store_nt(st_out + (size_t)(row0 + r) * GL_DK + col0,
+               make_uint4(__float_as_uint(S[r][0]), __float_as_uint(S[r][1]),
+                          __float_as_uint(S[r][2]), __float_as_uint(S[r][3])));
   }
   const float a_log = a.A_log[h], dtb = a.dt_bias[h];
   const float qscale = rsqrtf((float)GL_DK);
@@ -105,6 +120,10 @@ __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
       act[r][lc] = round_bf16(silu_g(round_bf16(acc)));
     }
     __syncthreads();
+    if (SHORT)  // k | v of the chunk's records
+      for (int i = tid; i < tc * 32; i += 256)
+        store_nt(rep_out + (size_t)(t0 + i / 32) * GL_REC_BYTES + (i % 32) * 16,
+                 gdn_record_kv(&act[i / 32][GL_DK], i % 32));
     // carry the last K-1 raw inputs as the next chunk's state
     {
       float keep[(GL_KMAX - 1) * GL_CH / 256 + 1];
@@ -151,28 +170,20 @@ __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
       const float rq = rsqrtf(pqq + 1e-6f) * qscale;
       const float kq = pkq * rk * rq;
       const float gam = __expf(gb[i][0]), bet = gb[i][1];
-      float d[4], o[4];
+      float vv[4], d[4], o[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float vv = act[i][2 * GL_DK + col0 + c];
-        d[c] = (vv - gam * pa[c] * rk) * bet;
-        o[c] = gam * pb[c] * rq + d[c] * kq;
-      }
+      for (int c = 0; c < 4; ++c) vv[c] = act[i][2 * GL_DK + col0 + c];
+      gdn_delta(d, pa, vv, gam, rk, bet);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = gam * pb[c] * rq + d[c] * kq;
       if (rg == 0) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) obuf[i][col0 + c] = o[c];
       }
-      float* snap = snaps ? a.rec + ((size_t)(b * 2 * a.S + rbase + t) * a.Hv + h) * SS : nullptr;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float k_r = kr[r] * rk;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) S[r][c] = fmaf(k_r, d[c], gam * S[r][c]);
-        if (snap)
-          store_nt(snap + (size_t)(row0 + r) * GL_DK + col0,
-                   make_uint4(__float_as_uint(S[r][0]), __float_as_uint(S[r][1]),
-                              __float_as_uint(S[r][2]), __float_as_uint(S[r][3])));
-      }
+      if (SHORT && tid == 0)
+        store_nt(rep_out + (size_t)t * GL_REC_BYTES + 4 * GL_DK,
+                 make_uint4(__float_as_uint(gam), __float_as_uint(bet), __float_as_uint(rk), 0u));
+      gdn_update(S, kr, rk, d, gam);
     }
     __syncthreads();
     // 3. gated RMSNorm of each token's 128 outputs: 16 threads per token, 8 columns each
@@ -213,12 +224,11 @@ __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
       }
     }
   }
-  // ---- long calls: final state in slot 0 and the final conv state in rows [0, K-1) ----
-  if (!snaps) {
-    float* sf = a.rec + ((size_t)(b * 2 * a.S + rbase) * a.Hv + h) * SS;
+  // ---- long calls: the final state and the final conv state in rows [0, K-1) ----
+  if (!SHORT) {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
-      *reinterpret_cast<float4*>(sf + (size_t)(row0 + r) * GL_DK + col0) =
+      *reinterpret_cast<float4*>(st_out + (size_t)(row0 + r) * GL_DK + col0) =
           make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
   }
   if (!full_window) {
@@ -232,14 +242,14 @@ __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
 
 
 // ---------------------------------------------------------------------------------
-// Verify / decode form (T <= GL_TC tokens, snapshots, conv kernel 4, the new window
-// fits one half): the same math as gdn_layer_kernel<true>, laid out so that a
-// workgroup makes ONE round trip to memory.  Every input -- the recurrent state
-// (registers), the conv window and the T projection rows of its 384 channels, the
-// conv weights, z, the norm weight, b and a -- is requested in one batch before the
-// first barrier; after it the workgroup only computes and stores: snapshots stream
-// out with non-temporal stores and no barrier ever waits for them (barriers order
-// LDS only).
+// Verify / decode form (T <= S <= GL_TC, conv kernel 4, the new window fits one half):
+// the same math as gdn_layer_kernel<true>, laid out so that a workgroup makes ONE round
+// trip to memory.  Every input -- the recurrent state (registers), the replay records
+// (LDS), the conv window and the T projection rows of its 384 channels, the conv
+// weights, z, the norm weight, b and a -- is requested in one batch before the first
+// barrier; after it the workgroup only computes and stores: the rebuilt state and the
+// new records stream out with non-temporal stores and no barrier ever waits for them
+// (barriers order LDS only).
 constexpr int GV_K = 4;
 
 __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
@@ -250,6 +260,7 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t zb[GL_TC][GL_DK]; // z rows of this head
   __shared__ __attribute__((aligned(16))) uint16_t nw[GL_DK];        // gated-norm weight
   __shared__ float gb[GL_TC][2];                                     // g, beta
+  __shared__ __attribute__((aligned(16))) uint4 rbuf[GL_TC * GL_REC_U4]; // records to replay
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cg = lane & 7, rg = lane >> 3;
   const int b = blockIdx.x / a.Hv, h = blockIdx.x % a.Hv;
@@ -262,9 +273,10 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
   int off = a.conv_off[b];
   off = off < 0 ? 0 : (off > 2 * a.W - Km1 ? 2 * a.W - Km1 : off);  // never out of range
   const int wbase = off >= a.W ? 0 : a.W;          // window half written by this call
-  int slot = a.rec_slot[b];
-  slot = slot < 0 ? 0 : (slot >= 2 * a.S ? 2 * a.S - 1 : slot);
-  const int rbase = slot >= a.S ? 0 : a.S;         // snapshot half written by this call
+  const int half = a.rec_half[b] & 1, other = half ^ 1;
+  int n = a.fresh ? 0 : a.replay[b];
+  n = n < 0 ? 0 : (n > a.S ? a.S : n);             // records to replay (a.S <= GL_TC)
+  const size_t hin = (size_t)(b * 2 + half) * a.Hv + h, hout = (size_t)(b * 2 + other) * a.Hv + h;
   const size_t win_b = (size_t)b * 2 * a.W;
   // channel group gi (q, k, v) -> first global conv channel
   auto gbase = [&](int gi) {
@@ -303,6 +315,17 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
   const size_t base_ba = ((size_t)b * T + (tid < T ? tid : T - 1)) * a.P + a.C + a.value_dim;
   const uint16_t bb_raw = a.proj[base_ba + h], aa_raw = a.proj[base_ba + a.Hv + h];
   const float a_log = a.A_log[h], dtb = a.dt_bias[h];
+  // the n records to replay, 33 chunks of 16 B each (n * 33 <= 264 chunks: two per thread;
+  // the descriptor ends at the n-th record, so the rest read zero and touch no memory)
+  uint4 rv[2];
+  {
+    const __amdgpu_buffer_rsrc_t rr =
+        buf_rsrc(a.rep + hin * a.S * GL_REC_BYTES, (uint32_t)(n * GL_REC_BYTES));
+#pragma unroll
+    for (int it = 0; it < 2; ++it)
+      rv[it] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(rr, (uint32_t)((it * 256 + tid) * 16), 0, 2));
+  }
   // The state last: every load above is waited for before the conv, and the waits are
   // in issue order, so the state (64 KB per workgroup) stays in flight through the conv,
   // gating and norms.  Its loads are unconditional -- a fresh call reads through an empty
@@ -310,7 +333,7 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
   // once per launch (a snapshot of the previous step): non-temporal.
   float S[16][4];
   {
-    const float* s0 = a.rec + ((size_t)(b * 2 * a.S + slot) * a.Hv + h) * SS;
+    const float* s0 = a.rec + hin * SS;
     const __amdgpu_buffer_rsrc_t rs = buf_rsrc(s0, a.fresh ? 0u : (uint32_t)(SS * sizeof(float)));
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -341,6 +364,9 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
   if (tid < 192) *reinterpret_cast<uint4*>(&cw[(tid / 64) * GL_DK + (tid % 64) * 2][0]) = cwv;
   if (tid < T * 16) *reinterpret_cast<uint4*>(&zb[tid / 16][(tid % 16) * 8]) = zv;
   if (tid >= 240) *reinterpret_cast<uint4*>(&nw[(tid - 240) * 8]) = nwv;
+#pragma unroll
+  for (int it = 0; it < 2; ++it)
+    if (it * 256 + tid < GL_TC * GL_REC_U4) rbuf[it * 256 + tid] = rv[it];
   if (tid < T) {
     const float bb = bf16_to_f32(bb_raw), aa = bf16_to_f32(aa_raw);
     gb[tid][0] = -__expf(a_log) * softplus_g(aa + dtb);
@@ -356,7 +382,23 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
     act[r][lc] = round_bf16(silu_g(round_bf16(acc)));
   }
   lds_only_barrier();
-  // ---- 4. the scan, a snapshot per position ----
+  // ---- 4. records of the new positions (k | v now, gamma, beta, 1/|k| in the scan) ----
+  uint8_t* rep_out = a.rep + hout * a.S * GL_REC_BYTES;
+  if (tid < T * 32)
+    store_nt(rep_out + (size_t)(tid / 32) * GL_REC_BYTES + (tid % 32) * 16,
+             gdn_record_kv(&act[tid / 32][GL_DK], tid % 32));
+  // ---- 5. the committed state: the stored state + n replayed records, to the other half ----
+  for (int j = 0; j < n; ++j)
+    gdn_replay_one(S, reinterpret_cast<const uint8_t*>(rbuf) + (size_t)j * GL_REC_BYTES, row0, col0);
+  {
+    float* so = a.rec + hout * SS;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      store_nt(so + (size_t)(row0 + r) * GL_DK + col0,
+               make_uint4(__float_as_uint(S[r][0]), __float_as_uint(S[r][1]),
+                          __float_as_uint(S[r][2]), __float_as_uint(S[r][3])));
+  }
+  // ---- 6. the scan ----
   const float qscale = rsqrtf((float)GL_DK);
   for (int t = 0; t < T; ++t) {
     float kr[16], qr[16];
@@ -395,30 +437,23 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
     const float rq = rsqrtf(pqq + 1e-6f) * qscale;
     const float kq = pkq * rk * rq;
     const float gam = __expf(gb[t][0]), bet = gb[t][1];
-    float d[4], o[4];
+    float vv[4], d[4], o[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float vv = act[t][2 * GL_DK + col0 + c];
-      d[c] = (vv - gam * pa[c] * rk) * bet;
-      o[c] = gam * pb[c] * rq + d[c] * kq;
-    }
+    for (int c = 0; c < 4; ++c) vv[c] = act[t][2 * GL_DK + col0 + c];
+    gdn_delta(d, pa, vv, gam, rk, bet);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = gam * pb[c] * rq + d[c] * kq;
     if (rg == 0) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) obuf[t][col0 + c] = o[c];
     }
-    float* snap = a.rec + ((size_t)(b * 2 * a.S + rbase + t) * a.Hv + h) * SS;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float k_r = kr[r] * rk;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) S[r][c] = fmaf(k_r, d[c], gam * S[r][c]);
-      store_nt(snap + (size_t)(row0 + r) * GL_DK + col0,
-               make_uint4(__float_as_uint(S[r][0]), __float_as_uint(S[r][1]),
-                          __float_as_uint(S[r][2]), __float_as_uint(S[r][3])));
-    }
+    if (tid == 0)
+      store_nt(rep_out + (size_t)t * GL_REC_BYTES + 4 * GL_DK,
+               make_uint4(__float_as_uint(gam), __float_as_uint(bet), __float_as_uint(rk), 0u));
+    if (t + 1 < T) gdn_update(S, kr, rk, d, gam);   // the state after the last position is not kept
   }
   lds_only_barrier();
-  // ---- 5. gated RMSNorm of each token's 128 outputs: 16 threads per token ----
+  // ---- 7. gated RMSNorm of each token's 128 outputs: 16 threads per token ----
   {
     const int i = tid >> 4, part = tid & 15;
     float ov[8], ss = 0.f;
@@ -453,18 +488,57 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
   }
 }
 
+// The committed state of each (sequence, head): the committed half's state with its first
+// replay[b] records applied, in the register layout and arithmetic of the scans above.
+// dst == nullptr: into the other half of rec (where a long call starts from); else into
+// dst (B, Hv, Dk, Dv).
+__global__ __launch_bounds__(256) void gdn_state_kernel(float* rec, const int32_t* rec_half,
+                                                        const uint8_t* rep, const int32_t* replay,
+                                                        int S, int Hv, float* dst) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row0 = (lane >> 3) * 16, col0 = wave * 32 + (lane & 7) * 4;
+  const int b = blockIdx.x / Hv, h = blockIdx.x % Hv;
+  constexpr size_t SS = (size_t)GL_DK * GL_DK;
+  const int half = rec_half[b] & 1;
+  int n = replay[b];
+  n = n < 0 ? 0 : (n > S ? S : n);
+  const float* si = rec + ((size_t)(b * 2 + half) * Hv + h) * SS;
+  float* so = dst ? dst + ((size_t)b * Hv + h) * SS : rec + ((size_t)(b * 2 + (half ^ 1)) * Hv + h) * SS;
+  float St[16][4];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float4 f = *reinterpret_cast<const float4*>(si + (size_t)(row0 + r) * GL_DK + col0);
+    St[r][0] = f.x; St[r][1] = f.y; St[r][2] = f.z; St[r][3] = f.w;
+  }
+  const uint8_t* rp = rep + ((size_t)(b * 2 + half) * Hv + h) * S * GL_REC_BYTES;
+  for (int j = 0; j < n; ++j) gdn_replay_one(St, rp + (size_t)j * GL_REC_BYTES, row0, col0);
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    *reinterpret_cast<float4*>(so + (size_t)(row0 + r) * GL_DK + col0) =
+        make_float4(St[r][0], St[r][1], St[r][2], St[r][3]);
+}
+
 }  // namespace lollm
 
 using namespace lollm;
 
+// Before a long call: the committed state into the other half (nothing to do on a fresh
+// sequence, whose long call starts from zero).  Shared with lollm_gdn_layer_chunked.
+int lollm::gdn_long_call_prologue(const GdnLayerArgs& a, int B, hipStream_t stream) {
+  if (a.fresh) return LOLLM_OK;
+  hipLaunchKernelGGL(gdn_state_kernel, dim3(B * a.Hv), dim3(256), 0, stream, a.rec, a.rec_half,
+                     a.rep, a.replay, a.S, a.Hv, (float*)nullptr);
+  return launch_status();
+}
+
 LOLLM_API int lollm_gdn_layer(const void* proj, long long proj_stride, const void* conv_w,
                               const float* A_log, const float* dt_bias, const void* norm_w,
                               void* win, const int32_t* conv_off, int win_rows, float* rec,
-                              const int32_t* rec_slot, int slots, int fresh, void* out, int B,
-                              int T, int Hk, int Hv, int Dk, int Dv, int conv_kernel, float eps,
-                              void* stream) {
+                              const int32_t* rec_half, void* rep, const int32_t* replay, int slots,
+                              int fresh, void* out, int B, int T, int Hk, int Hv, int Dk, int Dv,
+                              int conv_kernel, float eps, void* stream) {
   if (!proj || !conv_w || !A_log || !dt_bias || !norm_w || !win || !conv_off || !rec ||
-      !rec_slot || !out)
+      !rec_half || !rep || !replay || !out)
     return LOLLM_EINVAL;
   if (B <= 0 || T <= 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return LOLLM_EINVAL;
   if (Dk != GL_DK || Dv != GL_DK || conv_kernel < 1 || conv_kernel > GL_KMAX) return LOLLM_EUNSUPPORTED;
@@ -474,17 +548,33 @@ LOLLM_API int lollm_gdn_layer(const void* proj, long long proj_stride, const voi
   GdnLayerArgs a;
   a.proj = (const uint16_t*)proj; a.conv_w = (const uint16_t*)conv_w; a.A_log = A_log;
   a.dt_bias = dt_bias; a.norm_w = (const uint16_t*)norm_w; a.win = (uint16_t*)win;
-  a.conv_off = conv_off; a.rec = rec; a.rec_slot = rec_slot; a.out = (uint16_t*)out;
+  a.conv_off = conv_off; a.rec = rec; a.rec_half = rec_half; a.rep = (uint8_t*)rep;
+  a.replay = replay; a.out = (uint16_t*)out;
   a.P = proj_stride; a.T = T; a.Hk = Hk; a.Hv = Hv; a.C = C; a.key_dim = key_dim;
   a.value_dim = value_dim; a.K = conv_kernel; a.W = win_rows; a.S = slots; a.fresh = fresh ? 1 : 0;
   a.eps = eps;
-  const bool verify_form = T <= GL_TC && T <= slots && conv_kernel == GV_K &&
+  const hipStream_t st = (hipStream_t)stream;
+  const bool verify_form = T <= slots && slots <= GL_TC && conv_kernel == GV_K &&
                            conv_kernel - 1 + T <= win_rows && C % 8 == 0;
-  if (verify_form)
-    hipLaunchKernelGGL(gdn_layer_verify_kernel, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);
-  else if (T <= slots)
-    hipLaunchKernelGGL(gdn_layer_kernel<true>, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);
-  else
-    hipLaunchKernelGGL(gdn_layer_kernel<false>, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, a);
+  if (verify_form) {
+    hipLaunchKernelGGL(gdn_layer_verify_kernel, dim3(B * Hv), dim3(256), 0, st, a);
+  } else if (T <= slots) {
+    hipLaunchKernelGGL(gdn_layer_kernel<true>, dim3(B * Hv), dim3(256), 0, st, a);
+  } else {
+    const int rc = gdn_long_call_prologue(a, B, st);
+    if (rc != LOLLM_OK) return rc;
+    hipLaunchKernelGGL(gdn_layer_kernel<false>, dim3(B * Hv), dim3(256), 0, st, a);
+  }
+  return launch_status();
+}
+
+LOLLM_API int lollm_gdn_state(float* rec, const int32_t* rec_half, const void* rep,
+                              const int32_t* replay, int slots, int B, int Hv, int Dk, int Dv,
+                              float* out, void* stream) {
+  if (!rec || !rec_half || !rep || !replay) return LOLLM_EINVAL;
+  if (B <= 0 || Hv <= 0 || slots < 1) return LOLLM_EINVAL;
+  if (Dk != GL_DK || Dv != GL_DK) return LOLLM_EUNSUPPORTED;
+  hipLaunchKernelGGL(gdn_state_kernel, dim3(B * Hv), dim3(256), 0, (hipStream_t)stream, rec,
+                     rec_half, (const uint8_t*)rep, replay, slots, Hv, out);
   return launch_status();
 }

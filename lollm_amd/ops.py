@@ -504,42 +504,77 @@ GDN_CHUNK_MIN_T = 64
 
 def gdn_chunked_ok(T, slots, win_rows, conv_kernel, proj_stride=0):
     """Whether a call can take the chunked long-call kernel (lollm_gdn_layer_chunked):
-    a call longer than the snapshot slots and the conv window, and one sequence's
+    a call longer than the replay-record slots and the conv window, and one sequence's
     projection rows addressable with 32-bit byte offsets."""
     return (conv_kernel == 4 and T > slots and conv_kernel - 1 + T > win_rows
             and T * proj_stride * 2 < 2 ** 31)
 
 
-def gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_slot, fresh, B, T,
-              Hk, Hv, D, conv_kernel, eps, out=None, chunked=None):
+def gdn_record_bytes(D):
+    """Bytes of one replay record of a GDN head with Dk = Dv = D: k and v (bf16), then
+    exp(g), beta and 1/|k| (fp32) and a pad word."""
+    return 4 * D + 16
+
+
+def _check_gdn_state(rec, rec_half, rep, replay, B, Hv, D):
+    _need(rec, "rec", torch.float32, (B, 2, Hv, D, D))
+    _need(rec_half, "rec_half", torch.int32, (B,))
+    _need(replay, "replay", torch.int32, (B,))
+    _need(rep, "rep", torch.uint8)
+    if (rep.dim() != 5 or tuple(rep.shape[:3]) != (B, 2, Hv)
+            or rep.shape[4] != gdn_record_bytes(D) or rep.shape[3] < 1):
+        raise ValueError(f"rep must be (B, 2, Hv, slots, {gdn_record_bytes(D)}) uint8")
+    return rep.shape[3]
+
+
+def gdn_layer(proj, conv_w, A_log, dt_bias, norm_w, win, conv_off, rec, rec_half, rep, replay,
+              fresh, B, T, Hk, Hv, D, conv_kernel, eps, out=None, chunked=None):
     """Fused GDN mixer (include/lollm_amd.h).  proj (B, T, P) bf16; win (B, 2W,
-    conv_dim) bf16; rec (B, 2S, Hv, D, D) fp32; conv_off / rec_slot (B,) int32.
+    conv_dim) bf16; rec (B, 2, Hv, D, D) fp32 state halves; rep (B, 2, Hv, S,
+    gdn_record_bytes(D)) uint8 replay records; conv_off / rec_half / replay (B,) int32.
     chunked: None = the chunked kernel for long calls of at least GDN_CHUNK_MIN_T tokens
     that it supports, the recurrent kernel otherwise; True / False force one."""
     P = proj.shape[-1]
     _need(proj, "proj", torch.bfloat16)
     _need(win, "win", torch.bfloat16)
-    _need(rec, "rec", torch.float32)
     _need(conv_off, "conv_off", torch.int32, (B,))
-    _need(rec_slot, "rec_slot", torch.int32, (B,))
-    if win.shape[0] != B or win.shape[1] % 2 or rec.shape[0] != B or rec.shape[1] % 2:
-        raise ValueError("win / rec must hold two halves per sequence")
+    S = _check_gdn_state(rec, rec_half, rep, replay, B, Hv, D)
+    if win.shape[0] != B or win.shape[1] % 2:
+        raise ValueError("win must hold two halves per sequence")
     value_dim = Hv * D
     if out is None:
         out = torch.empty(B, T, value_dim, dtype=torch.bfloat16, device=proj.device)
-    W, S = win.shape[1] // 2, rec.shape[1] // 2
+    W = win.shape[1] // 2
     if chunked is None:
         chunked = T >= GDN_CHUNK_MIN_T and gdn_chunked_ok(T, S, W, conv_kernel, P)
     fn = "lollm_gdn_layer_chunked" if chunked else "lollm_gdn_layer"
     rc = getattr(_lib.lib(), fn)(
         _ptr(proj), P, _ptr(conv_w), _ptr(A_log), _ptr(dt_bias), _ptr(norm_w), _ptr(win),
-        _ptr(conv_off), W, _ptr(rec), _ptr(rec_slot), S, int(bool(fresh)), _ptr(out), B, T, Hk,
-        Hv, D, D, conv_kernel, float(eps), _stream())
+        _ptr(conv_off), W, _ptr(rec), _ptr(rec_half), _ptr(rep), _ptr(replay), S,
+        int(bool(fresh)), _ptr(out), B, T, Hk, Hv, D, D, conv_kernel, float(eps), _stream())
     _lib.check(rc, fn)
     return out
 
 
-def spec_commit(verify_ids, n_accepted, next_token, lengths, rec_slot, conv_off, pending,
+def gdn_state(rec, rec_half, rep, replay, out=None, to_other_half=False):
+    """The committed recurrent state of one GDN layer (lollm_gdn_state): (B, Hv, D, D) fp32
+    in `out` (allocated if None), or, with to_other_half, written into the other half of
+    rec (returns None; the caller then flips rec_half and zeroes replay)."""
+    B, _, Hv, D, _ = rec.shape
+    S = _check_gdn_state(rec, rec_half, rep, replay, B, Hv, D)
+    if to_other_half:
+        out = None
+    elif out is None:
+        out = torch.empty(B, Hv, D, D, dtype=torch.float32, device=rec.device)
+    else:
+        _need(out, "out", torch.float32, (B, Hv, D, D))
+    rc = _lib.lib().lollm_gdn_state(_ptr(rec), _ptr(rec_half), _ptr(rep), _ptr(replay), S, B, Hv,
+                                    D, D, _ptr(out), _stream())
+    _lib.check(rc, "lollm_gdn_state")
+    return out
+
+
+def spec_commit(verify_ids, n_accepted, next_token, lengths, rec_half, replay, conv_off, pending,
                 out_tokens, out_count, hidden, h_last, offset, slots, win_rows, accept_hist=None,
                 seen=None):
     B, T = verify_ids.shape
@@ -549,8 +584,8 @@ def spec_commit(verify_ids, n_accepted, next_token, lengths, rec_slot, conv_off,
         if seen.dim() != 2 or seen.shape[0] != B:
             raise ValueError("seen must be (B, words) int32")
     rc = _lib.lib().lollm_spec_commit(
-        _ptr(verify_ids), _ptr(n_accepted), _ptr(next_token), _ptr(lengths), _ptr(rec_slot),
-        _ptr(conv_off), _ptr(pending), _ptr(out_tokens), _ptr(out_count), out_tokens.shape[1],
+        _ptr(verify_ids), _ptr(n_accepted), _ptr(next_token), _ptr(lengths), _ptr(rec_half),
+        _ptr(replay), _ptr(conv_off), _ptr(pending), _ptr(out_tokens), _ptr(out_count), out_tokens.shape[1],
         _ptr(hidden), _ptr(h_last), B, T, H, slots, win_rows, _ptr(offset), _ptr(accept_hist),
         _ptr(seen), 0 if seen is None else seen.shape[1], _stream())
     _lib.check(rc, "lollm_spec_commit")

@@ -175,7 +175,8 @@ class GatedDeltaNet:
         proj = self.in_proj(x)
         s = cache.layers[layer]
         return ops.gdn_layer(proj, self.conv_w, self.A_log, self.dt_bias, self.norm_w, s["win"],
-                             cache.conv_off, s["rec"], cache.rec_slot, cache.fresh, B, T,
+                             cache.conv_off, s["rec"], cache.rec_half, s["rep"], cache.replay,
+                             cache.fresh, B, T,
                              cfg.linear_num_key_heads, cfg.linear_num_value_heads,
                              cfg.linear_key_head_dim, cfg.linear_conv_kernel_dim,
                              cfg.rms_norm_eps)

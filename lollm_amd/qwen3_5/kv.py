@@ -10,19 +10,23 @@ for the MI355X kernels:
     device holds each sequence's committed length (the reference has one scalar
     `seen_tokens`, so it cannot hold ragged batches).
   * Gated DeltaNet layers: a conv-window buffer (B, 2W, conv_dim) bf16 with W = K-1+S
-    rows per half and a recurrent-state buffer (B, 2S, n_v, Dk, Dv) fp32 with S = 1 + k
-    snapshot slots per half.  `conv_off` and `rec_slot` (B,) int32 locate, per
-    sequence, the committed conv state and recurrent state; a forward reads that half
-    and writes the other one (the kernel derives the halves on the device), so rolling
-    back to `a` accepted drafts only rewrites three small integers per sequence
-    (`lollm_spec_commit`) -- the reference instead deep-copies the whole cache before
-    every verify (kv.py:49-54, mtp.py:141) and re-runs on reject (mtp.py:156-162).
+    rows per half, a recurrent-state buffer (B, 2, n_v, Dk, Dv) fp32 and a replay-record
+    buffer (B, 2, n_v, S, 4 Dk + 16) bytes with S = 1 + k positions per half.
+    `conv_off` (B,) int32 locates each sequence's committed conv state; `rec_half` and
+    `replay` (B,) int32 say that its committed recurrent state is that half's state with
+    the half's first `replay` records applied.  A forward reads the committed half and
+    writes the other one (the kernel derives the halves on the device); a short forward
+    (T <= S) writes the committed state plus one record per position instead of T
+    states, so rolling back to `a` accepted drafts only rewrites four small integers per
+    sequence (`lollm_spec_commit`) -- the reference instead deep-copies the whole cache
+    before every verify (kv.py:49-54, mtp.py:141) and re-runs on reject (mtp.py:156-162).
 """
 
 from __future__ import annotations
 
 import torch
 
+from .. import ops
 from .config import Qwen3_5Config
 
 
@@ -49,13 +53,17 @@ class Qwen3_5Cache:
                 self.layers[i] = {
                     "win": torch.zeros(batch, 2 * self.win_rows, cfg.conv_dim,
                                        dtype=torch.bfloat16, device=device),
-                    "rec": torch.zeros(batch, 2 * spec_slots, cfg.linear_num_value_heads,
+                    "rec": torch.zeros(batch, 2, cfg.linear_num_value_heads,
                                        cfg.linear_key_head_dim, cfg.linear_value_head_dim,
                                        dtype=torch.float32, device=device),
+                    "rep": torch.zeros(batch, 2, cfg.linear_num_value_heads, spec_slots,
+                                       4 * cfg.linear_key_head_dim + 16, dtype=torch.uint8,
+                                       device=device),
                 }
         self.fresh = True                 # no GDN state yet (zero initial state)
         self.lengths = torch.zeros(batch, dtype=torch.int32, device=device)
-        self.rec_slot = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.rec_half = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.replay = torch.zeros(batch, dtype=torch.int32, device=device)
         self.conv_off = torch.zeros(batch, dtype=torch.int32, device=device)
         self.last_T = 0
         # host-side upper bound of max(lengths): every forward or speculative step adds
@@ -89,13 +97,13 @@ class Qwen3_5Cache:
     def commit_all(self, T: int):
         """After a forward over T tokens: every token is committed (the reference's
         forward + advance(T), modeling_qwen3_5.py:97).  The forward wrote the other half
-        of every GDN buffer."""
+        of every GDN buffer: a short forward its T records, a long one its final state."""
         S, W, K = self.spec_slots, self.win_rows, self.cfg.linear_conv_kernel_dim
         self.fresh = False
         self.last_T = T
-        snap = T <= S
         full = K - 1 + T <= W
-        self.rec_slot.copy_(torch.where(self.rec_slot >= S, 0, S) + (T - 1 if snap else 0))
+        self.rec_half.bitwise_xor_(1)
+        self.replay.fill_(T if T <= S else 0)
         self.conv_off.copy_(torch.where(self.conv_off >= W, 0, W) + (T if full else 0))
         self.lengths.add_(T)
         self.grew(T)
@@ -104,10 +112,10 @@ class Qwen3_5Cache:
         """After commit_all(T) with T <= spec_slots: keep n_accepted[b] + 1 tokens."""
         T = self.last_T
         if T > self.spec_slots:
-            raise RuntimeError("rollback needs the last forward to have written snapshots")
+            raise RuntimeError("rollback needs the last forward to have written replay records")
         a = n_accepted.to(torch.int32).clamp(0, T - 1)
         self.lengths.sub_(T - 1 - a)
-        self.rec_slot.sub_(T - 1 - a)
+        self.replay.sub_(T - 1 - a)
         self.conv_off.sub_(T - 1 - a)
 
     # -- the reference cache API (kv.py:26-58) ---------------------------------------
@@ -154,17 +162,30 @@ class Qwen3_5Cache:
         b = torch.arange(self.batch, device=self.device)
         rows = self.conv_off[:, None].long() + torch.arange(K - 1, device=self.device)[None]
         conv = s["win"][b[:, None], rows].transpose(1, 2).contiguous()
-        rec = s["rec"][b, self.rec_slot.long()].contiguous()
+        rec = ops.gdn_state(s["rec"], self.rec_half, s["rep"], self.replay)
         return conv, rec
+
+    def settle(self):
+        """Fold every GDN layer's pending replay records into its state: each layer's
+        committed state goes to the other half, which becomes the committed one with no
+        records (the cache holds the same state afterwards)."""
+        if self.fresh:
+            return
+        for s in self.layers:
+            if s is not None and "rec" in s:
+                ops.gdn_state(s["rec"], self.rec_half, s["rep"], self.replay, to_other_half=True)
+        self.rec_half.bitwise_xor_(1)
+        self.replay.zero_()
 
     def set_linear_state(self, layer, conv, rec):
         s = self.layers[layer]
         K = self.cfg.linear_conv_kernel_dim
         b = torch.arange(self.batch, device=self.device)
+        self.settle()   # the other layers keep their states; this one's is replaced whole
         rows = self.conv_off[:, None].long() + torch.arange(K - 1, device=self.device)[None]
         s["win"][b[:, None], rows] = conv.transpose(1, 2).to(torch.bfloat16)
-        s["rec"][b, self.rec_slot.long()] = rec.float()
-        self.fresh = False
+        s["rec"][b, self.rec_half.long()] = rec.float()
+        self.fresh = False   # (a new cache's other layers hold zero states, as on a first call)
 
     def clone(self):
         new = Qwen3_5Cache.__new__(Qwen3_5Cache)
@@ -175,7 +196,7 @@ class Qwen3_5Cache:
                 new.layers.append(None)
             else:
                 new.layers.append({n: t.clone() for n, t in s.items()})
-        for n in ("lengths", "rec_slot", "conv_off"):
+        for n in ("lengths", "rec_half", "replay", "conv_off"):
             setattr(new, n, getattr(self, n).clone())
         return new
 

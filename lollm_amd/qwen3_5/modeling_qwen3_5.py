@@ -111,7 +111,7 @@ class Qwen3_5Model:
 
     def hidden_states(self, input_ids, cache):
         """The decoder stack; returns (pre-norm hidden, final-normed hidden).  Writes
-        the KV rows / GDN snapshots of the T new tokens but does not commit them.  The
+        the KV rows / GDN records of the T new tokens but does not commit them.  The
         caller has checked the capacity (cache.reserve(T))."""
         B, T = input_ids.shape
         cfg = self.cfg

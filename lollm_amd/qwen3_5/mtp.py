@@ -270,8 +270,8 @@ class SpecDecoder:
         ops.spec_accept(logits, self.draft_logits, self.drafts, self.temperature, self.top_k,
                         self.top_p, self.seed, 0, offset_dev=self.offset,
                         workspace=self.spec_ws, n_accepted=self.n_acc, next_token=self.next_tok)
-        ops.spec_commit(verify_ids, self.n_acc, self.next_tok, cache.lengths, cache.rec_slot,
-                        cache.conv_off, self.pending, self.out_tokens, self.out_count,
+        ops.spec_commit(verify_ids, self.n_acc, self.next_tok, cache.lengths, cache.rec_half,
+                        cache.replay, cache.conv_off, self.pending, self.out_tokens, self.out_count,
                         hidden.contiguous(), self.h_last, self.offset, cache.spec_slots,
                         cache.win_rows, self.accept_hist, seen=self.seen)
         cache.fresh = False

@@ -176,7 +176,8 @@ def test_repetition_penalty_bit_exact_acceptance_shape():
 
 def test_spec_commit_marks_context():
     """lollm_spec_commit adds the accepted drafts and the new pending token to the
-    sequence's seen bitmap (mtp.py:129,150), nothing else."""
+    sequence's seen bitmap (mtp.py:129,150), nothing else; the GDN state moves to the
+    half the verify wrote, with a + 1 of its replay records kept."""
     from lollm_amd import ops
     B, T, H, V = 3, 4, 64, 1000
     i32 = dict(dtype=torch.int32, device="cuda")
@@ -185,10 +186,16 @@ def test_spec_commit_marks_context():
     nxt = torch.tensor([100, 200, 300], **i32)
     z = lambda: torch.zeros(B, **i32)  # noqa: E731
     seen = ops.new_seen(B, V, "cuda")
-    ops.spec_commit(ids, n_acc, nxt, z(), z(), z(), z(), torch.zeros(B, 16, **i32), z(),
+    rec_half = torch.tensor([0, 1, 0], **i32)
+    replay, conv_off = z(), torch.tensor([0, 7, 3], **i32)
+    ops.spec_commit(ids, n_acc, nxt, z(), rec_half, replay, conv_off, z(),
+                    torch.zeros(B, 16, **i32), z(),
                     torch.zeros(B, T, H, dtype=torch.bfloat16, device="cuda"),
                     torch.zeros(B, H, dtype=torch.bfloat16, device="cuda"),
                     torch.zeros(1, dtype=torch.int64, device="cuda"), 4, 7, seen=seen)
+    assert rec_half.tolist() == [1, 0, 1]
+    assert replay.tolist() == [1, 3, 4]
+    assert conv_off.tolist() == [7 + 1, 0 + 3, 7 + 4]
     bits = seen.cpu().numpy().view(np.uint32)
     marked = [{t for t in range(V) if bits[b, t >> 5] >> (t & 31) & 1} for b in range(B)]
     assert marked == [{100}, {10, 11, 200}, {14, 15, 16, 300}]
