@@ -37,6 +37,34 @@ template <> struct Elt<uint16_t> {
 
 __device__ __forceinline__ float wave_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// Sum over the 8 lanes of a wave that share lane % 8 (partners 8, 16 and 32 lanes away),
+// the same value in each of them: a DPP rotation by 8 inside each 16-lane row, then the
+// gfx950 row swaps (v_permlane16_swap, v_permlane32_swap) for the partners in the other
+// row of the pair and in the other half.  Every step adds a lane's value and its
+// partner's, so the sums and their rounding are those of the xor-shuffle tree
+// (v + shfl_xor(v, 8), then 16, then 32) without its LDS-crossbar round trips.
+__device__ __forceinline__ float sum_lanes8(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128 /* row_ror:8 */,
+                                                  0xf, 0xf, false));
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Sum over each 16-lane row of a wave (lanes 16 r .. 16 r + 15), the same value in each
+// lane, with DPP only: partners 1 and 2 away (quad permutes), 4 away (after the first two
+// steps every lane of a quad holds the quad's sum, and the half-row mirror reads the other
+// quad) and 8 away (row rotation).  The sums are those of the xor-shuffle tree over masks
+// 1, 2, 4, 8.
+__device__ __forceinline__ float sum_lanes16(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1 /* quad 1,0,3,2 */, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e /* quad 2,3,0,1 */, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141 /* row_half_mirror */, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128 /* row_ror:8 */, 0xf, 0xf, false));
+  return v;
+}
+
 // Streaming (non-temporal) 16-byte global load/store: data touched once per launch
 // should not displace reusable lines in L2 / MALL.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));

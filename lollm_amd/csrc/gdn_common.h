@@ -80,9 +80,7 @@ __device__ __forceinline__ void gdn_replay_one(float (&S)[16][4], const uint8_t*
 #pragma unroll
     for (int c = 0; c < 4; ++c) pa[c] = fmaf(S[r][c], kr[r], pa[c]);
 #pragma unroll
-  for (int m = 8; m < 64; m <<= 1)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) pa[c] += wave_xor(pa[c], m);
+  for (int c = 0; c < 4; ++c) pa[c] = sum_lanes8(pa[c]);
   float d[4];
   gdn_delta(d, pa, vv, sc.x, sc.z, sc.y);
   gdn_update(S, kr, sc.z, d, sc.x);

@@ -156,16 +156,13 @@ __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
         pqq = fmaf(qr[r], qr[r], pqq);
       }
 #pragma unroll
-      for (int m = 8; m < 64; m <<= 1) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          pa[c] += wave_xor(pa[c], m);
-          pb[c] += wave_xor(pb[c], m);
-        }
-        pkq += wave_xor(pkq, m);
-        pkk += wave_xor(pkk, m);
-        pqq += wave_xor(pqq, m);
+      for (int c = 0; c < 4; ++c) {
+        pa[c] = sum_lanes8(pa[c]);
+        pb[c] = sum_lanes8(pb[c]);
       }
+      pkq = sum_lanes8(pkq);
+      pkk = sum_lanes8(pkk);
+      pqq = sum_lanes8(pqq);
       const float rk = rsqrtf(pkk + 1e-6f);
       const float rq = rsqrtf(pqq + 1e-6f) * qscale;
       const float kq = pkq * rk * rq;
@@ -197,8 +194,7 @@ __global__ __launch_bounds__(256) void gdn_layer_kernel(GdnLayerArgs a) {
           ss += ov[e] * ov[e];
         }
       }
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+      ss = sum_lanes16(ss);
       if (i < tc) {
         const float r = rsqrtf(ss / (float)GL_DK + a.eps);
         const size_t zb = ((size_t)b * a.T + t0 + i) * a.P + a.C + (size_t)h * GL_DK + part * 8;
@@ -423,16 +419,13 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
       pqq = fmaf(qr[r], qr[r], pqq);
     }
 #pragma unroll
-    for (int m = 8; m < 64; m <<= 1) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        pa[c] += wave_xor(pa[c], m);
-        pb[c] += wave_xor(pb[c], m);
-      }
-      pkq += wave_xor(pkq, m);
-      pkk += wave_xor(pkk, m);
-      pqq += wave_xor(pqq, m);
+    for (int c = 0; c < 4; ++c) {
+      pa[c] = sum_lanes8(pa[c]);
+      pb[c] = sum_lanes8(pb[c]);
     }
+    pkq = sum_lanes8(pkq);
+    pkk = sum_lanes8(pkk);
+    pqq = sum_lanes8(pqq);
     const float rk = rsqrtf(pkk + 1e-6f);
     const float rq = rsqrtf(pqq + 1e-6f) * qscale;
     const float kq = pkq * rk * rq;
@@ -464,8 +457,7 @@ __global__ __launch_bounds__(256) void gdn_layer_verify_kernel(GdnLayerArgs a) {
         ss += ov[e] * ov[e];
       }
     }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    ss = sum_lanes16(ss);
     if (i < T) {
       const float r = rsqrtf(ss / (float)GL_DK + a.eps);
       uint32_t od[4];

@@ -170,17 +170,14 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(
 
     // reduce over the 8 row groups (lanes differing in bits 3..5)
 #pragma unroll
-    for (int m = 8; m < 64; m <<= 1) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        pa[c] += wave_xor(pa[c], m);
-        pb[c] += wave_xor(pb[c], m);
-      }
-      pkq += wave_xor(pkq, m);
-      if (L2) {
-        pkk += wave_xor(pkk, m);
-        pqq += wave_xor(pqq, m);
-      }
+    for (int c = 0; c < NC; ++c) {
+      pa[c] = sum_lanes8(pa[c]);
+      pb[c] = sum_lanes8(pb[c]);
+    }
+    pkq = sum_lanes8(pkq);
+    if (L2) {
+      pkk = sum_lanes8(pkk);
+      pqq = sum_lanes8(pqq);
     }
     const float rk = L2 ? rsqrtf(pkk + 1e-6f) : 1.f;
     const float rq = (L2 ? rsqrtf(pqq + 1e-6f) : 1.f) * q_scale;
