@@ -788,7 +788,8 @@ __device__ __forceinline__ void split_range(int nch, int ns, int s, int& lo, int
 }
 
 // Pass 1, grid (ns, B): workgroup (s, b) sums the draw's weights over the s-th of ns
-// contiguous slices of the vocabulary (exact integers, u128 in part[b ns + s]).
+// contiguous slices of the vocabulary, per wave: the 16 wave segments' exact totals
+// (u128) in part[(b ns + s) 16 + w].
 __global__ __launch_bounds__(SP_THREADS) void spec_partial_kernel(
     const uint16_t* __restrict__ target, const uint16_t* __restrict__ draft,
     const int32_t* __restrict__ drafts, int k, int V, float inv_temp, uint64_t seed,
@@ -810,13 +811,15 @@ __global__ __launch_bounds__(SP_THREADS) void spec_partial_kernel(
     using Acc = decltype(tag);
     Acc* wtot;
     if constexpr (sizeof(Acc) == 16) wtot = wt128; else wtot = wt64;
-    const Acc tot = draw_totals<Acc, sizeof(Acc) == 16 ? SP_UN128 : SP_UN64>(lo, hi, ld, wt, wtot);
-    if (threadIdx.x == 0) part[(size_t)b * ns + s] = (u128)tot;
+    draw_totals<Acc, sizeof(Acc) == 16 ? SP_UN128 : SP_UN64>(lo, hi, ld, wt, wtot);
+    if (threadIdx.x < SP_THREADS / 64)
+      part[((size_t)b * ns + s) * (SP_THREADS / 64) + threadIdx.x] = (u128)wtot[threadIdx.x];
   });
 }
 
-// Pass 2, grid (B): the slice holding the target, then the token inside it (the slice
-// summed by the 16 waves, the owning sixteenth summed again, its owning sixteenth walked).
+// Pass 2, grid (B): the wave segment of pass 1 holding the target (from its totals), that
+// segment summed again split over the 16 waves, and the owning sixteenth walked -- the
+// same token as walking the whole slice, one pass over the slice fewer.
 __global__ __launch_bounds__(SP_THREADS) void spec_final_kernel(
     const uint16_t* __restrict__ target, const uint16_t* __restrict__ draft,
     const int32_t* __restrict__ drafts, int k, int V, float inv_temp, uint64_t seed,
@@ -836,8 +839,19 @@ __global__ __launch_bounds__(SP_THREADS) void spec_final_kernel(
   const AcceptPlan pl = accept_plan(target, draft, drafts, k, V, c, seed, offset, st_t, st_d, b, ok);
   const RowStat sp = st_t[b * (k + 1) + pl.a];
   const int nch = V >> 3;
-  u128 R = 0;
-  for (int s = 0; s < ns; ++s) R += part[(size_t)b * ns + s];
+  constexpr int NW = SP_THREADS / 64;
+  // the ns x 16 segment totals, lane l of every wave holding entries 4 l .. 4 l + 3
+  // (ns * NW <= 256), their lane-inclusive prefix and the total R
+  const u128* pb = part + (size_t)b * ns * NW;
+  const int lane = threadIdx.x & 63;
+  u128 pv[4], p4 = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    pv[u] = 4 * lane + u < ns * NW ? pb[4 * lane + u] : (u128)0;
+    p4 += pv[u];
+  }
+  const u128 pinc = wave_incl_scan(p4);
+  const u128 R = shfl_any(pinc, 63);
   int32_t tok;
   if (sp.greedy && pl.kind == 0) {
     tok = sp.argmax;
@@ -849,22 +863,35 @@ __global__ __launch_bounds__(SP_THREADS) void spec_final_kernel(
     // target: floor(U Z / 2^24) for the bonus (Z = the kept mass of p), U R scaled for
     // a residual; then the slice whose running total passes it
     const u128 tgt = pl.kind == 0 ? (u128)(((u128)pl.U * sp.Z) >> 24) : scaled_target(pl.U, R);
-    u128 before = 0;
-    int s_hit = ns - 1;
-    for (int s = 0; s < ns; ++s) {
-      const u128 v = part[(size_t)b * ns + s];
-      if (before + v > tgt) { s_hit = s; break; }
-      before += v;
+    // the segment whose running total passes it: its lane walks its 4 entries
+    int i_hit = -1;
+    u128 before = pinc - p4;
+    if (before <= tgt && pinc > tgt) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (i_hit < 0 && before + pv[u] > tgt) i_hit = 4 * lane + u;
+        if (i_hit < 0) before += pv[u];
+      }
+    }
+    const uint64_t owner = __ballot(i_hit >= 0);
+    if (owner) {
+      const int ol = __ffsll((unsigned long long)owner) - 1;
+      i_hit = __shfl(i_hit, ol, 64);
+      before = shfl_any(before, ol);
+    } else {   // not reached for tgt < R
+      i_hit = ns * NW - 1;
+      before = R - pb[ns * NW - 1];
     }
     int lo, hi;
-    split_range(nch, ns, s_hit, lo, hi);
+    split_range(nch, ns, i_hit / NW, lo, hi);
+    const int seg = range_seg(lo, hi);
+    const int lo1 = min(hi, lo + (i_hit % NW) * seg), hi1 = min(lo1 + seg, hi);
     with_draw(pl, target, draft, k, V, c, st_t, st_d, b, tab_p, tab_q, [&](auto ld, auto wt, auto tag) {
       using Acc = decltype(tag);
-      constexpr int UN = sizeof(Acc) == 16 ? SP_UN128 : SP_UN64;
       Acc* wtot;
       if constexpr (sizeof(Acc) == 16) wtot = wt128; else wtot = wt64;
-      draw_totals<Acc, UN>(lo, hi, ld, wt, wtot);
-      tok = draw_find<Acc>(lo, hi, ld, wt, wtot, (Acc)(tgt - before), V, &found);
+      draw_totals<Acc, 1>(lo1, hi1, ld, wt, wtot);
+      tok = draw_find<Acc>(lo1, hi1, ld, wt, wtot, (Acc)(tgt - before), V, &found);
     });
   }
   if (threadIdx.x == 0) {
@@ -996,6 +1023,8 @@ static long long stats_bytes(long long rows) {
 
 constexpr int SP_MAXSLICE = 16;   // vocabulary slices of the acceptance draw
 
+static int accept_slices(int B) { return std::max(1, std::min(SP_MAXSLICE, 256 / B)); }
+
 static long long accept_part_offset(int B, int k, int with_draft) {
   const long long st = stats_bytes((long long)B * (k + 1) + (with_draft ? (long long)B * k : 0));
   return (st + 15) / 16 * 16;
@@ -1003,7 +1032,9 @@ static long long accept_part_offset(int B, int k, int with_draft) {
 
 LOLLM_API long long lollm_spec_workspace_bytes(int B, int k, int with_draft) {
   if (B <= 0 || k < 0) return -1;
-  return accept_part_offset(B, k, with_draft) + (long long)B * SP_MAXSLICE * (long long)sizeof(u128);
+  // one u128 per (sequence, slice, wave)
+  return accept_part_offset(B, k, with_draft) +
+         (long long)B * accept_slices(B) * (SP_THREADS / 64) * (long long)sizeof(u128);
 }
 
 LOLLM_API long long lollm_sample_workspace_bytes(int rows) {
@@ -1032,7 +1063,7 @@ LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int
   // the draw: B x ns workgroups sum the draw's weights over ns vocabulary slices (one
   // round of workgroups: one 1024-thread workgroup fits a CU), then one workgroup per
   // sequence finds the slice and the token in it
-  const int ns = std::max(1, std::min(SP_MAXSLICE, 256 / B));
+  const int ns = accept_slices(B);
   u128* apart = (u128*)((char*)workspace + accept_part_offset(B, k, draft != nullptr));
   const size_t tabs = (draft ? 2 : 1) * SP_NBINS * sizeof(uint64_t);
   static bool lds_set[64] = {};   // per device: the attribute is set on the current device
