@@ -306,6 +306,16 @@ int lollm_gdn_layer_chunked(const void* proj, long long proj_stride, const void*
                             int fresh, void* out, int B, int T, int Hk, int Hv, int Dk, int Dv,
                             int conv_kernel, float eps, void* stream);
 
+/* Greedy acceptance (temperature 0) without the verify logits: argmax (B, k + 1) int32
+ * holds the argmax token of each verify row (lollm_gemm_argmax on the lm_head, same
+ * token as lollm_gemm + the greedy sampler); n_accepted[b] = the number of leading drafts
+ * (B, k) equal to their row's argmax, next_token[b] = the argmax of row n_accepted[b].
+ * Replaces the draft == true_next test and the next sample_next of src/qwen3_5/mtp.py
+ * :141-155 at temperature 0 (sample_next's argmax, src/generate.py:23-24); with
+ * lollm_gemm_argmax it keeps the (B, 1 + k, V) verify logits from being materialised. */
+int lollm_greedy_accept(const int32_t* argmax, const int32_t* drafts, int B, int k,
+                        int32_t* n_accepted, int32_t* next_token, void* stream);
+
 /* End of one speculative step, per sequence b with a = n_accepted[b] (of T - 1
  * drafts): keep a + 1 of the T verified positions (lengths += a + 1, GDN state half =
  * the written half with replay = a + 1 records, conv window offset = written half + a

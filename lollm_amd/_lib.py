@@ -63,6 +63,7 @@ SIGNATURES = {
                     ctypes.c_longlong, _I, _P], _I),
     "lollm_gemm_rmsnorm": ([_P, ctypes.c_longlong, _P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P,
                             ctypes.c_longlong, _I, _P], _I),
+    "lollm_greedy_accept": ([_P, _P, _I, _I, _P, _P, _P], _I),
     "lollm_spec_commit": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I,
                            _P, _P, _P, _I, _P], _I),
     "lollm_repetition_penalty": ([_P, ctypes.c_longlong, _I, _I, _I, _P, _I, _P, _I, _I, _F, _P],

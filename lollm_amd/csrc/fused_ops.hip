@@ -308,6 +308,24 @@ __global__ __launch_bounds__(256) void attn_small_kernel(
   }
 }
 
+// Greedy acceptance from the verify rows' argmax tokens (temperature 0): draft i of
+// sequence b is kept while it equals the argmax of verify row i (the draft == true_next
+// test of src/qwen3_5/mtp.py:141-155 with sample_next's argmax, src/generate.py:23-24), and
+// the next pending token is the argmax of row a (the bonus row when all k are kept).
+// One thread per sequence.
+__global__ __launch_bounds__(64) void greedy_accept_kernel(const int32_t* __restrict__ amax,
+                                                           const int32_t* __restrict__ drafts, int B,
+                                                           int k, int32_t* __restrict__ n_acc,
+                                                           int32_t* __restrict__ next_tok) {
+  const int b = blockIdx.x * 64 + threadIdx.x;
+  if (b >= B) return;
+  const int32_t* am = amax + (size_t)b * (k + 1);
+  int a = 0;
+  while (a < k && drafts[(size_t)b * k + a] == am[a]) ++a;
+  n_acc[b] = a;
+  next_tok[b] = am[a];
+}
+
 // One workgroup per sequence: the bookkeeping that ends a speculative step.
 __global__ __launch_bounds__(256) void spec_commit_kernel(
     const int32_t* __restrict__ verify_ids, const int32_t* __restrict__ n_acc,
@@ -418,6 +436,15 @@ LOLLM_API int lollm_attn_small(const void* qkv, const void* q_norm_w, const void
                      inv_freq, lengths, rope_pos, kv_len, Hq, Hkv, rotary_dim, eps,
                      scale * 1.4426950408889634f, (uint16_t*)k_cache, (uint16_t*)v_cache, max_len,
                      (uint16_t*)out);
+  return launch_status();
+}
+
+LOLLM_API int lollm_greedy_accept(const int32_t* argmax, const int32_t* drafts, int B, int k,
+                                  int32_t* n_accepted, int32_t* next_token, void* stream) {
+  if (!argmax || !n_accepted || !next_token || (k > 0 && !drafts)) return LOLLM_EINVAL;
+  if (B <= 0 || k < 0) return LOLLM_EINVAL;
+  hipLaunchKernelGGL(greedy_accept_kernel, dim3((B + 63) / 64), dim3(64), 0, (hipStream_t)stream,
+                     argmax, drafts, B, k, n_accepted, next_token);
   return launch_status();
 }
 

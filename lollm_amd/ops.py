@@ -574,6 +574,21 @@ def gdn_state(rec, rec_half, rep, replay, out=None, to_other_half=False):
     return out
 
 
+def greedy_accept(argmax, drafts, n_accepted, next_token):
+    """Greedy acceptance from the verify rows' argmax tokens (lollm_greedy_accept):
+    argmax (B, k + 1) int32, drafts (B, k) int32; writes n_accepted, next_token (B,)."""
+    B, T = argmax.shape
+    k = T - 1
+    _need(argmax, "argmax", torch.int32)
+    if k > 0:
+        _need(drafts, "drafts", torch.int32, (B, k))
+    _need(n_accepted, "n_accepted", torch.int32, (B,))
+    _need(next_token, "next_token", torch.int32, (B,))
+    rc = _lib.lib().lollm_greedy_accept(_ptr(argmax), _ptr(drafts) if k > 0 else None, B, k,
+                                        _ptr(n_accepted), _ptr(next_token), _stream())
+    _lib.check(rc, "lollm_greedy_accept")
+
+
 def spec_commit(verify_ids, n_accepted, next_token, lengths, rec_half, replay, conv_off, pending,
                 out_tokens, out_count, hidden, h_last, offset, slots, win_rows, accept_hist=None,
                 seen=None):

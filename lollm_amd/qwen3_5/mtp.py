@@ -174,6 +174,16 @@ class SpecDecoder:
         self.mtp_ws = model.attn_workspace(batch, 1, max(k, 1))
         self.draft_logits = (torch.empty(batch, k, cfg.vocab_size, dtype=torch.bfloat16, device=dev)
                              if self.draft_mode == "sample" else None)
+        # temperature 0 without a penalty: the verify rows need only their argmax, taken
+        # from the lm_head GEMM without writing the (B, 1 + k, V) logits (same grid as the
+        # logits path, so the same bits decide; set False to verify through the logits)
+        lm = model.lm_head
+        self.greedy_argmax = (temperature <= 0 and self.seen is None and lm.tiled is not None
+                              and lm.path(batch * (k + 1)) == "gemm")
+        self.verify_amax = torch.zeros(batch, k + 1, **i32)
+        if self.greedy_argmax:   # reserve its workspace before any capture
+            ops.gemm_workspace(ops._lib.lib().lollm_gemm_argmax_workspace_bytes(
+                batch * (k + 1), lm.N, lm.K, lm.grid()), dev)
         # per-draft-position index tensors (fixed across steps, so a graph can hold them)
         self.mtp_len = [torch.full((batch,), j, **i32) for j in range(k + 1)]
         self.graph = None
@@ -263,13 +273,20 @@ class SpecDecoder:
         self._draft_chain()
         verify_ids = torch.cat([self.pending.view(B, 1), self.drafts], 1)
         hidden, normed = model.hidden_states(verify_ids, cache)   # int32 ids: no widening copy
-        logits = model.lm_head(normed)
-        if self.seen is not None:
-            # position t's context holds the pending token and the drafts before t
-            ops.repetition_penalty(logits, self.seen, self.penalty, extra=self.drafts)
-        ops.spec_accept(logits, self.draft_logits, self.drafts, self.temperature, self.top_k,
-                        self.top_p, self.seed, 0, offset_dev=self.offset,
-                        workspace=self.spec_ws, n_accepted=self.n_acc, next_token=self.next_tok)
+        if self.greedy_argmax:
+            lm = model.lm_head
+            ops.gemm_argmax(normed.reshape(-1, lm.K), lm.tiled, lm.N, lm.K,
+                            out=self.verify_amax.view(-1), grid=lm.grid())
+            ops.greedy_accept(self.verify_amax, self.drafts, self.n_acc, self.next_tok)
+        else:
+            logits = model.lm_head(normed)
+            if self.seen is not None:
+                # position t's context holds the pending token and the drafts before t
+                ops.repetition_penalty(logits, self.seen, self.penalty, extra=self.drafts)
+            ops.spec_accept(logits, self.draft_logits, self.drafts, self.temperature, self.top_k,
+                            self.top_p, self.seed, 0, offset_dev=self.offset,
+                            workspace=self.spec_ws, n_accepted=self.n_acc,
+                            next_token=self.next_tok)
         ops.spec_commit(verify_ids, self.n_acc, self.next_tok, cache.lengths, cache.rec_half,
                         cache.replay, cache.conv_off, self.pending, self.out_tokens, self.out_count,
                         hidden.contiguous(), self.h_last, self.offset, cache.spec_slots,

@@ -165,6 +165,33 @@ def test_greedy_spec_decode_matches_oracle(micro, k):
     assert agreed >= 2 * n              # near-ties are rare on this model
 
 
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_greedy_verify_without_logits_matches_logits_path(micro, use_graph):
+    """Temperature 0: verifying through the lm_head argmax (lollm_gemm_argmax +
+    lollm_greedy_accept, no logits) emits exactly the tokens and accepted lengths of the
+    logits path (lollm_gemm + lollm_spec_accept), eager and replayed from a graph."""
+    model, mtp, _, cfg = micro
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    print(f"case greedy argmax verify graph={use_graph}", flush=True)
+    g = torch.Generator().manual_seed(8)
+    prompts = torch.randint(0, cfg.vocab_size, (4, 10), generator=g)
+    res = []
+    for fused in (True, False):
+        dec = SpecDecoder(model, mtp, 4, 80, k=3, temperature=0.0)
+        assert dec.greedy_argmax
+        dec.greedy_argmax = fused
+        dec.prefill(prompts.cuda())
+        dec.step()
+        if use_graph:
+            dec.capture()
+        for _ in range(8):
+            dec.replay() if use_graph else dec.step()
+        torch.cuda.synchronize()
+        res.append((dec.tokens(), dec.accept_hist.cpu().tolist()))
+    assert res[0] == res[1]
+    assert sum(res[0][1]) == 9 * 4
+
+
 @pytest.mark.parametrize("pen,draft", [(1.0, "argmax"), (1.05, "argmax"), (1.3, "sample")])
 def test_graph_replay_matches_eager(micro, pen, draft):
     model, mtp, _, cfg = micro
