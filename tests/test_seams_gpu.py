@@ -92,6 +92,38 @@ def test_sample_next_draws_bit_exact(temp, top_k, top_p, pen):
 
 
 # ----------------------------------------------------------------- cache methods
+def test_linear_state_with_replay_records_matches_refcache(micro):
+    """After a long forward (prefill: the state itself) and then a short one (T <= the
+    replay slots: the committed state is the stored state plus T replay records),
+    linear_state equals the oracle cache after the same 12 tokens (bf16 bar);
+    set_linear_state on one layer folds every layer's records first and leaves the other
+    layers' states bit for bit as they were."""
+    model, _, W, W16, cfg = micro
+    g = torch.Generator().manual_seed(14)
+    ids = torch.randint(0, cfg.vocab_size, (2, 12), generator=g)
+    cache = model.new_cache(2, 32, spec_slots=4)
+    model(ids[:, :9].cuda(), cache)
+    model(ids[:, 9:].cuda(), cache)
+    assert int(cache.replay.min()) == 3
+    _, past = R.model_forward(W, cfg, ids)
+    _, p16 = R.model_forward(W16, cfg, ids)
+    gdn = [i for i, lt in enumerate(cfg.layer_types) if lt != "full_attention"]
+    before = {}
+    for i in gdn:
+        conv, rec = cache.linear_state(i)
+        before[i] = (conv, rec)
+        c_ref, r_ref = past.linear_state(i)
+        c16, r16 = p16.linear_state(i)
+        assert (conv.float().cpu() - c_ref).abs().max() <= 2 * (c16.float() - c_ref).abs().max() + 1e-3
+        assert (rec.cpu() - r_ref).abs().max() <= 2 * (r16.float() - r_ref).abs().max() + 1e-3
+    cache.set_linear_state(gdn[0], before[gdn[0]][0], before[gdn[0]][1] * 0 + 2)
+    assert int(cache.replay.max()) == 0
+    assert bool((cache.linear_state(gdn[0])[1] == 2).all())
+    for i in gdn[1:]:
+        conv, rec = cache.linear_state(i)
+        assert torch.equal(conv, before[i][0]) and torch.equal(rec, before[i][1])
+
+
 def test_cache_methods_match_refcache(micro):
     """read_kv / linear_state after a forward equal the oracle cache's contents (bf16
     bar); set_linear_state / append_kv / advance / clone / nbytes / seen_tokens behave as
