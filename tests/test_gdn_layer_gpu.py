@@ -138,7 +138,9 @@ def check_committed_untouched(m, dev):
         assert torch.equal(rep_o[b, h], m["rep"][b, h])
 
 
-@pytest.mark.parametrize("B,T,S", [(3, 4, 4), (2, 1, 4), (2, 2, 2), (2, 5, 5), (2, 8, 8)])
+# (the last case has more replay slots than the verify form takes: the chunked
+# short-call kernel, two chunks of positions)
+@pytest.mark.parametrize("B,T,S", [(3, 4, 4), (2, 1, 4), (2, 2, 2), (2, 5, 5), (2, 8, 8), (2, 9, 10)])
 def test_gdn_layer_verify_matches_oracle(B, T, S):
     print(f"case gdn_layer B={B} T={T} S={S}", flush=True)
     m = make(B, T, S, 10 * T + B)
@@ -170,7 +172,7 @@ def commit(dev, a, W):
 
 
 @pytest.mark.parametrize("B,T1,T2,S,seed", [(3, 4, 4, 4, 1), (2, 4, 1, 4, 2), (2, 3, 5, 5, 3),
-                                            (2, 8, 8, 8, 4)])
+                                            (2, 8, 8, 8, 4), (2, 9, 10, 10, 5)])
 def test_gdn_layer_after_accepting_drafts(B, T1, T2, S, seed):
     """A verify call, a commit of a random accepted prefix a + 1 (the record replay), then
     the next call: its outputs and the states after each of its positions against the
