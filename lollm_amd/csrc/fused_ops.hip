@@ -214,8 +214,8 @@ __global__ __launch_bounds__(256) void attn_small_kernel(
     const int32_t* __restrict__ kv_len, int Hq, int Hkv, int rd, float eps, float cl2,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int max_len, uint16_t* __restrict__ out) {
   constexpr int D = 256;
-  __shared__ float red[4];
-  __shared__ float xs[D];
+  __shared__ float redn[1 + AS_MAXREP][4];   // per-wave partial sums of the 1 + n_rep norms
+  __shared__ float xsn[1 + AS_MAXREP][D];    // normed rows (k, then the query heads), for RoPE
   __shared__ float knew[D], vnew[D];
   __shared__ float qsh[AS_MAXREP][D], gsh[AS_MAXREP][D];
   const int b = blockIdx.x, kvh = blockIdx.y, d = threadIdx.x;
@@ -226,10 +226,55 @@ __global__ __launch_bounds__(256) void attn_small_kernel(
   const int pos = lengths[b];
   const int rpos = rope_pos ? rope_pos[b] : pos;
   const size_t cbase = ((size_t)b * Hkv + kvh) * max_len;
+  // every input of this (sequence, kv head) in one batch: k, v, the n_rep query heads and
+  // their gates (the heads' norms below then run side by side, not one after another)
+  const float kx = bf16_to_f32(src[(long long)Hq * 2 * D + kvh * D + d]);
+  const uint16_t vb = src[(long long)Hq * 2 * D + Hkv * D + kvh * D + d];
+  const float kw = bf16_to_f32(kn_w[d]), qw = bf16_to_f32(qn_w[d]);
+  float qx[AS_MAXREP], gx[AS_MAXREP];
+#pragma unroll
+  for (int hr = 0; hr < AS_MAXREP; ++hr) {
+    const int h = kvh * n_rep + (hr < n_rep ? hr : 0);
+    qx[hr] = bf16_to_f32(src[(long long)h * 2 * D + d]);
+    gx[hr] = bf16_to_f32(src[(long long)h * 2 * D + D + d]);
+  }
+  // the 1 + n_rep sums of squares, each with block_sum_f's order (the wave's xor tree, then
+  // the four wave sums in order), so the k row has the prologue's bits
+#pragma unroll
+  for (int v = 0; v <= AS_MAXREP; ++v) {
+    if (v > n_rep) break;
+    const float x = v == 0 ? kx : qx[v - 1];
+    float sq = x * x;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    if (lane == 0) redn[v][wave] = sq;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v <= AS_MAXREP; ++v) {
+    if (v > n_rep) break;
+    const float t = 0.f + redn[v][0] + redn[v][1] + redn[v][2] + redn[v][3];
+    const float r = rsqrtf(t / (float)D + eps);
+    const float x = v == 0 ? kx : qx[v - 1];
+    xsn[v][d] = round_bf16(x * r * (1.f + (v == 0 ? kw : qw)));  // QK-norm output (bf16 tensor)
+  }
+  __syncthreads();
+  // partial rotate-half RoPE at rpos on the first rd dims (qk_norm_rope's arithmetic)
+  float cs = 1.f, sn = 0.f;
+  const int half = rd / 2;
+  if (d < rd) {
+    const float ang = (float)rpos * inv_freq[d % half];
+    cs = round_bf16(cosf(ang));
+    sn = round_bf16(sinf(ang));
+  }
+  auto rope = [&](int v) {
+    const float xn = xsn[v][d];
+    if (d >= rd) return xn;
+    const float rot = d < half ? -xsn[v][d + half] : xsn[v][d - half];
+    return round_bf16(round_bf16(xn * cs) + round_bf16(rot * sn));
+  };
   {
-    const float y = qk_norm_rope(bf16_to_f32(src[(long long)Hq * 2 * D + kvh * D + d]),
-                                 bf16_to_f32(kn_w[d]), inv_freq, rpos, rd, eps, red, xs);
-    const uint16_t yb = f32_to_bf16(y), vb = src[(long long)Hq * 2 * D + Hkv * D + kvh * D + d];
+    const uint16_t yb = f32_to_bf16(rope(0));
     knew[d] = bf16_to_f32(yb);
     vnew[d] = bf16_to_f32(vb);
     if (pos >= 0 && pos < max_len) {
@@ -237,11 +282,11 @@ __global__ __launch_bounds__(256) void attn_small_kernel(
       vc[(cbase + pos) * D + d] = vb;
     }
   }
-  for (int hr = 0; hr < n_rep; ++hr) {
-    const int h = kvh * n_rep + hr;
-    qsh[hr][d] = qk_norm_rope(bf16_to_f32(src[(long long)h * 2 * D + d]), bf16_to_f32(qn_w[d]),
-                              inv_freq, rpos, rd, eps, red, xs);
-    gsh[hr][d] = bf16_to_f32(src[(long long)h * 2 * D + D + d]);
+#pragma unroll
+  for (int hr = 0; hr < AS_MAXREP; ++hr) {
+    if (hr >= n_rep) break;
+    qsh[hr][d] = rope(1 + hr);
+    gsh[hr][d] = gx[hr];
   }
   __syncthreads();
   int L = kv_len[b];
