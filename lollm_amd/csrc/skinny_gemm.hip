@@ -14,8 +14,8 @@
 // gate and up rows 8 by 8 (tile t = gate rows 8t..8t+7, then up rows 8t..8t+7) so a lane
 // and its partner 32 lanes away hold gate and up of the same output columns.
 //
-// Work decomposition: a group = 64 output columns (4 n-tiles), a unit = (group, 128-k
-// stage).  Units are laid end to end group-major and dealt out in equal contiguous ranges
+// Work decomposition: a group = 64 output columns (4 n-tiles; 96 where that leaves no
+// group cut, gemm_group_tiles), a unit = (group, 128-k stage).  Units are laid end to end group-major and dealt out in equal contiguous ranges
 // to a fixed grid (one workgroup per CU), so every workgroup streams the same number of
 // weight bytes whatever N is (N / 64 groups over 256 CUs would run uneven rounds).  Two
 // kernels: gemm_ksplit_kernel for at most 32 rows (operands straight to registers, each
@@ -165,7 +165,8 @@ __device__ __forceinline__ void gm_emit(const GemmArgs& a, const gm_f32x4 (&v)[M
 }
 
 // The product for 33..64 rows, warp-specialised.  Waves 4 and 5 only stream weights:
-// each copies its half of a unit's 16 weight blocks (2 n-tiles x 4 k-steps, 1 KB each)
+// each copies its half of a unit's weight blocks (2 n-tiles x 4 k-steps, 1 KB each, for
+// 64-column groups)
 // straight into LDS with 16-byte DMA loads (global_load_lds_dwordx4, non-temporal) into a
 // ring of GS_WSLOTS slots, GS_WSLOTS - 1 units ahead; wave 6 copies the unit's 64-row
 // activation tile (128 k) the same way into a ring of GS_ASLOTS slots.  Only these
@@ -193,13 +194,15 @@ constexpr int GS_SLOT = 16384;
 constexpr int GS_THREADS = 448;
 constexpr int GS_NT = 2;                    // cache policy of the weight DMA: non-temporal
 
+template <int NT>
 __device__ __forceinline__ void gs_emit_tile(const GemmArgs& a, const gm_f32x4& v, int i, int j,
                                              int g, bool whole, int w, int lane) {
   const int l16 = lane & 15, g4 = lane >> 4;
   const int m = 16 * i + l16;
+  const int t = NT * g + j;                  // n-tile of the tiled weight
   if (whole) {
     if (a.epi == GM_EPI_ARGMAX) {
-      const int col = GM_COLS * g + 16 * j + 4 * g4;
+      const int col = 16 * t + 4 * g4;
       uint64_t best = gm_key(v[0], col);
 #pragma unroll
       for (int e = 1; e < 4; ++e) {
@@ -208,7 +211,7 @@ __device__ __forceinline__ void gs_emit_tile(const GemmArgs& a, const gm_f32x4& 
       }
       best = gm_max_xor(best, 16);
       best = gm_max_xor(best, 32);
-      if (g4 == 0 && m < a.M) a.am[(size_t)m * (a.N / 16) + 4 * g + j] = best;
+      if (g4 == 0 && m < a.M) a.am[(size_t)m * (a.N / 16) + t] = best;
     } else if (a.epi == GM_EPI_SWIGLU) {
       float other[4];
 #pragma unroll
@@ -217,20 +220,21 @@ __device__ __forceinline__ void gs_emit_tile(const GemmArgs& a, const gm_f32x4& 
         float y[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[e] = round_bf16(gm_silu_bf16(v[e]) * round_bf16(other[e]));
-        const int col = 8 * (4 * g + j) + 4 * g4;
+        const int col = 8 * t + 4 * g4;
         *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
             make_uint2((uint32_t)f32_to_bf16(y[0]) | ((uint32_t)f32_to_bf16(y[1]) << 16),
                        (uint32_t)f32_to_bf16(y[2]) | ((uint32_t)f32_to_bf16(y[3]) << 16));
       }
     } else if (m < a.M) {
-      const int col = GM_COLS * g + 16 * j + 4 * g4;
+      const int col = 16 * t + 4 * g4;
       *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
           make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
                      (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
     }
-  } else {
+  } else if constexpr (NT == 4) {
     // the piece of a cut group in the layout the merge kernels read: (16 mt) x 64 fp32
     // with mt = ceil(M / 16) m-tiles, so an m-tile made only of padding rows is skipped
+    // (wider groups are never cut: the host gives them a grid that divides them)
     const int mt = (a.M + 15) / 16;
     if (i >= mt) return;
     float* pp = a.part + ((size_t)w + g) * ((size_t)mt * 16 * GM_COLS);
@@ -240,10 +244,22 @@ __device__ __forceinline__ void gs_emit_tile(const GemmArgs& a, const gm_f32x4& 
   }
 }
 
+// NT n-tiles per group: 4 (64 columns) in general; 6 (96 columns) where 96-column groups
+// divide evenly over the grid and 64-column ones would be cut (the MLP gate|up of the
+// 4096-hidden model: 256 groups, one per CU, so no merge launch follows; the attention
+// q|gate|k|v: 192).  A wide unit is 24 KB of weights against the same 16 KB activation
+// tile, so the weight ring holds 4 units instead of 5 to stay within LDS.  Each output
+// tile accumulates the same k-steps in the same order for either width, so a group
+// finished by one workgroup has the same bits at both widths.
+template <int NT>
 __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(1024))) unsigned char lds[(GS_WSLOTS + GS_ASLOTS) * GS_SLOT];
+  constexpr int WSLOTS = NT == 4 ? GS_WSLOTS : 4;
+  constexpr int WSLOT = NT * GM_KS * 1024;   // bytes of one unit's weight blocks
+  constexpr int HALF = NT / 2;               // n-tiles per loader wave and per MFMA wave
+  static_assert(NT % 2 == 0 && WSLOTS * WSLOT + GS_ASLOTS * GS_SLOT <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[WSLOTS * WSLOT + GS_ASLOTS * GS_SLOT];
   unsigned char* wring = lds;
-  unsigned char* aring = lds + GS_WSLOTS * GS_SLOT;
+  unsigned char* aring = lds + WSLOTS * WSLOT;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int w = blockIdx.x;
   const int u0 = gm_begin(a.U, w, a.nw), u1 = gm_begin(a.U, w + 1, a.nw);
@@ -254,11 +270,11 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
     auto issue = [&](int u) {
       const int uu = u < u1 ? u : u1 - 1;
       const int g = uu / a.SK, st = uu - g * a.SK;
-      unsigned char* sb = wring + ((u - u0) % GS_WSLOTS) * GS_SLOT;
+      unsigned char* sb = wring + ((u - u0) % WSLOTS) * WSLOT;
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int j = 2 * lw + jj;
-        const uint16_t* src = a.Wt + ((size_t)(4 * g + j) * kt + (size_t)st * GM_KS) * 512 + lane * 8;
+      for (int jj = 0; jj < HALF; ++jj) {
+        const int j = HALF * lw + jj;
+        const uint16_t* src = a.Wt + ((size_t)(NT * g + j) * kt + (size_t)st * GM_KS) * 512 + lane * 8;
 #pragma unroll
         for (int q = 0; q < GM_KS; ++q)
           __builtin_amdgcn_global_load_lds((gs_global_t*)(src + q * 512),
@@ -266,11 +282,11 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
       }
     };
 #pragma unroll
-    for (int p = 0; p < GS_WSLOTS - 1; ++p) issue(u0 + p);
+    for (int p = 0; p < WSLOTS - 1; ++p) issue(u0 + p);
     for (int u = u0; u < u1; ++u) {
-      // unit u has landed once at most GS_WSLOTS - 2 younger units (8 DMAs each) remain
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"((GS_WSLOTS - 2) * 8) : "memory");
-      issue(u + GS_WSLOTS - 1);
+      // unit u has landed once at most WSLOTS - 2 younger units (HALF * 4 DMAs each) remain
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"((WSLOTS - 2) * HALF * GM_KS) : "memory");
+      issue(u + WSLOTS - 1);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     return;
@@ -298,23 +314,23 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
     return;
   }
   const int wn = wave & 1, wm = wave >> 1, l16 = lane & 15, g4 = lane >> 4;
-  gm_f32x4 acc[2][2];
+  gm_f32x4 acc[2][HALF];
 #pragma unroll
   for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) acc[ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int jj = 0; jj < HALF; ++jj) acc[ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
   bool whole_from_start = (u0 % a.SK) == 0;
   for (int u = u0; u < u1; ++u) {
     // this wave's reads of the previous unit are complete before the loaders may refill it
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const unsigned char* wb = wring + ((u - u0) % GS_WSLOTS) * GS_SLOT;
+    const unsigned char* wb = wring + ((u - u0) % WSLOTS) * WSLOT;
     const unsigned char* ab = aring + ((u - u0) % GS_ASLOTS) * GS_SLOT;
 #pragma unroll
     for (int q = 0; q < GM_KS; ++q) {
-      gm_bf16x8 wf[2], af[2];
+      gm_bf16x8 wf[HALF], af[2];
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj)
-        wf[jj] = *reinterpret_cast<const gm_bf16x8*>(wb + ((2 * wn + jj) * GM_KS + q) * 1024 + lane * 16);
+      for (int jj = 0; jj < HALF; ++jj)
+        wf[jj] = *reinterpret_cast<const gm_bf16x8*>(wb + ((HALF * wn + jj) * GM_KS + q) * 1024 + lane * 16);
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii) {
         const int row = 16 * (2 * wm + ii) + l16, c = q * 4 + g4;
@@ -323,7 +339,7 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
+        for (int jj = 0; jj < HALF; ++jj)
           acc[ii][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[jj], af[ii], acc[ii][jj], 0, 0, 0);
     }
     const int st = u % a.SK;
@@ -333,8 +349,8 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          gs_emit_tile(a, acc[ii][jj], 2 * wm + ii, 2 * wn + jj, g, whole, w, lane);
+        for (int jj = 0; jj < HALF; ++jj) {
+          gs_emit_tile<NT>(a, acc[ii][jj], 2 * wm + ii, HALF * wn + jj, g, whole, w, lane);
           acc[ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
         }
       whole_from_start = true;
@@ -693,9 +709,18 @@ LOLLM_API long long lollm_gemm_workspace_bytes(int M, int N, int K, int grid) {
 }
 
 // Validates the arguments common to the GEMM entry points and launches the main kernel.
+// n-tiles per group of a lollm_gemm call: 6 (96 columns) when the 33..64-row kernel runs,
+// the 96-column groups divide evenly over the grid and the 64-column ones would not (so
+// the call needs no merge launch); else 4.  A pure function of (M, N, grid).
+static int gemm_group_tiles(int M, int N, int nw) {
+  if (M > 32 && N % 96 == 0 && (N / 96) % nw == 0 && (N / GM_COLS) % nw != 0) return 6;
+  return 4;
+}
+
 static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, void* C,
                      long long ldc, int M, int N, int K, int epilogue, void* workspace,
-                     long long workspace_bytes, int grid, int rowmajor, hipStream_t st) {
+                     long long workspace_bytes, int grid, int rowmajor, hipStream_t st,
+                     bool allow_wide = false) {
   if (!A || !Wt || !C || !workspace) return LOLLM_EINVAL;
   if (!gemm_shape_ok(M, N, K, epilogue)) return LOLLM_EUNSUPPORTED;
   const long long outc = epilogue == GM_EPI_SWIGLU ? N / 2 : N;
@@ -708,7 +733,8 @@ static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, 
   a.A = (const uint16_t*)A; a.Wt = (const uint16_t*)Wt; a.C = (uint16_t*)C;
   a.part = (float*)workspace;
   a.lda = lda; a.ldc = ldc;
-  a.M = M; a.N = N; a.K = K; a.G = N / GM_COLS; a.SK = K / GM_KC; a.nw = nw; a.epi = epilogue;
+  const int nt = allow_wide ? gemm_group_tiles(M, N, nw) : 4;
+  a.M = M; a.N = N; a.K = K; a.G = N / (16 * nt); a.SK = K / GM_KC; a.nw = nw; a.epi = epilogue;
   a.U = a.G * a.SK;
   a.rowmajor = rowmajor;
   a.am = nullptr;
@@ -718,7 +744,10 @@ static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, 
     case 1: hipLaunchKernelGGL(gemm_ksplit_kernel<1>, dim3(nw), dim3(256), 0, st, a); break;
     case 2: hipLaunchKernelGGL(gemm_ksplit_kernel<2>, dim3(nw), dim3(256), 0, st, a); break;
     default:   // 33..64 rows: the warp-specialised stream (64-row tiles, rows past M clamped)
-      hipLaunchKernelGGL(gemm_stream_kernel, dim3(nw), dim3(GS_THREADS), 0, st, a);
+      if (nt == 6)
+        hipLaunchKernelGGL(gemm_stream_kernel<6>, dim3(nw), dim3(GS_THREADS), 0, st, a);
+      else
+        hipLaunchKernelGGL(gemm_stream_kernel<4>, dim3(nw), dim3(GS_THREADS), 0, st, a);
       break;
   }
   return launch_status();
@@ -730,9 +759,11 @@ LOLLM_API int lollm_gemm(const void* A, long long lda, const void* Wt, void* C, 
   if (epilogue != GM_EPI_NONE && epilogue != GM_EPI_SWIGLU) return LOLLM_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   GemmArgs a;
-  int rc = gemm_main(a, A, lda, Wt, C, ldc, M, N, K, epilogue, workspace, workspace_bytes, grid, 0, st);
+  int rc = gemm_main(a, A, lda, Wt, C, ldc, M, N, K, epilogue, workspace, workspace_bytes, grid, 0, st,
+                     true);
   if (rc) return rc;
-  // every range a whole number of whole groups (grid divides the groups): nothing to merge
+  // every range a whole number of whole groups (grid divides the groups, always so for
+  // 96-column groups): nothing to merge
   if (a.G % a.nw == 0) return LOLLM_OK;
   hipLaunchKernelGGL(gemm_fixup_kernel, dim3(a.G, (M + 15) / 16), dim3(256), 0, st, a);
   return launch_status();

@@ -38,12 +38,20 @@ def gemm_path(N, K, epilogue, rows, tiled=True):
     return "gemm" if tiled and rows <= ops.GEMM_MAX_ROWS else "blas"
 
 
-def gemm_grid(N, cus):
-    """Workgroups of a lollm_gemm call with N output columns on a device with `cus`
-    CUs: one per 64-column group when that covers 3/4 of the CUs or more, else one per
-    CU."""
+def gemm_grid(N, cus, rows=ops.GEMM_MAX_ROWS):
+    """Workgroups of a lollm_gemm call with N output columns and `rows` rows on a device
+    with `cus` CUs: one per 64-column group when that covers 3/4 of the CUs or more; for
+    33..64 rows, else one per 96-column group on the same condition (lollm_gemm then
+    takes 96-column groups, none cut: the attention q|gate|k|v of the 4096-hidden model,
+    192 groups; its MLP gate|up, 256 = one per CU); else one per CU."""
     groups = N // 64
-    return groups if 4 * groups >= 3 * cus and groups <= cus else cus
+    if 4 * groups >= 3 * cus and groups <= cus:
+        return groups
+    if rows > 32 and N % 96 == 0:
+        wide = N // 96
+        if 4 * wide >= 3 * cus and wide <= cus:
+            return wide
+    return cus
 
 
 class Projection:
@@ -63,11 +71,11 @@ class Projection:
     def workspace_bytes(self, rows=ops.GEMM_MAX_ROWS):
         if self.tiled is None:
             return 0
-        return max(ops.gemm_workspace_bytes(rows, self.N, self.K, self.grid()),
+        return max(ops.gemm_workspace_bytes(rows, self.N, self.K, self.grid(rows)),
                    ops.gemm_workspace_bytes(rows, self.N, self.K, _cus()))
 
-    def grid(self):
-        return gemm_grid(self.N, _cus())
+    def grid(self, rows=ops.GEMM_MAX_ROWS):
+        return gemm_grid(self.N, _cus(), rows)
 
     def path(self, rows):
         return gemm_path(self.N, self.K, self.epilogue, rows, self.tiled is not None)
@@ -84,7 +92,7 @@ class Projection:
         rows = x.numel() // self.K
         if self.path(rows) == "blas":
             return self._blas(x)
-        return ops.gemm(x, self.tiled, self.N, self.K, self.epilogue, grid=self.grid())
+        return ops.gemm(x, self.tiled, self.N, self.K, self.epilogue, grid=self.grid(rows))
 
     def add_norm(self, x, residual, norm):
         """The projection feeding the residual stream with the add and the next RMSNorm
@@ -93,7 +101,7 @@ class Projection:
         kernel) when the path is lollm_gemm and the shape fits it, else the projection
         followed by lollm_rmsnorm."""
         rows = x.numel() // self.K
-        g1 = self.grid()
+        g1 = self.grid(rows)
         if (self.path(rows) == "gemm" and self.epilogue == ops.GEMM_NONE
                 and ops.gemm_rmsnorm_supported(rows, self.N, self.K, g1)):
             return ops.gemm_rmsnorm(x, self.tiled, self.N, self.K, residual, norm.weight, norm.eps,

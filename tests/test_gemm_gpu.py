@@ -54,6 +54,32 @@ def test_gemm_pieces_equal_whole_groups(M):
     torch.testing.assert_close(a, b, rtol=8e-3, atol=8e-3 * a.abs().max().item())
 
 
+@pytest.mark.parametrize("M", [33, 40, 64])
+@pytest.mark.parametrize("N,K,grid", [(1536, 1024, 16), (2304, 512, 8), (18432, 256, 192)])
+@pytest.mark.parametrize("epi", [0, 1])
+def test_gemm_wide_groups_equal_whole_groups(M, N, K, grid, epi):
+    """33..64 rows on a grid that divides the 96-column groups but not the 64-column ones
+    (N = 1536 on 16 workgroups, 2304 on 8: three groups each, the attention q|gate|k|v
+    width on 192): lollm_gemm takes 96-column groups, none cut, no merge launch.  Each
+    output tile sums the same k-steps in the same order as with 64-column groups
+    finished whole (grid 1), so the two are bit-identical, with and without the SwiGLU
+    epilogue, and both match the oracle."""
+    from lollm_amd import ops
+    print(f"case gemm wide M={M} N={N} K={K} grid={grid} epi={epi}", flush=True)
+    x, W = case(M, N, K, seed=N + K + M + epi)
+    assert (N // 96) % grid == 0 and (N // 64) % grid != 0
+    Wt = ops.gemm_tile_weights(W.cuda(), epi)
+    a = ops.gemm(x.cuda(), Wt, N, K, epi, grid=grid)
+    b = ops.gemm(x.cuda(), Wt, N, K, epi, grid=1)
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), b.cpu())
+    y = R.linear(x.float(), W.float())
+    if epi == ops.GEMM_SWIGLU:
+        gu = y.bfloat16()
+        y = (F.silu(gu[:, :N // 2]) * gu[:, N // 2:]).float()
+    close(a, y)
+
+
 @pytest.mark.parametrize("M,grid", [(64, 0), (16, 0), (5, 1), (64, 1024)])
 def test_gemm_swiglu_epilogue(M, grid):
     """[gate; up] with silu(gate) * up fused (blocks.py:341-342), against the oracle's
