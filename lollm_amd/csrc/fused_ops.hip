@@ -28,6 +28,15 @@ __device__ __forceinline__ void rms_row(const uint16_t* __restrict__ x_row,
   const uint4* h4 = h_row ? reinterpret_cast<const uint4*>(h_row) : nullptr;
   const int n8 = H / 8;
   constexpr int MAXV = RMS_CHUNKS;  // H <= 8192
+  // the norm weights are loaded with the row, not after the reduction: one memory round
+  // trip per launch instead of two
+  const uint4* w4 = reinterpret_cast<const uint4*>(w);
+  uint4 wv[MAXV];
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int c = threadIdx.x + i * RMS_THREADS;
+    wv[i] = c < n8 ? w4[c] : make_uint4(0, 0, 0, 0);
+  }
   float v[MAXV][8];
   float ss = 0.f;
 #pragma unroll
@@ -56,12 +65,11 @@ __device__ __forceinline__ void rms_row(const uint16_t* __restrict__ x_row,
     }
   }
   const float r = rms_rstd(ss, red, H, eps);
-  const uint4* w4 = reinterpret_cast<const uint4*>(w);
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     const int c = threadIdx.x + i * RMS_THREADS;
     if (c < n8) {
-      uint4 wu = w4[c];
+      const uint4 wu = wv[i];
       uint32_t wd[4] = {wu.x, wu.y, wu.z, wu.w};
       uint32_t od[4];
 #pragma unroll
@@ -136,12 +144,12 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
 // [Hq, Hq + Hkv) key heads, [Hq + Hkv, Hq + 2 Hkv) value heads.  D == 256: one
 // element per thread.
 // QK-norm (1 + w) of one 256-value head vector (thread d holds x) followed by the partial
-// rotate-half RoPE at position rpos (blocks.py:166-183,221-227); returns thread d's output,
-// a bf16 value.  Shared by the prologue and the short-cache attention so both give the
-// same bits.  (red and xs are reused by the next call only after the barriers inside
-// block_sum_f.)
-__device__ __forceinline__ float qk_norm_rope(float x, float wv, const float* __restrict__ inv_freq,
-                                              int rpos, int rd, float eps, float* red, float* xs) {
+// rotate-half RoPE at position rpos (blocks.py:166-183,221-227), freq = inv_freq[d % (rd / 2)]
+// for d < rd; returns thread d's output, a bf16 value.  The short-cache attention repeats
+// this arithmetic so both give the same bits.  (red and xs are reused by the next call
+// only after the barriers inside block_sum_f.)
+__device__ __forceinline__ float qk_norm_rope(float x, float wv, float freq, int rpos, int rd,
+                                              float eps, float* red, float* xs) {
   constexpr int D = 256;
   const int d = threadIdx.x;
   const float r = rsqrtf(block_sum_f<256>(x * x, red) / (float)D + eps);
@@ -150,8 +158,8 @@ __device__ __forceinline__ float qk_norm_rope(float x, float wv, const float* __
   __syncthreads();
   float y = xn;
   if (d < rd) {
-    const int half = rd / 2, i = d % half;
-    const float ang = (float)rpos * inv_freq[i];
+    const int half = rd / 2;
+    const float ang = (float)rpos * freq;
     const float c = round_bf16(cosf(ang)), s = round_bf16(sinf(ang));
     const float rot = d < half ? -xs[d + half] : xs[d - half];
     y = round_bf16(round_bf16(xn * c) + round_bf16(rot * s));
@@ -184,7 +192,9 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
   const bool is_q = slot < Hq;
   const uint16_t* xin = is_q ? src + (long long)slot * 2 * D : src + (long long)Hq * 2 * D + (slot - Hq) * D;
   if (is_q) gate_out[((long long)bt * Hq + slot) * D + d] = src[(long long)slot * 2 * D + D + d];
-  const float y = qk_norm_rope(bf16_to_f32(xin[d]), bf16_to_f32((is_q ? qn_w : kn_w)[d]), inv_freq,
+  // inv_freq[d % (rd / 2)] is loaded with the row, not after the norm's reduction
+  const float freq = d < rd ? inv_freq[d % (rd / 2)] : 0.f;
+  const float y = qk_norm_rope(bf16_to_f32(xin[d]), bf16_to_f32((is_q ? qn_w : kn_w)[d]), freq,
                                rpos, rd, eps, red, xs);
   if (is_q) {
     q_out[((long long)bt * Hq + slot) * D + d] = f32_to_bf16(y);
@@ -379,29 +389,33 @@ __global__ __launch_bounds__(256) void spec_commit_kernel(
     int32_t* pending, int32_t* out_tokens, int32_t* out_count, int cap,
     const uint16_t* __restrict__ hidden, uint16_t* __restrict__ h_last, int H, int T, int S,
     int W, long long* offset, int* hist, uint32_t* seen, int words) {
-  const int b = blockIdx.x;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  // every bookkeeping value is loaded before any store (the stores may alias the loads
+  // as far as the compiler knows, which would otherwise order them one round trip each);
+  // thread i < T holds verified position i
+  const int len = lengths[b], rh = rec_half[b], co = conv_off[b], c = out_count[b];
+  const int nt = next_tok[b];
+  const int vid = tid < T ? verify_ids[b * T + tid] : 0;
   int a = n_acc[b];
   a = a < 0 ? 0 : (a > T - 1 ? T - 1 : a);
   const uint4* src = reinterpret_cast<const uint4*>(hidden + ((size_t)b * T + a) * H);
   uint4* dst = reinterpret_cast<uint4*>(h_last + (size_t)b * H);
-  for (int i = threadIdx.x; i < H / 8; i += 256) dst[i] = src[i];
-  if (threadIdx.x == 0) {
-    lengths[b] += a + 1;                           // keep a + 1 of the T positions
-    rec_half[b] = (rec_half[b] & 1) ^ 1;            // the half the forward wrote,
+  for (int i = tid; i < H / 8; i += 256) dst[i] = src[i];
+  __syncthreads();   // every thread's loads of this sequence's counters precede the stores
+  // keep a + 1 of the T positions
+  if (tid <= a && c + tid < cap) out_tokens[(size_t)b * cap + c + tid] = vid;
+  if (seen && tid >= 1 && tid <= a + 1) {
+    // the repetition-penalty context: accepted drafts and the new pending token
+    const int t = tid <= a ? vid : nt;
+    if (t >= 0 && t < 32 * words) atomicOr(&seen[(size_t)b * words + (t >> 5)], 1u << (t & 31));
+  }
+  if (tid == 0) {
+    lengths[b] = len + a + 1;
+    rec_half[b] = (rh & 1) ^ 1;                     // the half the forward wrote,
     replay[b] = a + 1;                              // whose first a + 1 records are kept
-    conv_off[b] = (conv_off[b] >= W ? 0 : W) + a + 1;
-    const int c = out_count[b];
-    for (int i = 0; i <= a; ++i)
-      if (c + i < cap) out_tokens[(size_t)b * cap + c + i] = verify_ids[b * T + i];
+    conv_off[b] = (co >= W ? 0 : W) + a + 1;
     out_count[b] = c + a + 1;
-    pending[b] = next_tok[b];
-    if (seen) {   // the repetition-penalty context: accepted drafts and the new pending token
-      uint32_t* sb = seen + (size_t)b * words;
-      for (int i = 1; i <= a + 1; ++i) {
-        const int t = i <= a ? verify_ids[b * T + i] : next_tok[b];
-        if (t >= 0 && t < 32 * words) atomicOr(&sb[t >> 5], 1u << (t & 31));
-      }
-    }
+    pending[b] = nt;
     if (hist) atomicAdd(&hist[a], 1);
     if (b == 0) offset[0] += 1;
   }
@@ -504,6 +518,7 @@ LOLLM_API int lollm_spec_commit(const int32_t* verify_ids, const int32_t* n_acce
       !pending || !out_tokens || !out_count || !hidden || !h_last || !offset)
     return LOLLM_EINVAL;
   if (B <= 0 || T <= 0 || H <= 0 || out_cap <= 0 || slots < T || win_rows <= 0) return LOLLM_EINVAL;
+  if (T > 255) return LOLLM_EUNSUPPORTED;   // one thread per position and the pending token
   if (H % 8) return LOLLM_EUNSUPPORTED;
   if (seen && seen_words <= 0) return LOLLM_EINVAL;
   hipLaunchKernelGGL(spec_commit_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, verify_ids,

@@ -588,15 +588,24 @@ __global__ __launch_bounds__(RMS_THREADS) void gemm_norm_kernel(GemmArgs a,
   __shared__ int own[2 * GM_NORM_MAXG];
   __shared__ float red[RMS_THREADS / 64];
   const int m = blockIdx.x, tid = threadIdx.x;
+  const int n8 = a.N / 8;
+  const size_t piece = (size_t)((a.M + 15) / 16) * 16 * GM_COLS;
+  const size_t row = (size_t)m * a.N;
+  constexpr int MAXV = RMS_CHUNKS;
+  // the residual and the norm weights are loaded first, with the pieces, not after the
+  // sums and the reduction: one memory round trip per launch
+  uint4 wv[MAXV], hv[MAXV];
+#pragma unroll
+  for (int ci = 0; ci < MAXV; ++ci) {
+    const int c = tid + RMS_THREADS * ci;
+    wv[ci] = c < n8 ? *reinterpret_cast<const uint4*>(w + 8 * c) : make_uint4(0, 0, 0, 0);
+    hv[ci] = c < n8 ? *reinterpret_cast<const uint4*>(res + row + 8 * c) : make_uint4(0, 0, 0, 0);
+  }
   for (int g = tid; g < a.G; g += RMS_THREADS) {
     own[2 * g] = gm_owner(a.U, g * a.SK, a.nw);
     own[2 * g + 1] = gm_owner(a.U, g * a.SK + a.SK - 1, a.nw);
   }
   __syncthreads();
-  const int n8 = a.N / 8;
-  const size_t piece = (size_t)((a.M + 15) / 16) * 16 * GM_COLS;
-  const size_t row = (size_t)m * a.N;
-  constexpr int MAXV = RMS_CHUNKS;
   float v[MAXV][8];
   float ss = 0.f;
 #pragma unroll
@@ -636,7 +645,7 @@ __global__ __launch_bounds__(RMS_THREADS) void gemm_norm_kernel(GemmArgs a,
 #pragma unroll
         for (int e = 0; e < 8; ++e) cv[e] = round_bf16(sv[e]);
       }
-      const uint4 h = *reinterpret_cast<const uint4*>(res + row + 8 * c);
+      const uint4 h = hv[ci];
       const uint32_t hd[4] = {h.x, h.y, h.z, h.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -657,7 +666,7 @@ __global__ __launch_bounds__(RMS_THREADS) void gemm_norm_kernel(GemmArgs a,
   for (int ci = 0; ci < MAXV; ++ci) {
     const int c = tid + RMS_THREADS * ci;
     if (c < n8) {
-      const uint4 wu = *reinterpret_cast<const uint4*>(w + 8 * c);
+      const uint4 wu = wv[ci];
       const uint32_t wd[4] = {wu.x, wu.y, wu.z, wu.w};
       uint32_t od[4];
 #pragma unroll
