@@ -244,7 +244,9 @@ int lollm_gemm_argmax(const void* A, long long lda, const void* Wt, int M, int N
  * `x = x + mlp(...)` feeding the next layer's input_layernorm or the final norm.
  *
  * C (M, N) bf16 scratch; residual, x_out, y (M, N) bf16 contiguous (x_out may alias
- * residual); norm_w (N) bf16; workspace as lollm_gemm.  Supported: N <= 8192 and at
+ * residual; residual NULL: x_out = bf16(x W^T), no add -- the MTP fc followed by the MTP
+ * layer's input_layernorm, src/qwen3_5/mtp.py:61-73); norm_w (N) bf16; workspace as
+ * lollm_gemm.  Supported: N <= 8192 and at
  * least as many (64-column, 128-k) units as workgroups, else LOLLM_EUNSUPPORTED. */
 int lollm_gemm_rmsnorm(const void* A, long long lda, const void* Wt, int M, int N, int K,
                        const void* residual, const void* norm_w, float eps, void* C, void* x_out,

@@ -99,71 +99,6 @@ __global__ void gemm_tile_kernel(const uint16_t* __restrict__ W, uint16_t* __res
   *reinterpret_cast<uint4*>(Wt + blk * 512 + L * 8) = v;
 }
 
-// A group's result (lane holds, for m-tile i, rows m = 16 i + l16 and tiled columns
-// 4 g4 .. 4 g4 + 3 of n-tile 4 g + wave): with the epilogue when the workgroup covered
-// the whole group, else as the workgroup's fp32 piece.
-template <int MT>
-__device__ __forceinline__ void gm_emit(const GemmArgs& a, const gm_f32x4 (&v)[MT], int g, bool whole,
-                                        int w, int wave, int lane) {
-  const int l16 = lane & 15, g4 = lane >> 4;
-  if (whole) {
-    if (a.epi == GM_EPI_ARGMAX) {
-#pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const int m = 16 * i + l16, col = GM_COLS * g + 16 * wave + 4 * g4;
-        uint64_t best = gm_key(v[i][0], col);
-#pragma unroll
-        for (int j = 1; j < 4; ++j) {
-          const uint64_t k2 = gm_key(v[i][j], col + j);
-          best = k2 > best ? k2 : best;
-        }
-        best = gm_max_xor(best, 16);
-        best = gm_max_xor(best, 32);
-        if (g4 == 0 && m < a.M) a.am[(size_t)m * (a.N / 16) + 4 * g + wave] = best;
-      }
-    } else if (a.epi == GM_EPI_SWIGLU) {
-      // partner lane (g4 ^ 2) holds the other half of the same output columns
-#pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        float other[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) other[j] = __shfl_xor(v[i][j], 32, 64);
-        const int m = 16 * i + l16;
-        if (g4 < 2 && m < a.M) {
-          float y[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) y[j] = round_bf16(gm_silu_bf16(v[i][j]) * round_bf16(other[j]));
-          const int col = 8 * (4 * g + wave) + 4 * g4;
-          *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
-              make_uint2((uint32_t)f32_to_bf16(y[0]) | ((uint32_t)f32_to_bf16(y[1]) << 16),
-                         (uint32_t)f32_to_bf16(y[2]) | ((uint32_t)f32_to_bf16(y[3]) << 16));
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const int m = 16 * i + l16;
-        if (m < a.M) {
-          const int col = GM_COLS * g + 16 * wave + 4 * g4;
-          *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
-              make_uint2((uint32_t)f32_to_bf16(v[i][0]) | ((uint32_t)f32_to_bf16(v[i][1]) << 16),
-                         (uint32_t)f32_to_bf16(v[i][2]) | ((uint32_t)f32_to_bf16(v[i][3]) << 16));
-        }
-      }
-    }
-  } else {
-    // a piece: the raw fp32 sums of the group's 64 tiled columns, slot w + g (pieces
-    // are ordered in both w and g, so the slot is unique); padding rows included
-    float* pp = a.part + ((size_t)w + g) * ((size_t)MT * 16 * GM_COLS);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const size_t off = a.rowmajor ? (size_t)(16 * i + l16) * GM_COLS + 16 * wave + 4 * g4
-                                    : (((size_t)i * 4 + wave) * 64 + lane) * 4;
-      *reinterpret_cast<float4*>(pp + off) = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
-    }
-  }
-}
-
 // The product for 33..64 rows, warp-specialised.  Waves 4 and 5 only stream weights:
 // each copies its half of a unit's weight blocks (2 n-tiles x 4 k-steps, 1 KB each, for
 // 64-column groups)
@@ -360,18 +295,18 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
 
 
 // The same product for at most 32 rows: each wave takes one k-step of every unit for all
-// 4 n-tiles of the group, so it reads its MFMA operands straight from memory -- weights
-// (4 blocks, one per n-tile) and activations (one 16-row x 64 B chunk per m-tile) -- into
+// NT n-tiles of the group, so it reads its MFMA operands straight from memory -- weights
+// (NT blocks, one per n-tile) and activations (one 16-row x 64 B chunk per m-tile) -- into
 // a register ring 4 units deep, with no LDS staging and no barrier in the unit loop.
 // At a group's end the 4 waves' k-quarters are summed through LDS in a fixed order
-// (wave 0 .. 3) and emitted as above.  The activation chunks are half cache lines (every
+// (wave 0 .. 3) and emitted as above, n-tile j by wave j % 4.  The activation chunks are half cache lines (every
 // line is read by two waves), which costs more than the LDS staging at 64 rows; at 16
 // and 32 rows, with one workgroup per CU, this form measured 3-10% faster.
-template <int MT>
+template <int MT, int NT>
 __global__ __launch_bounds__(256, 2) void gemm_ksplit_kernel(GemmArgs a) {
   typedef unsigned int v4u __attribute__((ext_vector_type(4)));
   // the waves' partial sums at a group's end: (n-tile j, wave v, m-tile i) x 64 lanes
-  __shared__ __attribute__((aligned(16))) gm_f32x4 red[4 * 4 * MT * 64];
+  __shared__ __attribute__((aligned(16))) gm_f32x4 red[NT * 4 * MT * 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
   const int w = blockIdx.x;
@@ -385,20 +320,20 @@ __global__ __launch_bounds__(256, 2) void gemm_ksplit_kernel(GemmArgs a) {
     const int r = min(16 * i + l16, a.M - 1);   // padding rows re-read the last row
     alane[i] = a.A + (size_t)r * a.lda + 32 * wave + 8 * g4;
   }
-  v4u wr[GM_P][4], ar[GM_P][MT];
-  // weights of unit u: n-tiles 4 g + j, k-step 4 st + wave; activations: k-step 4 st + wave
+  v4u wr[GM_P][NT], ar[GM_P][MT];
+  // weights of unit u: n-tiles NT g + j, k-step 4 st + wave; activations: k-step 4 st + wave
   auto load = [&](v4u* dw, v4u* da, int u) {
     const int g = u / a.SK, st = u - g * a.SK;
-    const uint16_t* p = wlane + ((size_t)4 * g * kt + (size_t)st * GM_KS) * 512;
+    const uint16_t* p = wlane + ((size_t)NT * g * kt + (size_t)st * GM_KS) * 512;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NT; ++j)
       dw[j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p + (size_t)j * kt * 512));
 #pragma unroll
     for (int i = 0; i < MT; ++i) da[i] = *reinterpret_cast<const v4u*>(alane[i] + st * GM_KC);
   };
-  gm_f32x4 acc[4][MT];
+  gm_f32x4 acc[NT][MT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < NT; ++j)
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[j][i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
   // every load is issued unconditionally (units past the range re-read the last one) and
@@ -414,20 +349,22 @@ __global__ __launch_bounds__(256, 2) void gemm_ksplit_kernel(GemmArgs a) {
   auto finish = [&](int g, bool whole) {
     gm_lds_barrier();   // the previous group's reads of red are done
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int i = 0; i < MT; ++i) red[((j * 4 + wave) * MT + i) * 64 + lane] = acc[j][i];
     gm_lds_barrier();
-    gm_f32x4 fin[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      fin[i] = red[((wave * 4) * MT + i) * 64 + lane];
+    for (int j = wave; j < NT; j += 4) {
 #pragma unroll
-      for (int v = 1; v < 4; ++v) fin[i] += red[((wave * 4 + v) * MT + i) * 64 + lane];
+      for (int i = 0; i < MT; ++i) {
+        gm_f32x4 fin = red[((j * 4) * MT + i) * 64 + lane];
+#pragma unroll
+        for (int v = 1; v < 4; ++v) fin += red[((j * 4 + v) * MT + i) * 64 + lane];
+        gs_emit_tile<NT>(a, fin, i, j, g, whole, w, lane);
+      }
     }
-    gm_emit<MT>(a, fin, g, whole, w, wave, lane);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int i = 0; i < MT; ++i) acc[j][i] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
   };
@@ -437,7 +374,7 @@ __global__ __launch_bounds__(256, 2) void gemm_ksplit_kernel(GemmArgs a) {
     const int u = ub + (J);                                                                   \
     const bool livej = u < u1;                                                                \
     if (livej) {                                                                              \
-      _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                         \
+      _Pragma("unroll") for (int j = 0; j < NT; ++j) {                                        \
         _Pragma("unroll") for (int i = 0; i < MT; ++i) {                                      \
           acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                                \
               __builtin_bit_cast(gm_bf16x8, wr[J][j]), __builtin_bit_cast(gm_bf16x8, ar[J][i]), \
@@ -570,7 +507,9 @@ __global__ __launch_bounds__(GM_AF_THREADS) void gemm_argmax_final_kernel(
 
 // The GEMM output completed, the residual added and the row normalised, for a
 // projection that feeds the decoder's residual stream (o_proj / out_proj / down, then
-// modeling_qwen3_5.py:59-60): x_out = bf16(C + residual), y = RMSNorm_{1+w}(x_out).
+// modeling_qwen3_5.py:59-60): x_out = bf16(C + residual), y = RMSNorm_{1+w}(x_out); with
+// no residual (the MTP fc, whose output starts the MTP layer's residual stream and is
+// normalised by its input_layernorm, mtp.py:61-73) x_out = bf16(C).
 // One workgroup per row; thread t owns the 8-column chunks of lollm_rmsnorm's
 // chunking, and first forms each C value the way gemm_fixup_kernel does (groups
 // one workgroup finished come from C, the others are the fp32 sum of their pieces in
@@ -599,7 +538,7 @@ __global__ __launch_bounds__(RMS_THREADS) void gemm_norm_kernel(GemmArgs a,
   for (int ci = 0; ci < MAXV; ++ci) {
     const int c = tid + RMS_THREADS * ci;
     wv[ci] = c < n8 ? *reinterpret_cast<const uint4*>(w + 8 * c) : make_uint4(0, 0, 0, 0);
-    hv[ci] = c < n8 ? *reinterpret_cast<const uint4*>(res + row + 8 * c) : make_uint4(0, 0, 0, 0);
+    hv[ci] = c < n8 && res ? *reinterpret_cast<const uint4*>(res + row + 8 * c) : make_uint4(0, 0, 0, 0);
   }
   for (int g = tid; g < a.G; g += RMS_THREADS) {
     own[2 * g] = gm_owner(a.U, g * a.SK, a.nw);
@@ -649,7 +588,9 @@ __global__ __launch_bounds__(RMS_THREADS) void gemm_norm_kernel(GemmArgs a,
       const uint32_t hd[4] = {h.x, h.y, h.z, h.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float f = round_bf16(cv[e] + __uint_as_float(e & 1 ? hd[e >> 1] & 0xffff0000u : hd[e >> 1] << 16));
+        // no residual: x_out is the GEMM output itself (not + 0, which would turn -0 into +0)
+        const float f = res ? round_bf16(cv[e] + __uint_as_float(e & 1 ? hd[e >> 1] & 0xffff0000u : hd[e >> 1] << 16))
+                            : cv[e];
         v[ci][e] = f;
         ss += f * f;
       }
@@ -718,11 +659,11 @@ LOLLM_API long long lollm_gemm_workspace_bytes(int M, int N, int K, int grid) {
 }
 
 // Validates the arguments common to the GEMM entry points and launches the main kernel.
-// n-tiles per group of a lollm_gemm call: 6 (96 columns) when the 33..64-row kernel runs,
-// the 96-column groups divide evenly over the grid and the 64-column ones would not (so
-// the call needs no merge launch); else 4.  A pure function of (M, N, grid).
-static int gemm_group_tiles(int M, int N, int nw) {
-  if (M > 32 && N % 96 == 0 && (N / 96) % nw == 0 && (N / GM_COLS) % nw != 0) return 6;
+// n-tiles per group of a lollm_gemm call: 6 (96 columns) when the 96-column groups divide
+// evenly over the grid and the 64-column ones would not (so the call needs no merge
+// launch); else 4.  A pure function of (N, grid).
+static int gemm_group_tiles(int N, int nw) {
+  if (N % 96 == 0 && (N / 96) % nw == 0 && (N / GM_COLS) % nw != 0) return 6;
   return 4;
 }
 
@@ -742,7 +683,7 @@ static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, 
   a.A = (const uint16_t*)A; a.Wt = (const uint16_t*)Wt; a.C = (uint16_t*)C;
   a.part = (float*)workspace;
   a.lda = lda; a.ldc = ldc;
-  const int nt = allow_wide ? gemm_group_tiles(M, N, nw) : 4;
+  const int nt = allow_wide ? gemm_group_tiles(N, nw) : 4;
   a.M = M; a.N = N; a.K = K; a.G = N / (16 * nt); a.SK = K / GM_KC; a.nw = nw; a.epi = epilogue;
   a.U = a.G * a.SK;
   a.rowmajor = rowmajor;
@@ -750,8 +691,14 @@ static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, 
   if (epilogue == GM_EPI_ARGMAX)
     a.am = (uint64_t*)((char*)workspace + ((gemm_ws_bytes(M, N, nw) + 255) / 256) * 256);
   switch ((M + 15) / 16) {
-    case 1: hipLaunchKernelGGL(gemm_ksplit_kernel<1>, dim3(nw), dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(gemm_ksplit_kernel<2>, dim3(nw), dim3(256), 0, st, a); break;
+    case 1:
+      if (nt == 6) hipLaunchKernelGGL((gemm_ksplit_kernel<1, 6>), dim3(nw), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((gemm_ksplit_kernel<1, 4>), dim3(nw), dim3(256), 0, st, a);
+      break;
+    case 2:
+      if (nt == 6) hipLaunchKernelGGL((gemm_ksplit_kernel<2, 6>), dim3(nw), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((gemm_ksplit_kernel<2, 4>), dim3(nw), dim3(256), 0, st, a);
+      break;
     default:   // 33..64 rows: the warp-specialised stream (64-row tiles, rows past M clamped)
       if (nt == 6)
         hipLaunchKernelGGL(gemm_stream_kernel<6>, dim3(nw), dim3(GS_THREADS), 0, st, a);
@@ -819,7 +766,7 @@ LOLLM_API int lollm_gemm_rmsnorm(const void* A, long long lda, const void* Wt, i
                                  const void* residual, const void* norm_w, float eps, void* C,
                                  void* x_out, void* y, void* workspace, long long workspace_bytes,
                                  int grid, void* stream) {
-  if (!residual || !norm_w || !x_out || !y) return LOLLM_EINVAL;
+  if (!norm_w || !x_out || !y) return LOLLM_EINVAL;   // residual may be null
   if (N > 8 * RMS_THREADS * RMS_CHUNKS) return LOLLM_EUNSUPPORTED;
   if (M <= 0 || N <= 0 || K <= 0 || N % GM_COLS || K % GM_KC) return LOLLM_EUNSUPPORTED;
   const int nw = gemm_grid(grid);

@@ -293,7 +293,8 @@ _cu_count = {}
 def gemm_rmsnorm(x, tiled, N, K, residual, w, eps, grid=0):
     """h = x W^T completed with the residual add and RMSNorm of the decoder layer:
     x_out = bf16(h + residual), y = RMSNorm_{1+w}(x_out).  Returns (y, x_out), the same
-    bits as gemm() followed by rmsnorm(h, w, eps, residual=residual)."""
+    bits as gemm() followed by rmsnorm(h, w, eps, residual=residual).  residual=None:
+    x_out = h and y = rmsnorm(h, w, eps)."""
     lead = x.shape[:-1]
     M = x.numel() // K
     if x.shape[-1] != K:
@@ -303,14 +304,16 @@ def gemm_rmsnorm(x, tiled, N, K, residual, w, eps, grid=0):
     x = x.contiguous()
     _need(x, "x", torch.bfloat16)
     _need(tiled, "tiled", torch.bfloat16, (N * K,))
-    residual = residual.contiguous()
-    _need(residual, "residual", torch.bfloat16, (*lead, N))
+    if residual is not None:
+        residual = residual.contiguous()
+        _need(residual, "residual", torch.bfloat16, (*lead, N))
     _need(w, "w", torch.bfloat16, (N,))
     c = torch.empty(*lead, N, dtype=torch.bfloat16, device=x.device)
     x_out = torch.empty_like(c)
     y = torch.empty_like(c)
     ws = gemm_workspace(gemm_workspace_bytes(M, N, K, grid), x.device)
-    rc = _lib.lib().lollm_gemm_rmsnorm(_ptr(x), K, _ptr(tiled), M, N, K, _ptr(residual), _ptr(w),
+    rc = _lib.lib().lollm_gemm_rmsnorm(_ptr(x), K, _ptr(tiled), M, N, K,
+                                       None if residual is None else _ptr(residual), _ptr(w),
                                        float(eps), _ptr(c), _ptr(x_out), _ptr(y), _ptr(ws),
                                        ws.numel(), grid, _stream())
     _lib.check(rc, "lollm_gemm_rmsnorm")

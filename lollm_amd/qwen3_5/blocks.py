@@ -40,14 +40,15 @@ def gemm_path(N, K, epilogue, rows, tiled=True):
 
 def gemm_grid(N, cus, rows=ops.GEMM_MAX_ROWS):
     """Workgroups of a lollm_gemm call with N output columns and `rows` rows on a device
-    with `cus` CUs: one per 64-column group when that covers 3/4 of the CUs or more; for
-    33..64 rows, else one per 96-column group on the same condition (lollm_gemm then
-    takes 96-column groups, none cut: the attention q|gate|k|v of the 4096-hidden model,
-    192 groups; its MLP gate|up, 256 = one per CU); else one per CU."""
+    with `cus` CUs: one per 64-column group when that covers 3/4 of the CUs or more; else
+    one per 96-column group on the same condition (lollm_gemm then takes 96-column
+    groups, none cut: the attention q|gate|k|v of the 4096-hidden model, 192 groups; its
+    MLP gate|up, 256 = one per CU); else one per CU.  (`rows` is kept for shapes whose
+    grid may come to depend on it; every rule is the same for 1..64 rows today.)"""
     groups = N // 64
     if 4 * groups >= 3 * cus and groups <= cus:
         return groups
-    if rows > 32 and N % 96 == 0:
+    if N % 96 == 0:
         wide = N // 96
         if 4 * wide >= 3 * cus and wide <= cus:
             return wide
@@ -97,7 +98,8 @@ class Projection:
     def add_norm(self, x, residual, norm):
         """The projection feeding the residual stream with the add and the next RMSNorm
         (modeling_qwen3_5.py:59-60): x_out = residual + x W^T, y = norm(x_out); returns
-        (y, x_out).  lollm_gemm_rmsnorm (one GEMM call, the norm fused into its second
+        (y, x_out).  residual=None: x_out = x W^T (the MTP fc, which starts the MTP
+        layer's residual stream).  lollm_gemm_rmsnorm (one GEMM call, the norm fused into its second
         kernel) when the path is lollm_gemm and the shape fits it, else the projection
         followed by lollm_rmsnorm."""
         rows = x.numel() // self.K
@@ -106,6 +108,9 @@ class Projection:
                 and ops.gemm_rmsnorm_supported(rows, self.N, self.K, g1)):
             return ops.gemm_rmsnorm(x, self.tiled, self.N, self.K, residual, norm.weight, norm.eps,
                                     grid=g1)
+        if residual is None:
+            h = self(x)
+            return norm(h), h
         return norm(self(x), residual=residual)
 
 

@@ -55,15 +55,15 @@ class MTP:
         pre-fc norms and the concatenation run as one kernel (lollm_mtp_input)."""
         if tok is not None:
             B = tok.numel()
-            x = self.fc(ops.mtp_input(tok, hidden, self.model.model.embed_tokens.weight,
-                                      self.pre_fc_norm_embedding.weight,
-                                      self.pre_fc_norm_hidden.weight,
-                                      self.pre_fc_norm_embedding.eps).view(B, 1, -1))
+            fc_in = ops.mtp_input(tok, hidden, self.model.model.embed_tokens.weight,
+                                  self.pre_fc_norm_embedding.weight, self.pre_fc_norm_hidden.weight,
+                                  self.pre_fc_norm_embedding.eps).view(B, 1, -1)
         else:
-            x = self.fc(torch.cat([self.pre_fc_norm_embedding(next_emb),
-                                   self.pre_fc_norm_hidden(hidden)], -1))
+            fc_in = torch.cat([self.pre_fc_norm_embedding(next_emb),
+                               self.pre_fc_norm_hidden(hidden)], -1)
         layer = self.layers[0]
-        h_in = layer.input_layernorm(x)
+        # fc and the layer's input_layernorm (the fc output starts the residual stream)
+        h_in, x = self.fc.add_norm(fc_in, None, layer.input_layernorm)
         core = layer.self_attn.core(h_in, k_cache, v_cache, lengths, kv_len, rope_pos=rope_pos,
                                     grid=self.model.attn_grid, workspace=ws)
         y, x = layer.self_attn.out.add_norm(core, x, layer.post_attention_layernorm)

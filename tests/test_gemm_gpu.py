@@ -54,16 +54,17 @@ def test_gemm_pieces_equal_whole_groups(M):
     torch.testing.assert_close(a, b, rtol=8e-3, atol=8e-3 * a.abs().max().item())
 
 
-@pytest.mark.parametrize("M", [33, 40, 64])
+@pytest.mark.parametrize("M", [1, 16, 17, 32, 33, 40, 64])
 @pytest.mark.parametrize("N,K,grid", [(1536, 1024, 16), (2304, 512, 8), (18432, 256, 192)])
 @pytest.mark.parametrize("epi", [0, 1])
 def test_gemm_wide_groups_equal_whole_groups(M, N, K, grid, epi):
-    """33..64 rows on a grid that divides the 96-column groups but not the 64-column ones
-    (N = 1536 on 16 workgroups, 2304 on 8: three groups each, the attention q|gate|k|v
-    width on 192): lollm_gemm takes 96-column groups, none cut, no merge launch.  Each
-    output tile sums the same k-steps in the same order as with 64-column groups
-    finished whole (grid 1), so the two are bit-identical, with and without the SwiGLU
-    epilogue, and both match the oracle."""
+    """A grid that divides the 96-column groups but not the 64-column ones (N = 1536 on
+    16 workgroups, 2304 on 8: three groups each, the attention q|gate|k|v width on 192):
+    lollm_gemm takes 96-column groups, none cut, no merge launch -- in the k-split kernel
+    (1..32 rows; each wave sums its k-quarter, the quarters are added in wave order) and
+    in the LDS-staged one (33..64 rows).  Each output tile sums the same terms in the same
+    order as with 64-column groups finished whole (grid 1) in the same kernel, so the two
+    are bit-identical, with and without the SwiGLU epilogue, and both match the oracle."""
     from lollm_amd import ops
     print(f"case gemm wide M={M} N={N} K={K} grid={grid} epi={epi}", flush=True)
     x, W = case(M, N, K, seed=N + K + M + epi)
@@ -157,6 +158,30 @@ def test_gemm_rmsnorm_equals_gemm_then_rmsnorm(M, N, K, grid):
     xref = (href.float() + res.float()).bfloat16()
     close(xo, xref.float())
     close(y, R.rmsnorm_plus1(xref, w, eps).float())
+
+
+@pytest.mark.parametrize("M,N,K,grid", [(16, 4096, 8192, 0), (5, 512, 128, 4), (64, 2048, 1024, 200)])
+def test_gemm_rmsnorm_without_residual(M, N, K, grid):
+    """residual=None (the MTP fc followed by the MTP layer's input_layernorm,
+    mtp.py:61-73): x_out is the GEMM output itself and y its norm -- the same bits as
+    lollm_gemm followed by lollm_rmsnorm without a residual (a zero row included) -- and
+    both match the oracle."""
+    from lollm_amd import ops
+    print(f"case gemm_rmsnorm no residual M={M} N={N} K={K} grid={grid}", flush=True)
+    x, W = case(M, N, K, seed=M + N + K + 7)
+    x[0] = 0
+    w = (torch.randn(N, generator=torch.Generator().manual_seed(N)) * 0.1).bfloat16()
+    eps = 1e-6
+    Wt = ops.gemm_tile_weights(W.cuda())
+    y, xo = ops.gemm_rmsnorm(x.cuda(), Wt, N, K, None, w.cuda(), eps, grid=grid)
+    h = ops.gemm(x.cuda(), Wt, N, K, grid=grid)
+    y2 = ops.rmsnorm(h, w.cuda(), eps)
+    torch.cuda.synchronize()
+    assert torch.equal(xo.view(torch.int16), h.view(torch.int16))
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    href = R.linear(x.float(), W.float()).bfloat16()
+    close(xo, href.float())
+    close(y, R.rmsnorm_plus1(href, w, eps).float())
 
 
 def test_gemm_rmsnorm_rejects_unsupported():

@@ -17,12 +17,12 @@ def test_gemm_grid_whole_groups_only_when_they_fill_the_device():
     # 4 groups per 3 CUs or more, or fewer than 3/4 of the CUs: one workgroup per CU
     for N in (4096, 8192, 24576, 151936):
         assert gemm_grid(N, 256) == 256
-    # 33..64 rows: one workgroup per 96-column group when those fill 3/4 of the CUs or
-    # more (attention q|gate|k|v 18432 = 192 x 96; gate|up 24576 = 256 x 96, one per CU
-    # either way); at most 32 rows the 64-column rule alone
-    assert gemm_grid(18432, 256, 64) == 192 and gemm_grid(18432, 256, 33) == 192
-    assert gemm_grid(18432, 256, 32) == 256 and gemm_grid(18432, 256, 16) == 256
-    assert gemm_grid(24576, 256, 64) == 256 and gemm_grid(24576, 256, 16) == 256
+    # else one workgroup per 96-column group when those fill 3/4 of the CUs or more
+    # (attention q|gate|k|v 18432 = 192 x 96; gate|up 24576 = 256 x 96, one per CU either
+    # way), for any number of rows
+    for rows in (64, 33, 32, 16, 1):
+        assert gemm_grid(18432, 256, rows) == 192
+        assert gemm_grid(24576, 256, rows) == 256
     assert gemm_grid(191 * 96, 256, 64) == 256
     assert gemm_grid(192 * 64, 256) == 192
     assert gemm_grid(191 * 64, 256) == 256
