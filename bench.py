@@ -126,8 +126,10 @@ def run_e2e(model, mtp, cfg, B, prompt_len, k, steps, warmup, temperature, top_p
 
 
 def projection_paths(model, mtp, B, k):
-    """The path of each projection shape of the step ("gemm grid g" = lollm_gemm on g
-    workgroups, "blas" = hipBLASLt; a fixed function of the shape), keyed "NxK M=rows"."""
+    """The path of each projection shape of the step ("gemm grid g, c-col groups" =
+    lollm_gemm on g workgroups with c-column groups -- 96 where those divide over the
+    grid and 64-column ones would not, the library's rule -- "blas" = hipBLASLt; a fixed
+    function of the shape), keyed "NxK M=rows"."""
     out = {}
     layers = list(model.model.layers) + list(mtp.layers)
     projs = [model.lm_head, mtp.fc]
@@ -138,7 +140,12 @@ def projection_paths(model, mtp, B, k):
         for rows in (B, B * (k + 1)):
             tag = f"{p.N}x{p.K}{' swiglu' if p.epilogue else ''} M={rows}"
             path = p.path(rows)
-            out[tag] = f"gemm grid {p.grid()}" if path == "gemm" else path
+            if path == "gemm":
+                g = p.grid(rows)
+                cols = 96 if p.N % 96 == 0 and (p.N // 96) % g == 0 and (p.N // 64) % g else 64
+                out[tag] = f"gemm grid {g}, {cols}-col groups"
+            else:
+                out[tag] = path
     return dict(sorted(out.items()))
 
 
