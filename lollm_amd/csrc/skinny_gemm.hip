@@ -103,7 +103,9 @@ __global__ void gemm_tile_kernel(const uint16_t* __restrict__ W, uint16_t* __res
 // each copies its half of a unit's weight blocks (2 n-tiles x 4 k-steps, 1 KB each, for
 // 64-column groups)
 // straight into LDS with 16-byte DMA loads (global_load_lds_dwordx4, non-temporal) into a
-// ring of GS_WSLOTS slots, GS_WSLOTS - 1 units ahead; wave 6 copies the unit's 64-row
+// ring of GS_WSLOTS slots, GS_WSLOTS - 1 units ahead (3 slots: measured 1-3% faster per
+// launch than 4 to 7 in the decode step -- a shallower DMA queue per CU queues less on
+// the memory side -- and 2 slots 7% slower); wave 6 copies the unit's 64-row
 // activation tile (128 k) the same way into a ring of GS_ASLOTS slots.  Only these
 // three waves wait on vmcnt, each for its own oldest unit with a fixed count, so the
 // weight stream never waits for anything else (in the register-ring kernel every wait
@@ -123,7 +125,7 @@ __global__ void gemm_tile_kernel(const uint16_t* __restrict__ W, uint16_t* __res
 // the MFMA waves) on every projection shape of the 8B-class verify pass.
 typedef __attribute__((address_space(1))) void gs_global_t;
 typedef __attribute__((address_space(3))) void gs_lds_t;
-constexpr int GS_WSLOTS = 5;
+constexpr int GS_WSLOTS = 3;
 constexpr int GS_ASLOTS = 3;
 constexpr int GS_SLOT = 16384;
 constexpr int GS_THREADS = 448;
@@ -183,12 +185,12 @@ __device__ __forceinline__ void gs_emit_tile(const GemmArgs& a, const gm_f32x4& 
 // divide evenly over the grid and 64-column ones would be cut (the MLP gate|up of the
 // 4096-hidden model: 256 groups, one per CU, so no merge launch follows; the attention
 // q|gate|k|v: 192).  A wide unit is 24 KB of weights against the same 16 KB activation
-// tile, so the weight ring holds 4 units instead of 5 to stay within LDS.  Each output
+// tile.  Each output
 // tile accumulates the same k-steps in the same order for either width, so a group
 // finished by one workgroup has the same bits at both widths.
 template <int NT>
 __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
-  constexpr int WSLOTS = NT == 4 ? GS_WSLOTS : 4;
+  constexpr int WSLOTS = GS_WSLOTS;
   constexpr int WSLOT = NT * GM_KS * 1024;   // bytes of one unit's weight blocks
   constexpr int HALF = NT / 2;               // n-tiles per loader wave and per MFMA wave
   static_assert(NT % 2 == 0 && WSLOTS * WSLOT + GS_ASLOTS * GS_SLOT <= 160 * 1024, "LDS");
