@@ -546,9 +546,10 @@ def pmc_probe(B=16, T=4, launches=20):
     the order of PROBE_ORDER, then torch.neg over 256 MiB (reads and writes
     PROBE_COPY_BYTES each) 5 times as the counter calibration:
       gdn_layer       the fused GDN layer, B=16, T=4, 32 v / 16 qk heads of 128
-      gemm_qkv        lollm_gemm, 64 rows x q|gate|k|v (N=18432) x K=4096
-      gemm_gate_up    lollm_gemm with the SwiGLU epilogue, 64 rows x N=24576 x K=4096
-      gemm_down       lollm_gemm, 64 rows x N=4096 x K=12288
+      gemm_qkv        lollm_gemm, 64 rows x q|gate|k|v (N=18432) x K=4096, 192 WGs
+      gemm_gate_up    lollm_gemm with the SwiGLU epilogue, 64 rows x N=24576 x K=4096, 256
+      gemm_down       lollm_gemm, 64 rows x N=4096 x K=12288, 256 WGs + the merge launch
+                      (the step merges it in lollm_gemm_rmsnorm's second kernel)
       attn_step       lollm_attn_verify, B=16, T=4, 32 q / 4 kv heads, contexts U[2052, 2308]
       spec_accept_c4  lollm_spec_accept, B=64, k=3, V=151936 with sampled drafts
     Each GEMM rotates over enough weight copies (> 512 MB) that every launch streams its
@@ -578,14 +579,16 @@ def pmc_probe(B=16, T=4, launches=20):
                       replay, False, B, T, Hk, Hv, D, K, 1e-6, out=out)
     del rec, rep, win
     M = B * T
+    from lollm_amd.qwen3_5.blocks import gemm_grid
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
     for N, Kd, epi in ((18432, 4096, ops.GEMM_NONE), (24576, 4096, ops.GEMM_SWIGLU),
                        (4096, 12288, ops.GEMM_NONE)):
         copies = max(2, -(-(512 << 20) // (N * Kd * 2)))
         Wts = [ops.gemm_tile_weights((0.02 * torch.randn(N, Kd, device="cuda", generator=g)).bfloat16(), epi)
                for _ in range(copies)]
         x = torch.randn(M, Kd, device="cuda", generator=g).bfloat16()
-        for i in range(launches):
-            ops.gemm(x, Wts[i % copies], N, Kd, epi)
+        for i in range(launches):   # the step's grid for the shape
+            ops.gemm(x, Wts[i % copies], N, Kd, epi, grid=gemm_grid(N, cus, M))
         del Wts
         torch.cuda.empty_cache()
     kv_len = torch.randint(2052, 2309, (16,), generator=torch.Generator().manual_seed(3)).int().cuda()
