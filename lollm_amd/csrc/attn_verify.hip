@@ -333,11 +333,14 @@ __global__ __launch_bounds__(AW_THREADS, 1) void attn_verify_kernel(AttnArgs a) 
         }
         bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
         // the reference max moves (and l, O are rescaled) only when a row's block max
-        // exceeds it by more than 16 in the exponent (always at a pair's first block)
+        // exceeds it by more than 16 in the exponent (always at a pair's first block).
+        // The decision is the row's own (the ballot only skips the rescale when no row
+        // needs one; other rows scale by exactly 1), so a row's bits do not depend on
+        // which other rows share the pair -- the verify length T, the padding rows.
         const bool big = (bm - m_ref) * a.cl2 > 16.f;
         if (__builtin_amdgcn_readfirstlane((int)(__ballot(big) != 0))) {
-          const float mn = fmaxf(m_ref, bm);
-          const float alpha = mn == -INFINITY ? 1.f : fast_exp2((m_ref - mn) * a.cl2);
+          const float mn = big ? fmaxf(m_ref, bm) : m_ref;
+          const float alpha = (!big || mn == -INFINITY) ? 1.f : fast_exp2((m_ref - mn) * a.cl2);
           m_ref = mn;
           l_s *= alpha;
 #pragma unroll

@@ -112,8 +112,11 @@ __global__ void gemm_tile_kernel(const uint16_t* __restrict__ W, uint16_t* __res
 // for an activation or a weight also waited for all older loads, in issue order, and
 // the compiler added full drains at the loop head).  Waves 0-3 read both MFMA operands
 // from LDS in a 2 x 2 arrangement -- wave (wn, wm) owns n-tiles 2 wn, 2 wn + 1 and m-tiles
-// 2 wm, 2 wm + 1 of the group -- accumulating each tile over the unit's k-steps in order,
-// as the register-ring kernel it replaced did, so results and pieces kept their bits.  One barrier per unit: past it the unit has
+// 2 wm, 2 wm + 1 of the group -- with one accumulator per k-step of the unit (q = k-step
+// mod 4), added in the order 0, 1, 2, 3 at the group's end: exactly the sums and order of
+// gemm_ksplit_kernel, whose wave q accumulates k-steps 4 s + q, so a row's bits do not
+// depend on how many rows share the call (1..32 rows run that kernel, 33..64 this one).
+// One barrier per unit: past it the unit has
 // landed and every consumer has finished the previous unit, whose slots the loaders
 // refill.  Activation rows sit in LDS without padding, the 16-byte chunk c of row r at
 // chunk position c ^ (r & 15) (the DMA writes a wave's 1 KB contiguously, so the loaders
@@ -251,11 +254,13 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
     return;
   }
   const int wn = wave & 1, wm = wave >> 1, l16 = lane & 15, g4 = lane >> 4;
-  gm_f32x4 acc[2][HALF];
+  gm_f32x4 acc[GM_KS][2][HALF];
 #pragma unroll
-  for (int ii = 0; ii < 2; ++ii)
+  for (int q = 0; q < GM_KS; ++q)
 #pragma unroll
-    for (int jj = 0; jj < HALF; ++jj) acc[ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int jj = 0; jj < HALF; ++jj) acc[q][ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
   bool whole_from_start = (u0 % a.SK) == 0;
   for (int u = u0; u < u1; ++u) {
     // this wave's reads of the previous unit are complete before the loaders may refill it
@@ -277,7 +282,7 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
       for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
         for (int jj = 0; jj < HALF; ++jj)
-          acc[ii][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[jj], af[ii], acc[ii][jj], 0, 0, 0);
+          acc[q][ii][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[jj], af[ii], acc[q][ii][jj], 0, 0, 0);
     }
     const int st = u % a.SK;
     if (st == a.SK - 1 || u == u1 - 1) {
@@ -287,8 +292,12 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
       for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
         for (int jj = 0; jj < HALF; ++jj) {
-          gs_emit_tile<NT>(a, acc[ii][jj], 2 * wm + ii, HALF * wn + jj, g, whole, w, lane);
-          acc[ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+          gm_f32x4 fin = acc[0][ii][jj];
+#pragma unroll
+          for (int q = 1; q < GM_KS; ++q) fin += acc[q][ii][jj];
+          gs_emit_tile<NT>(a, fin, 2 * wm + ii, HALF * wn + jj, g, whole, w, lane);
+#pragma unroll
+          for (int q = 0; q < GM_KS; ++q) acc[q][ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
         }
       whole_from_start = true;
     }

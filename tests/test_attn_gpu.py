@@ -48,7 +48,7 @@ def oracle(q, kc, vc, lens, gate):
 
 
 CASES = [
-    # B, T, Hq, Hkv, lens, grid (workgroups of the balanced split; 0 = two per CU)
+    # B, T, Hq, Hkv, lens, grid (workgroups of the balanced split; 0 = one per CU)
     (3, 4, 16, 2, [4, 37, 700], 0),            # plain causal, whole pairs and cut pairs
     (2, 1, 8, 2, [1, 1000], 5),                # decode, a long pair cut in many pieces
     (2, 2, 8, 2, [2, 129], 3),                 # k = 1 verify, n_rep = 4
@@ -97,6 +97,26 @@ def test_attn_split_invariance():
             for g in (4, 9, 64)]
     for o in outs[1:]:
         torch.testing.assert_close(o.float(), outs[0].float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("Hq,Hkv,base,grid", [(16, 2, [1000, 37, 700], 0), (32, 4, [2048, 2049, 130], 7),
+                                            (8, 2, [1, 300, 129], 0)])
+def test_attn_rows_do_not_depend_on_T(Hq, Hkv, base, grid):
+    """Query i of a verify call over T = 4 positions and of a call over only the first
+    t <= 4 positions (the history a rollback keeps) sees the same keys, and gets the same
+    bits: every row keeps its own running maximum (the rescale decision is per row), so
+    the other rows of its pair -- the later queries, or padding -- do not change it.
+    Contexts are chosen so both calls deal the same key blocks out to the workgroups."""
+    from lollm_amd import ops
+    print(f"case attn rows Hq={Hq} Hkv={Hkv} base={base} grid={grid}", flush=True)
+    B, T = len(base), 4
+    q, kc, vc, kl, gate = make_case(B, T, Hq, Hkv, [b + T for b in base], seed=sum(base) + Hq)
+    full = ops.attn_verify(q.cuda(), kc.cuda(), vc.cuda(), kl.cuda(), gate.cuda(), grid=grid)
+    for t in (1, 2, 3):
+        assert all((b + t + 127) // 128 == (b + T + 127) // 128 for b in base)
+        part = ops.attn_verify(q[:, :t].contiguous().cuda(), kc.cuda(), vc.cuda(),
+                               (kl - (T - t)).cuda(), gate[:, :t].contiguous().cuda(), grid=grid)
+        assert torch.equal(part.cpu(), full[:, :t].cpu()), t
 
 
 def test_attn_workspace_is_validated():

@@ -54,6 +54,43 @@ def test_gemm_pieces_equal_whole_groups(M):
     torch.testing.assert_close(a, b, rtol=8e-3, atol=8e-3 * a.abs().max().item())
 
 
+@pytest.mark.parametrize("N,K,epi,grid", [(1024, 1024, 0, 0), (2048, 1024, 0, 32),
+                                          (1536, 1024, 0, 16), (2304, 512, 1, 8),
+                                          (4096, 4096, 0, 0)])
+def test_gemm_row_count_does_not_change_bits(N, K, epi, grid):
+    """A row's output bits do not depend on how many rows share the call: 1..32 rows run
+    the k-split kernel (wave q sums k-steps 4 s + q, the four quarters added in wave
+    order), 33..64 rows the LDS-staged kernel, which keeps one accumulator per k-step of
+    a unit and adds them in the same order.  So the verify pass (B x (1 + k) rows) and a
+    shorter or smaller call give a sequence the same products -- with groups cut and
+    merged (grid 0), whole (one workgroup per group), 96 columns wide, with the SwiGLU
+    epilogue, and through the fused argmax and residual + RMSNorm kernels."""
+    from lollm_amd import ops
+    print(f"case gemm rows N={N} K={K} epi={epi} grid={grid}", flush=True)
+    x, W = case(64, N, K, seed=N + K + epi)
+    Wt = ops.gemm_tile_weights(W.cuda(), epi)
+    xd = x.cuda()
+    full = ops.gemm(xd, Wt, N, K, epi, grid=grid)
+    if epi == ops.GEMM_NONE:
+        am_full = ops.gemm_argmax(xd, Wt, N, K, grid=grid)
+        g = torch.Generator().manual_seed(N)
+        res = torch.randn(64, N, generator=g).bfloat16().cuda()
+        w = (torch.randn(N, generator=g) * 0.1).bfloat16().cuda()
+        norm_ok = ops.gemm_rmsnorm_supported(64, N, K, grid)
+        if norm_ok:
+            y_full, xo_full = ops.gemm_rmsnorm(xd, Wt, N, K, res, w, 1e-6, grid=grid)
+    for M in (1, 5, 16, 17, 32, 33, 48, 63):
+        part = ops.gemm(xd[:M], Wt, N, K, epi, grid=grid)
+        assert torch.equal(part.cpu(), full[:M].cpu()), M
+        if epi == ops.GEMM_NONE:
+            assert torch.equal(ops.gemm_argmax(xd[:M], Wt, N, K, grid=grid).cpu(),
+                               am_full[:M].cpu()), M
+            if norm_ok:
+                y, xo = ops.gemm_rmsnorm(xd[:M], Wt, N, K, res[:M], w, 1e-6, grid=grid)
+                assert torch.equal(xo.cpu(), xo_full[:M].cpu()), M
+                assert torch.equal(y.cpu(), y_full[:M].cpu()), M
+
+
 @pytest.mark.parametrize("M", [1, 16, 17, 32, 33, 40, 64])
 @pytest.mark.parametrize("N,K,grid", [(1536, 1024, 16), (2304, 512, 8), (18432, 256, 192)])
 @pytest.mark.parametrize("epi", [0, 1])
