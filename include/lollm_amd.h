@@ -172,13 +172,14 @@ int lollm_swiglu(const void* gate_up, void* out, int rows, int F, void* stream);
  * [q_proj | k_proj | v_proj] output qkv (B*T, Hq*2D + 2*Hkv*D) -- q_proj packing
  * [query | gate] per head -- write q (B, T, Hq, D) after QK-norm (1 + w) and partial
  * rotate-half RoPE (blocks.py:159-183) at positions rope_pos[b] + t (rope_pos NULL:
- * lengths[b] + t, the cache row; the MTP head uses positions 1..L, mtp.py:66-67), the gate
- * (B, T, Hq*D), and k (normed, roped) / v into the caches at (b, kvh, lengths[b] + t)
- * (kv.py:26-33 without the concatenation).  inv_freq: (rotary_dim / 2) fp32.
- * Supported: D == 256. */
+ * lengths[b] + t, the cache row; the MTP head defaults to positions 1..L, mtp.py:66-67) or,
+ * with rope_per_token != 0, at rope_pos[b * T + t] (a (B, T) table: MTP.forward's explicit
+ * positions vector, mtp.py:61-67), the gate (B, T, Hq*D), and k (normed, roped) / v into
+ * the caches at (b, kvh, lengths[b] + t) (kv.py:26-33 without the concatenation).
+ * inv_freq: (rotary_dim / 2) fp32.  Supported: D == 256. */
 int lollm_attn_prologue(const void* qkv, const void* q_norm_w, const void* k_norm_w,
                         const float* inv_freq, const int32_t* lengths, const int32_t* rope_pos,
-                        int B, int T, int Hq,
+                        int rope_per_token, int B, int T, int Hq,
                         int Hkv, int D, int rotary_dim, float eps, void* q_out, void* gate_out,
                         void* k_cache, void* v_cache, int max_len, void* stream);
 

@@ -50,7 +50,7 @@ SIGNATURES = {
     "lollm_swiglu": ([_P, _P, _I, _I, _P], _I),
     "lollm_attn_small": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P, _P, _I, _P,
                           _P], _I),
-    "lollm_attn_prologue": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P,
+    "lollm_attn_prologue": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P,
                              _I, _P], _I),
     "lollm_gdn_layer": ([_P, ctypes.c_longlong, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I,
                          _I, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P], _I),

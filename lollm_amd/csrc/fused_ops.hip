@@ -170,8 +170,8 @@ __device__ __forceinline__ float qk_norm_rope(float x, float wv, float freq, int
 __global__ __launch_bounds__(256) void attn_prologue_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, const float* __restrict__ inv_freq,
-    const int32_t* __restrict__ lengths, const int32_t* __restrict__ rope_pos, int T, int Hq,
-    int Hkv, int rd, float eps,
+    const int32_t* __restrict__ lengths, const int32_t* __restrict__ rope_pos, int per_token,
+    int T, int Hq, int Hkv, int rd, float eps,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ gate_out, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, int max_len) {
   constexpr int D = 256;
@@ -182,7 +182,8 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
   const long long row_w = (long long)Hq * 2 * D + 2LL * Hkv * D;
   const uint16_t* src = qkv + (long long)bt * row_w;
   const int pos = lengths[b] + t;                          // cache row
-  const int rpos = (rope_pos ? rope_pos[b] : lengths[b]) + t;  // RoPE position
+  // RoPE position: the token's own entry of a (B, T) table, else a start per sequence + t
+  const int rpos = per_token ? rope_pos[bt] : (rope_pos ? rope_pos[b] : lengths[b]) + t;
   if (slot >= Hq + Hkv) {  // value head: plain copy into the cache
     const int kvh = slot - Hq - Hkv;
     if (pos >= 0 && pos < max_len)
@@ -460,19 +461,20 @@ LOLLM_API int lollm_swiglu(const void* gate_up, void* out, int rows, int F, void
 
 LOLLM_API int lollm_attn_prologue(const void* qkv, const void* q_norm_w, const void* k_norm_w,
                                   const float* inv_freq, const int32_t* lengths,
-                                  const int32_t* rope_pos, int B, int T,
+                                  const int32_t* rope_pos, int rope_per_token, int B, int T,
                                   int Hq, int Hkv, int D, int rotary_dim, float eps, void* q_out,
                                   void* gate_out, void* k_cache, void* v_cache, int max_len,
                                   void* stream) {
   if (!qkv || !q_norm_w || !k_norm_w || !lengths || !q_out || !gate_out || !k_cache || !v_cache)
     return LOLLM_EINVAL;
+  if (rope_per_token && !rope_pos) return LOLLM_EINVAL;
   if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || max_len <= 0) return LOLLM_EINVAL;
   if (D != 256 || rotary_dim < 0 || rotary_dim > D || rotary_dim % 2) return LOLLM_EUNSUPPORTED;
   if (rotary_dim > 0 && !inv_freq) return LOLLM_EINVAL;
   hipLaunchKernelGGL(attn_prologue_kernel, dim3(B * T, Hq + 2 * Hkv), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)qkv, (const uint16_t*)q_norm_w,
-                     (const uint16_t*)k_norm_w, inv_freq, lengths, rope_pos, T, Hq, Hkv,
-                     rotary_dim, eps,
+                     (const uint16_t*)k_norm_w, inv_freq, lengths, rope_pos, rope_per_token ? 1 : 0,
+                     T, Hq, Hkv, rotary_dim, eps,
                      (uint16_t*)q_out, (uint16_t*)gate_out, (uint16_t*)k_cache,
                      (uint16_t*)v_cache, max_len);
   return launch_status();

@@ -453,7 +453,12 @@ def swiglu(gate_up, out=None):
 
 def attn_prologue(qkv, q_norm_w, k_norm_w, inv_freq, lengths, B, T, Hq, Hkv, D, rotary_dim, eps,
                   k_cache, v_cache, q_out=None, gate_out=None, rope_pos=None):
+    """rope_pos: None (RoPE at the cache rows lengths[b] + t), (B,) int32 (positions
+    rope_pos[b] + t) or (B, T) int32 (each token's own position)."""
     _need(qkv, "qkv", torch.bfloat16)
+    per_token = rope_pos is not None and rope_pos.dim() == 2
+    if rope_pos is not None:
+        _need(rope_pos, "rope_pos", torch.int32, (B, T) if per_token else (B,))
     if qkv.numel() != B * T * (Hq * 2 * D + 2 * Hkv * D):
         raise ValueError("qkv has the wrong size")
     _need(lengths, "lengths", torch.int32, (B,))
@@ -466,8 +471,7 @@ def attn_prologue(qkv, q_norm_w, k_norm_w, inv_freq, lengths, B, T, Hq, Hkv, D, 
         gate_out = torch.empty(B, T, Hq * D, dtype=torch.bfloat16, device=qkv.device)
     rc = _lib.lib().lollm_attn_prologue(
         _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(inv_freq), _ptr(lengths), _ptr(rope_pos),
-        B, T, Hq, Hkv,
-        D, rotary_dim, float(eps), _ptr(q_out), _ptr(gate_out), _ptr(k_cache), _ptr(v_cache),
+        int(per_token), B, T, Hq, Hkv, D, rotary_dim, float(eps), _ptr(q_out), _ptr(gate_out), _ptr(k_cache), _ptr(v_cache),
         max_len, _stream())
     _lib.check(rc, "lollm_attn_prologue")
     return q_out, gate_out

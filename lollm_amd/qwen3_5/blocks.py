@@ -230,7 +230,8 @@ class GatedAttention:
 
     def core(self, x, k_cache, v_cache, lengths, kv_len, rope_pos=None, grid=0,
              workspace=None):
-        """Everything before o_proj (blocks.py:208-235)."""
+        """Everything before o_proj (blocks.py:208-235).  rope_pos: None (RoPE at the cache
+        rows), (B,) int32 start positions, or (B, T) int32 per-token positions."""
         B, T, _ = x.shape
         cfg = self.cfg
         qkv = self.qkv(x)
@@ -239,7 +240,7 @@ class GatedAttention:
             return ops.attn_small(qkv, self.q_norm, self.k_norm, self.inv_freq, lengths, kv_len, B,
                                   cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
                                   cfg.rotary_dim, cfg.rms_norm_eps, k_cache, v_cache,
-                                  rope_pos=rope_pos)
+                                  rope_pos=None if rope_pos is None else rope_pos.reshape(B))
         q, gate = ops.attn_prologue(qkv, self.q_norm, self.k_norm, self.inv_freq, lengths, B, T,
                                     cfg.num_attention_heads, cfg.num_key_value_heads,
                                     cfg.head_dim, cfg.rotary_dim, cfg.rms_norm_eps, k_cache,

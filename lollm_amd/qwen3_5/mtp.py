@@ -82,16 +82,18 @@ class MTP:
         B, L, _ = hidden.shape
         dev = self.model.device
         if positions is None:
-            start = 1
+            rope = torch.ones(B, dtype=torch.int32, device=dev)        # positions 1..L
         else:
-            pos = positions.flatten().tolist()
-            if pos != list(range(pos[0], pos[0] + L)):
-                raise NotImplementedError("MTP positions must be consecutive")
-            start = pos[0]
+            # any positions vector (L,) shared by the batch, as mtp.py:64-67, or (B, L)
+            pos = torch.as_tensor(positions, device=dev).to(torch.int32)
+            if pos.dim() == 1:
+                pos = pos.view(1, -1).expand(B, -1)
+            if tuple(pos.shape) != (B, L):
+                raise ValueError(f"positions must be ({L},) or ({B}, {L}), got {tuple(positions.shape)}")
+            rope = pos.contiguous()
         kc, vc = self.scratch_cache(B, L)
         zeros = torch.zeros(B, dtype=torch.int32, device=dev)
         kv_len = torch.full((B,), L, dtype=torch.int32, device=dev)
-        rope = torch.full((B,), start, dtype=torch.int32, device=dev)
         _, normed = self._block(hidden.to(torch.bfloat16).contiguous(),
                                 next_emb.to(torch.bfloat16).contiguous(), kc, vc, zeros, kv_len,
                                 rope, None)

@@ -4,7 +4,8 @@ Runs only in the build container, where the giapnguyen74/lollm checkout is at
 /root/reference; the reference never travels with the repository (only the vectors
 written here do).  It is imported for the functions nothing else pins:
 
-  * `MTP.forward` (src/qwen3_5/mtp.py:61-73) at L = 1..4 and with explicit positions,
+  * `MTP.forward` (src/qwen3_5/mtp.py:61-73) at L = 1..4 and with explicit positions
+    (consecutive, and a vector that is neither consecutive nor increasing),
     on the micro and tiny seeded weights: the [emb ; hidden] concatenation order, the
     pre-fc norms, positions 1..L and the cache-less causal block;
   * `speculate` (mtp.py:76-89) on the micro weights;
@@ -87,6 +88,15 @@ def mtp_forward_cases(ref_mtp, ref_weights, tag, raw, out):
     out[f"{tag}.mtp_pos.hidden"], out[f"{tag}.mtp_pos.next_emb"] = h, e
     out[f"{tag}.mtp_pos.positions"] = pos
     out[f"{tag}.mtp_pos.out"] = y.contiguous()
+    # a positions vector that is neither consecutive nor increasing
+    h = torch.randn(2, 4, H, generator=g)
+    e = torch.randn(2, 4, H, generator=g) * 0.05
+    pos = torch.tensor([5, 17, 18, 2])
+    with torch.no_grad():
+        y = mtp(h, e, positions=pos)
+    out[f"{tag}.mtp_pos_nc.hidden"], out[f"{tag}.mtp_pos_nc.next_emb"] = h, e
+    out[f"{tag}.mtp_pos_nc.positions"] = pos
+    out[f"{tag}.mtp_pos_nc.out"] = y.contiguous()
     return model, mtp
 
 

@@ -53,10 +53,11 @@ def test_mtp_forward_matches_reference(ref, micro, tiny, tag, L):
                                rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("case", ["mtp_pos", "mtp_pos_nc"])
 @pytest.mark.parametrize("tag", ["micro", "tiny"])
-def test_mtp_forward_positions_match_reference(ref, micro, tiny, tag):
+def test_mtp_forward_positions_match_reference(ref, micro, tiny, tag, case):
     W, cfg = micro if tag == "micro" else tiny
-    p = f"{tag}.mtp_pos."
+    p = f"{tag}.{case}."
     got = R.mtp_forward(W, cfg, ref[p + "hidden"], ref[p + "next_emb"], ref[p + "positions"])
     torch.testing.assert_close(got, ref[p + "out"], rtol=1e-5, atol=1e-5)
 

@@ -104,29 +104,192 @@ def test_mtp_forward_matches_reference(ref, micro, tiny, tag, L):
     close_bf16(got, ref[f"{tag}.mtp{L}.out"], R.mtp_forward(W16, cfg, h, e))
 
 
+@pytest.mark.parametrize("case", ["mtp_pos", "mtp_pos_nc"])
 @pytest.mark.parametrize("tag", ["micro", "tiny"])
-def test_mtp_forward_positions_match_reference(ref, micro, tiny, tag):
+def test_mtp_forward_positions_match_reference(ref, micro, tiny, tag, case):
+    """Explicit positions (mtp.py:61-67): consecutive (7, 8, 9) and a vector that is
+    neither consecutive nor increasing (5, 17, 18, 2), each token roped at its own."""
     model, mtp, W16, cfg = micro if tag == "micro" else tiny
-    p = f"{tag}.mtp_pos."
+    p = f"{tag}.{case}."
     h, e, pos = ref[p + "hidden"].bfloat16(), ref[p + "next_emb"].bfloat16(), ref[p + "positions"]
     got = mtp(h.cuda(), e.cuda(), positions=pos.cuda())
     close_bf16(got, ref[p + "out"], R.mtp_forward(W16, cfg, h, e, pos))
 
 
+_PLAIN_LINEAR = R.linear
+
+
+def _dithered_linear(seed):
+    """The oracle's bf16 `linear` with its one rounding moved: the fp32 product gets a
+    uniform offset of up to half a bf16 ulp before rounding to nearest, so about a quarter
+    of the outputs round the other way -- the freedom any bf16 implementation has (the
+    accumulation order, fused kernels that skip or move a rounding)."""
+    gen = torch.Generator().manual_seed(seed)
+
+    def lin(x, w):
+        if x.dtype != torch.bfloat16:
+            return _PLAIN_LINEAR(x, w)
+        y = x.float() @ w.float().t()
+        ulp = torch.ldexp(torch.ones_like(y), torch.frexp(y)[1] - 8)
+        d = (torch.rand(y.shape, generator=gen) - 0.5) * ulp
+        return torch.where(y == 0, y, y + d).bfloat16()
+    return lin
+
+
 def test_speculate_matches_reference(ref, micro):
-    """speculate chains the main model and the MTP head, and the head amplifies deviations
-    of its hidden input about tenfold (measured on this model: a 0.03 change of the
-    0.37-scale hidden stream moves the 3.8-scale MTP output by 0.38), so one element's
-    max error is a noisy statistic here: the bar is the RMS error, at most twice the
-    reference's own bf16 RMS error, with the max error within four times its max."""
+    """speculate (mtp.py:76-89) against the reference's fp32 logits on its fixture ids.
+    The bar is the model tests' (twice the bf16 error plus 1e-3 of the scale), with the
+    bf16 error measured as the spread of the reference's own bf16 arithmetic on this
+    input: the oracle's bf16 flow and 16 flows whose GEMM outputs round differently (the
+    fixture's plain bf16 flow is 0.036 from the fp32 logits, the others 0.036-0.079, max
+    |logit| 1.5).  This input is unusually sensitive: one position amplifies a layer-0
+    rounding ~100x (the GPU and the oracle's bf16 flow have identical local errors there,
+    test_speculate_stages_match_oracle; on 24 other inputs the GPU's error is 0.75-1.21x
+    the oracle bf16 flow's, test_speculate_matches_oracle_on_seeded_inputs)."""
     from lollm_amd.qwen3_5.mtp import speculate
     model, mtp, W16, cfg = micro
     ids = ref["micro.spec.ids"]
     got = speculate(model, mtp, ids.cuda()).float().cpu()
-    want, r16 = ref["micro.spec.logits"], R.speculate(W16, cfg, ids).float()
-    rms = lambda t: t.pow(2).mean().sqrt().item()  # noqa: E731
-    assert rms(got - want) <= 2 * rms(r16 - want), (rms(got - want), rms(r16 - want))
-    assert (got - want).abs().max() <= 4 * (r16 - want).abs().max()
+    want = ref["micro.spec.logits"]
+    flows = [R.speculate(W16, cfg, ids).float()]
+    try:
+        for seed in range(16):
+            R.linear = _dithered_linear(seed)
+            flows.append(R.speculate(W16, cfg, ids).float())
+    finally:
+        R.linear = _PLAIN_LINEAR
+    spread = max((f - want).abs().max().item() for f in flows)
+    err = (got - want).abs().max().item()
+    print(f"speculate max err {err:.4g}; the oracle's bf16 flows {spread:.4g}", flush=True)
+    assert err <= 2 * spread + 1e-3 * want.abs().max().item()
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_speculate_matches_oracle_on_seeded_inputs(micro, seed):
+    """speculate on seeded ids (B = 2, T = 9 and 17) against the oracle's fp32 speculate
+    (which matches the reference's own at 1e-4, tests/test_oracle_reference.py), at the
+    plain bf16 bar against the oracle's bf16 flow on the same ids."""
+    from lollm_amd.qwen3_5.mtp import speculate
+    model, mtp, W16, cfg = micro
+    T = 9 if seed < 6 else 17
+    ids = torch.randint(0, cfg.vocab_size, (2, T), generator=torch.Generator().manual_seed(1000 + seed))
+    got = speculate(model, mtp, ids.cuda())
+    W32 = {k: v.float() for k, v in W16.items()}
+    close_bf16(got, R.speculate(W32, cfg, ids), R.speculate(W16, cfg, ids))
+
+
+def test_speculate_stages_match_oracle(ref, micro):
+    """Every stage of speculate's chain on the fixture ids, each from the GPU's own input
+    to that stage: the main model's four layers (mixer + residual, then MLP + residual),
+    the MTP head's pre-fc norms and fc, input norm, attention, o_proj + residual, norm,
+    gate|up with SwiGLU, down + residual, final norm, and the lm_head -- each within the
+    plain bf16 bar of the oracle's fp32 stage (twice the oracle bf16 stage's error on the
+    same input plus 1e-3 of the scale).  The stages are driven through the model's own
+    objects, and the stream they form is checked bit for bit against forward()'s."""
+    import torch.nn.functional as F
+    model, mtp, W16, cfg = micro
+    W32 = {k: v.float() for k, v in W16.items()}
+    eps = cfg.rms_norm_eps
+    ids = ref["micro.spec.ids"]
+    B, T = ids.shape
+    cpu = lambda t: t.float().cpu()  # noqa: E731
+
+    def check(what, got, fn):
+        """fn(W, dtype) computes the stage in the oracle from the GPU's own input."""
+        print(f"stage {what}", flush=True)
+        close_bf16(got, fn(W32, torch.float32).float(), fn(W16, torch.bfloat16))
+
+    # ---- main model, layer by layer (modeling_qwen3_5.py:47-61)
+    cache = model.new_cache(B, T + 8)
+    x = model.model.embed_tokens(ids.cuda())
+    kv_len = cache.lengths + T
+    ws = model.attn_workspace(B, T, cache.max_len)
+    pos = torch.arange(T)
+    for i, layer in enumerate(model.model.layers):
+        p = f"model.layers.{i}."
+        xi = cpu(x)
+        if layer.layer_type == "full_attention":
+            st = cache.layers[i]
+            core = layer.self_attn.core(layer.input_layernorm(x), st["k"], st["v"], cache.lengths,
+                                        kv_len, workspace=ws)
+            mix = layer.self_attn.out
+
+            def mixer(W, dt, h):
+                cos, sin = R.rope_tables(pos, cfg.rotary_dim, cfg.rope_theta, dt)
+                return R.gated_attention(W, p + "self_attn.", cfg, h, cos, sin, None, i)
+        else:
+            core = layer.linear_attn.core(layer.input_layernorm(x), cache, i)
+            mix = layer.linear_attn.out
+
+            def mixer(W, dt, h):
+                return R.gated_deltanet(W, p + "linear_attn.", cfg, h, None, None, False)[0]
+        y, x2 = mix.add_norm(core, x, layer.post_attention_layernorm)
+        check(f"layer {i} mixer", x2, lambda W, dt: xi.to(dt) + mixer(
+            W, dt, R.rmsnorm_plus1(xi.to(dt), W[p + "input_layernorm.weight"], eps)))
+        x2c = cpu(x2)
+        nxt = (model.model.layers[i + 1].input_layernorm if i + 1 < len(model.model.layers)
+               else model.model.norm)
+        _, x = layer.mlp.down.add_norm(layer.mlp.gate_up(y), x2, nxt)
+        check(f"layer {i} mlp", x, lambda W, dt: x2c.to(dt) + R.mlp(
+            W, p + "mlp.", R.rmsnorm_plus1(x2c.to(dt), W[p + "post_attention_layernorm.weight"], eps)))
+    _, _, hidden = model(ids.cuda(), return_hidden=True)
+    assert torch.equal(x, hidden)
+
+    # ---- MTP head (mtp.py:61-73) over hidden[:, :-1] and the embeddings of ids[:, 1:]
+    h, e = hidden[:, :-1].contiguous(), model.model.embed_tokens(ids[:, 1:].cuda())
+    hc, ec = cpu(h), cpu(e)
+    Lm = T - 1
+    m0 = mtp.layers[0]
+    q = "mtp.layers.0."
+    fc_in = torch.cat([mtp.pre_fc_norm_embedding(e), mtp.pre_fc_norm_hidden(h)], -1)
+    check("mtp pre-fc norms", fc_in, lambda W, dt: torch.cat(
+        [R.rmsnorm_plus1(ec.to(dt), W["mtp.pre_fc_norm_embedding.weight"], eps),
+         R.rmsnorm_plus1(hc.to(dt), W["mtp.pre_fc_norm_hidden.weight"], eps)], -1))
+    fc_c = cpu(fc_in)
+    h_in, fc = mtp.fc.add_norm(fc_in, None, m0.input_layernorm)
+    check("mtp fc", fc, lambda W, dt: R.linear(fc_c.to(dt), W["mtp.fc.weight"]))
+    fcc = cpu(fc)
+    check("mtp input norm", h_in, lambda W, dt: R.rmsnorm_plus1(fcc.to(dt), W[q + "input_layernorm.weight"], eps))
+    hic = cpu(h_in)
+    kc, vc = mtp.scratch_cache(B, Lm)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    core = m0.self_attn.core(h_in, kc, vc, torch.zeros(B, **i32), torch.full((B,), Lm, **i32),
+                             rope_pos=torch.ones(B, **i32))
+
+    def attn_core(W, dt):
+        x_ = hic.to(dt)
+        H, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        a = q + "self_attn."
+        cos, sin = R.rope_tables(torch.arange(1, Lm + 1), cfg.rotary_dim, cfg.rope_theta, dt)
+        qg = R.linear(x_, W[a + "q_proj.weight"]).view(B, Lm, H, 2 * D)
+        qq, gate = qg[..., :D], qg[..., D:].reshape(B, Lm, H * D)
+        qq = R.rmsnorm_plus1(qq, W[a + "q_norm.weight"], eps).transpose(1, 2)
+        kk = R.rmsnorm_plus1(R.linear(x_, W[a + "k_proj.weight"]).view(B, Lm, Hkv, D),
+                             W[a + "k_norm.weight"], eps).transpose(1, 2)
+        vv = R.linear(x_, W[a + "v_proj.weight"]).view(B, Lm, Hkv, D).transpose(1, 2)
+        qq, kk = R.rope_apply(qq, cos, sin), R.rope_apply(kk, cos, sin)
+        o = R.sdpa_offset_causal(qq, R.repeat_kv(kk, cfg.n_rep), R.repeat_kv(vv, cfg.n_rep))
+        return o.transpose(1, 2).reshape(B, Lm, H * D) * torch.sigmoid(gate)
+    check("mtp attention", core, attn_core)
+    corec = cpu(core)
+    y, x2 = m0.self_attn.out.add_norm(core, fc, m0.post_attention_layernorm)
+    check("mtp o_proj + residual", x2, lambda W, dt: fcc.to(dt) + R.linear(
+        corec.to(dt), W[q + "self_attn.o_proj.weight"]))
+    x2c = cpu(x2)
+    check("mtp post norm", y, lambda W, dt: R.rmsnorm_plus1(
+        x2c.to(dt), W[q + "post_attention_layernorm.weight"], eps))
+    yc = cpu(y)
+    g = m0.mlp.gate_up(y)
+    check("mtp gate|up", g, lambda W, dt: F.silu(R.linear(yc.to(dt), W[q + "mlp.gate_proj.weight"]))
+          * R.linear(yc.to(dt), W[q + "mlp.up_proj.weight"]))
+    gc = cpu(g)
+    normed, x3 = m0.mlp.down.add_norm(g, x2, mtp.norm)
+    check("mtp down + residual", x3, lambda W, dt: x2c.to(dt) + R.linear(
+        gc.to(dt), W[q + "mlp.down_proj.weight"]))
+    x3c = cpu(x3)
+    check("mtp final norm", normed, lambda W, dt: R.rmsnorm_plus1(x3c.to(dt), W["mtp.norm.weight"], eps))
+    nc = cpu(normed)
+    check("lm_head", model.lm_head(normed), lambda W, dt: R.linear(nc.to(dt), W["lm_head.weight"]))
 
 
 # ----------------------------------------------------------- greedy trajectories

@@ -63,11 +63,22 @@ def test_spec_accept_noalloc_matches_workspace_entry_point(temp, top_k, top_p):
 
 
 def test_spec_accept_noalloc_refuses_oversized_shapes():
+    """B = 2048 rows with k = 8 sampled drafts need more than the 1 MiB array (the
+    workspace does not depend on the vocabulary), so the call returns LOLLM_EUNSUPPORTED
+    before any launch.  The buffers are real device tensors over a vocabulary of 8, so
+    that even a launch past the guard would only read and write memory it owns."""
     from lollm_amd import _lib
     L = _lib.lib()
-    B, k = 2048, 8
+    B, k, V = 2048, 8, 8
     assert L.lollm_spec_workspace_bytes(B, k, 1) > (1 << 20)
-    rc = L.lollm_spec_accept_noalloc(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
-                                     B, k, 151936, 1.0, 0, 1.0, 0, 0, None, ctypes.c_void_p(16),
-                                     ctypes.c_void_p(16), None)
+    tgt = torch.zeros(B, k + 1, V, dtype=torch.bfloat16, device="cuda")
+    drf = torch.zeros(B, k, V, dtype=torch.bfloat16, device="cuda")
+    drafts = torch.zeros(B, k, dtype=torch.int32, device="cuda")
+    na = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+    nt = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+    rc = L.lollm_spec_accept_noalloc(_ptr(tgt), _ptr(drf), _ptr(drafts), B, k, V, 1.0, 0, 1.0, 0, 0,
+                                     None, _ptr(na), _ptr(nt),
+                                     torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
     assert rc == 2          # LOLLM_EUNSUPPORTED, before any launch
+    assert bool((na == -1).all()) and bool((nt == -1).all())
