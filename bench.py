@@ -11,9 +11,14 @@ A step = draft chain (3 MTP passes + lm_head + argmax) + one verify forward over
 1 + k positions of all 16 sequences + acceptance + commit, replayed from a HIP graph.
 `value` = emitted tokens per second over the K timed steps (the pending token plus
 the accepted drafts of every sequence; random weights accept almost nothing, so this
-is close to B tokens per step).  Also reported: the accepted-length histogram, the
-verify-step time, the dominant hand-written kernel's bandwidth against the 8 TB/s
-HBM3E peak (measured live with HIP events), the isolated-kernel workloads, and the
+is close to B tokens per step).  `roofline` is the step itself: its algorithmic HBM
+bytes (every weight the verify pass and the k draft passes stream, the GDN states and
+replay records, the conv windows, the KV cache at the run's context, the logits) over
+the HIP-event time of one graph replay, against the 8 TB/s HBM3E peak.  Also
+reported: the accepted-length histogram, the verify-step time, a timed accepted path
+(drafts forced to the verify pass's own greedy fixed point, so every step commits
+k + 1 tokens per sequence), the hot kernels measured the way the step runs them (each
+timed over every layer's own buffers in turn), the isolated-kernel workloads, and the
 CPU restatement of the reference path timed on the host.
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 8]
@@ -107,6 +112,8 @@ def run_e2e(model, mtp, cfg, B, prompt_len, k, steps, warmup, temperature, top_p
     # timed region: K graph replays; per-step accepted counts read after the region
     counts_before = dec.out_count.clone()
     hist_before = dec.accept_hist.clone()
+    ctx_before = dec.cache.lengths.float().sum().item()
+    marker()
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -115,14 +122,27 @@ def run_e2e(model, mtp, cfg, B, prompt_len, k, steps, warmup, temperature, top_p
         dec.replay()
     e1.record()
     torch.cuda.synchronize()
+    marker()
     wall = time.perf_counter() - t_start
     gpu_s = e0.elapsed_time(e1) / 1000.0
     emitted = int((dec.out_count - counts_before).sum())
     hist = (dec.accept_hist - hist_before).cpu().tolist()
-    ctx = dec.cache.lengths.float().mean().item()
+    ctx_after = dec.cache.lengths.float().sum().item()
     return dec, {"emitted": emitted, "seconds": gpu_s, "wall_seconds": wall, "hist": hist,
                  "mean_accepted": sum(i * c for i, c in enumerate(hist)) / max(1, sum(hist)),
-                 "final_context_mean": ctx}
+                 "final_context_mean": ctx_after / B,
+                 # sum over the batch of the cache length a timed step starts from, averaged
+                 "ctx_sum_mean": (ctx_before + ctx_after) / 2 - (ctx_after - ctx_before) / (2 * steps)}
+
+
+MARKER_KERNEL = "scan"
+
+
+def marker():
+    """A small cumulative sum: its kernel (a scan, which the step never launches) marks
+    the start and the end of the timed region in a rocprofv3 trace."""
+    import torch
+    torch.cumsum(torch.ones(4096, device="cuda"), 0)
 
 
 def projection_paths(model, mtp, B, k):
@@ -174,8 +194,50 @@ def verify_breakdown(dec, iters=20):
 
 
 # ------------------------------------------------------------------------------------
-# the dominant hand-written kernel of the verify step: the fused GDN layer
+# the step's roofline and its hot kernels as the step runs them
 # ------------------------------------------------------------------------------------
+def step_bytes(cfg, B, k, ctx_sum, replayed, logits=True):
+    """Algorithmic HBM bytes of one speculative step: what must cross HBM at least once.
+    Weights (bf16): every decoder weight and the lm_head for the verify pass, and k times
+    the MTP layer's weights plus the lm_head for the draft chain (each draft streams them
+    again: 1.83 GB does not fit the 256 MB last-level cache).  GDN layers: the committed
+    state read and its copy written to the other half (B Hv Dk Dv fp32 each), the replay
+    records it applies (`replayed` positions over the batch) and the T it writes
+    (Hv (4 Dk + 16) bytes per position), the conv window read (K-1 rows) and written
+    (K-1+T rows).  Attention layers: the K and V rows of every sequence's context
+    (ctx_sum = sum of the kv lengths) and the T new rows.  The (B, T, V) bf16 logits
+    written and read once by the acceptance when the step samples (logits=True).
+    Activations between kernels are left out (they could stay on chip)."""
+    import math
+    from lollm_amd.qwen3_5.random_init import weight_shapes
+    T = k + 1
+    H, V = cfg.hidden_size, cfg.vocab_size
+    main = mtp = 0
+    for name, (shape, _) in weight_shapes(cfg, with_mtp=True).items():
+        if name.endswith("embed_tokens.weight") or name == "lm_head.weight":
+            continue
+        if name.startswith("mtp."):
+            mtp += math.prod(shape) * 2
+        else:
+            main += math.prod(shape) * 2
+    lm = V * H * 2
+    Hv, D, K = cfg.linear_num_value_heads, cfg.linear_key_head_dim, cfg.linear_conv_kernel_dim
+    n_gdn = sum(1 for i in range(cfg.num_hidden_layers) if cfg.layer_type(i) != "full_attention")
+    n_attn = cfg.num_hidden_layers - n_gdn
+    Hkv, Dh = cfg.num_key_value_heads, cfg.head_dim
+    parts = {
+        "verify_weights": main + lm,
+        "draft_chain_weights": k * (mtp + lm),
+        "gdn_state": n_gdn * 2 * B * Hv * D * D * 4,
+        "gdn_records": n_gdn * (replayed + B * T) * Hv * (4 * D + 16),
+        "conv_windows": n_gdn * B * (2 * (K - 1) + T) * cfg.conv_dim * 2,
+        "kv_cache": n_attn * (int(ctx_sum) + B * T) * Hkv * Dh * 2 * 2,
+        "logits": 2 * B * T * V * 2 if logits else 0,
+    }
+    parts["total"] = sum(parts.values())
+    return parts
+
+
 def gdn_layer_bytes(cfg, B, T, replayed=None):
     """Algorithmic HBM bytes of one short lollm_gdn_layer launch: read the committed
     half's state (B Hv Dk Dv fp32) and the records it replays (`replayed` positions over
@@ -192,33 +254,165 @@ def gdn_layer_bytes(cfg, B, T, replayed=None):
             + B * (K - 1 + T) * cfg.conv_dim * 2 + B * T * cfg.value_dim * 2)
 
 
-def gdn_layer_roofline(model, dec, iters=50):
-    import torch
-    import torch.nn.functional as F
-    cfg = model.cfg
-    B, T = dec.B, dec.k + 1
-    li = next(i for i in range(cfg.num_hidden_layers) if cfg.layer_type(i) != "full_attention")
-    gdn = model.model.layers[li].linear_attn
-    x = torch.randn(B, T, cfg.hidden_size, device="cuda").bfloat16()
-    proj = F.linear(x, gdn.w_in)
-    s = dec.cache.layers[li]
-    from lollm_amd import ops
-    out = torch.empty(B, T, cfg.value_dim, dtype=torch.bfloat16, device="cuda")
+def _rate(name, launches, us_total, byt_total, extra=None):
+    us = us_total / launches
+    gbs = byt_total / us_total / 1e3
+    row = {"kernel": name, "launches_per_step": launches, "avg_us": round(us, 2),
+           "bytes_per_launch": int(byt_total // launches), "achieved": round(gbs, 1),
+           "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    if extra:
+        row.update(extra)
+    return row
 
-    def launch():
-        ops.gdn_layer(proj, gdn.conv_w, gdn.A_log, gdn.dt_bias, gdn.norm_w, s["win"],
-                      dec.cache.conv_off, s["rec"], dec.cache.rec_half, s["rep"],
-                      dec.cache.replay, False, B, T, cfg.linear_num_key_heads,
-                      cfg.linear_num_value_heads, cfg.linear_key_head_dim,
-                      cfg.linear_conv_kernel_dim, cfg.rms_norm_eps, out=out)
-    us = time_fn(launch, iters)   # each launch replays the decode's committed records
-    byt = gdn_layer_bytes(cfg, B, T, int(dec.cache.replay.clamp(0, dec.cache.spec_slots).sum()))
-    gbs = byt / us / 1e3
-    return {"kernel": "lollm::gdn_layer_verify_kernel", "shape": f"B={B} T={T} Hv=32 Hk=16 D=128",
-            "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(gbs / PEAK_HBM_GBS, 4),
-            "traffic": measured_traffic("lollm::gdn_layer_verify_kernel", f"B={B} T={T} Hv=32 Hk=16 D=128"),
-            "avg_us": round(us, 2), "bytes_per_launch": byt}
+
+def in_step_kernels(model, mtp, dec, iters=2):
+    """The verify pass's hot kernels as the step runs them: each kind is captured in one
+    HIP graph that launches it once per layer of that kind, on that layer's own weights,
+    cache state and KV rows in turn (so a launch never finds its data in the 256 MB
+    last-level cache from the previous one, as in the step), and timed with HIP events
+    over the replays.  Per launch: the average time, the algorithmic bytes and their
+    rate against the 8 TB/s peak.  Attention is the (main + combine) pair; the
+    residual-stream projections include their merge + residual + RMSNorm kernel."""
+    import torch
+    from lollm_amd import ops
+    cfg, cache = model.cfg, dec.cache
+    B, T = dec.B, dec.k + 1
+    M = B * T
+    layers = model.model.layers
+    gdn_ids = [i for i, l in enumerate(layers) if l.layer_type != "full_attention"]
+    att_ids = [i for i, l in enumerate(layers) if l.layer_type == "full_attention"]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    rnd = lambda *shape: (0.5 * torch.randn(*shape, device="cuda", generator=g)).bfloat16()  # noqa: E731
+    out = {}
+    # fused GDN layer, one launch per GDN layer on its own state / records / window
+    Hk, Hv, D = cfg.linear_num_key_heads, cfg.linear_num_value_heads, cfg.linear_key_head_dim
+    projs = {i: rnd(B, T, layers[i].linear_attn.in_proj.N) for i in gdn_ids}
+    o = torch.empty(B, T, cfg.value_dim, dtype=torch.bfloat16, device="cuda")
+
+    def gdn_all():
+        for i in gdn_ids:
+            gdn, s = layers[i].linear_attn, cache.layers[i]
+            ops.gdn_layer(projs[i], gdn.conv_w, gdn.A_log, gdn.dt_bias, gdn.norm_w, s["win"],
+                          cache.conv_off, s["rec"], cache.rec_half, s["rep"], cache.replay, False,
+                          B, T, Hk, Hv, D, cfg.linear_conv_kernel_dim, cfg.rms_norm_eps, out=o)
+    replayed = int(cache.replay.clamp(0, cache.spec_slots).sum())
+    us = time_fn(gdn_all, iters)
+    out["gdn_layer"] = _rate("lollm::gdn_layer_verify_kernel", len(gdn_ids), us,
+                             len(gdn_ids) * gdn_layer_bytes(cfg, B, T, replayed),
+                             {"shape": f"B={B} T={T} Hv={Hv} Hk={Hk} D={D}, {replayed} records replayed"})
+    del projs
+    # gated attention (verify + combine), one launch per attention layer on its KV rows
+    Hq, Hkv, Dh = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    q, gate = rnd(B, T, Hq, Dh), rnd(B, T, Hq * Dh)
+    kv_len = (cache.lengths + T).contiguous()
+    ws = model.attn_workspace(B, T, cache.max_len)
+    ao = torch.empty(B, T, Hq * Dh, dtype=torch.bfloat16, device="cuda")
+
+    def attn_all():
+        for i in att_ids:
+            s = cache.layers[i]
+            ops.attn_verify(q, s["k"], s["v"], kv_len, gate, grid=model.attn_grid, workspace=ws, out=ao)
+    us = time_fn(attn_all, iters)
+    ctx = int(kv_len.sum())
+    out["attention"] = _rate("lollm::attn_verify_kernel + attn_combine_kernel", len(att_ids), us,
+                             len(att_ids) * (ctx * Hkv * Dh * 4 + 3 * M * Hq * Dh * 2),
+                             {"shape": f"B={B} T={T} Hq={Hq} Hkv={Hkv} D={Dh}, mean context {ctx / B:.0f}"})
+    # the verify pass's projections, one kind at a time over every layer that has it
+    H, F = cfg.hidden_size, cfg.intermediate_size
+    x, res = rnd(M, H), rnd(M, H)
+
+    def gemm_kind(name, picks, fn):
+        projs_ = [p for p in picks]
+        us = time_fn(lambda: [fn(p) for p in projs_], iters)
+        byt = sum(p.N * p.K * 2 + M * p.K * 2 + M * (p.N // (2 if p.epilogue else 1)) * 2 for p in projs_)
+        out[name] = _rate(f"lollm_gemm {projs_[0].N}x{projs_[0].K}, M={M}", len(projs_), us, byt,
+                          {"grid": projs_[0].grid(M)})
+    gdn_layers = [layers[i] for i in gdn_ids]
+    att_layers = [layers[i] for i in att_ids]
+    norm = layers[0].input_layernorm
+    core_v = rnd(M, cfg.value_dim)
+    core_a = rnd(M, Hq * Dh)
+    act = rnd(M, F)
+    gemm_kind("gemm_gdn_in_proj", [l.linear_attn.in_proj for l in gdn_layers], lambda p: p(x))
+    gemm_kind("gemm_attn_qkv", [l.self_attn.qkv for l in att_layers], lambda p: p(x))
+    gemm_kind("gemm_gdn_out_proj_norm", [l.linear_attn.out_proj for l in gdn_layers],
+              lambda p: p.add_norm(core_v, res, norm))
+    gemm_kind("gemm_attn_o_proj_norm", [l.self_attn.o_proj for l in att_layers],
+              lambda p: p.add_norm(core_a, res, norm))
+    gemm_kind("gemm_mlp_gate_up", [l.mlp.gate_up for l in layers], lambda p: p(x))
+    gemm_kind("gemm_mlp_down_norm", [l.mlp.down for l in layers], lambda p: p.add_norm(act, res, norm))
+    gemm_kind("gemm_lm_head", [model.lm_head], lambda p: p(x))
+    kinds = [v for key, v in out.items() if key.startswith("gemm_")]
+    tot_us = sum(v["avg_us"] * v["launches_per_step"] for v in kinds)
+    tot_b = sum(v["bytes_per_launch"] * v["launches_per_step"] for v in kinds)
+    out["gemm_verify_all"] = {"us_per_step": round(tot_us, 1), "bytes_per_step": tot_b,
+                              "achieved": round(tot_b / tot_us / 1e3, 1), "peak": PEAK_HBM_GBS,
+                              "unit": "GB/s", "frac": round(tot_b / tot_us / 1e3 / PEAK_HBM_GBS, 4)}
+    return out
+
+
+def accepted_path(model, mtp, cfg, B, prompt_len, k, steps, seed):
+    """The step when every draft is accepted: temperature 0, drafts forced to the verify
+    pass's own greedy fixed point (k rounds of the verify forward, not committed, so the
+    argmax at position i already follows drafts 1..i), computed before each step outside
+    the timed region; the step itself is the graph-replayed draft chain (its own drafts
+    then overwritten by the forced ones), verify, greedy acceptance and commit, timed
+    with HIP events around each replay.  Every sequence commits k + 1 tokens per step."""
+    import torch
+    from lollm_amd import ops
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 1)
+    prompts = torch.randint(0, cfg.vocab_size, (B, prompt_len), device="cuda", generator=gen)
+    n = (steps + 4) * (k + 1)
+    dec = SpecDecoder(model, mtp, B, prompt_len + n + 8, k=k, temperature=0.0, out_capacity=n + 8)
+    dec.prefill(prompts)
+    forced = torch.zeros(B, k, dtype=torch.int32, device="cuda")
+    lm = model.lm_head
+    am = torch.empty(B * (k + 1), dtype=torch.int32, device="cuda")
+
+    def fixed_point():
+        d = torch.zeros(B, k, dtype=torch.int32, device="cuda")
+        for _ in range(k):
+            ids = torch.cat([dec.pending.view(B, 1), d], 1)
+            _, normed = model.hidden_states(ids, dec.cache)
+            ops.gemm_argmax(normed.reshape(-1, lm.K), lm.tiled, lm.N, lm.K, out=am, grid=lm.grid())
+            d = am.view(B, k + 1)[:, :k].contiguous()
+        forced.copy_(d)
+    chain = dec._draft_chain
+
+    def forced_chain():
+        chain()
+        dec.drafts.copy_(forced)
+    dec._draft_chain = forced_chain
+    for _ in range(2):
+        fixed_point()
+        dec.step()
+    dec.capture()
+    hist0 = dec.accept_hist.clone()
+    total = 0.0
+    for _ in range(steps):
+        fixed_point()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dec.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        total += e0.elapsed_time(e1)
+    hist = (dec.accept_hist - hist0).cpu().tolist()
+    ms = total / steps
+    emitted = sum((i + 1) * c for i, c in enumerate(hist))
+    ctx = float(dec.cache.lengths.float().mean())
+    byt = step_bytes(cfg, B, k, (ctx - steps * (k + 1) / 2) * B, B * (k + 1), logits=False)
+    del dec
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(ms, 4), "tok_s": round(emitted / (total / 1e3), 1),
+            "tokens_per_step": round(emitted / steps, 2), "accepted_length_hist": hist,
+            "steps": steps, "temperature": 0.0,
+            "roofline_frac": round(byt["total"] / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "note": "drafts forced to the verify pass's greedy fixed point (computed outside "
+                    "the timed region); every draft accepted, k + 1 tokens per sequence per step"}
 
 
 # ------------------------------------------------------------------------------------
@@ -629,6 +823,116 @@ def measured_traffic(kernel, shape):
     return t.get("traffic_bytes")
 
 
+STEP_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "step_traffic.json")
+STEP_PROBE_STEPS = 3
+
+
+def pmc_probe_step(B=16, prompt_len=2048, k=3):
+    """For the counter runs of the whole step: the headline workload (model, prefill, two
+    eager steps, the graph capture and two warm replays), then STEP_PROBE_STEPS graph
+    replays between two marker kernels, then torch.neg over 256 MiB 5 times (the counter
+    calibration).  summarize_pmc_step() sums each counter over the dispatches between
+    the markers."""
+    import torch
+    raw, cfg, model, mtp, keep = build_8b(5)
+    del keep
+    dec, _ = run_e2e(model, mtp, cfg, B, prompt_len, k, STEP_PROBE_STEPS, 4, 0.7, 0.95, 5)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    x = torch.randn(PROBE_COPY_BYTES // 4, device="cuda", generator=g)
+    y = torch.empty_like(x)
+    for _ in range(5):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    log(f"pmc step probe: {STEP_PROBE_STEPS} replays between markers; 5 x neg over "
+        f"{PROBE_COPY_BYTES} bytes")
+
+
+def _csv_rows(directory, suffix):
+    import csv
+    import glob
+    files = sorted(glob.glob(os.path.join(directory, "**", "*" + suffix), recursive=True))
+    if not files:
+        raise FileNotFoundError(f"no *{suffix} under {directory}")
+    with open(files[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def _between_markers(rows, key):
+    """Rows strictly between the first two markers, ordered by `key` (a marker may be
+    more than one consecutive scan kernel)."""
+    rows = sorted(rows, key=lambda r: int(r[key]))
+    idx = [i for i, r in enumerate(rows) if MARKER_KERNEL in r["Kernel_Name"]]
+    j = 1
+    while j < len(idx) and idx[j] == idx[j - 1] + 1:
+        j += 1
+    if j >= len(idx):
+        raise ValueError("the two timed-region markers are not in the trace")
+    return rows[idx[j - 1] + 1:idx[j]]
+
+
+def summarize_pmc_step(directory, out=STEP_TRAFFIC_FILE):
+    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch, rocprofv3 --pmc over
+    `bench.py --pmc-probe-step`, in <directory>/pmc_FETCH_SIZE and pmc_WRITE_SIZE) summed
+    over the dispatches of the probe's timed replays, per step, each counter scaled by
+    what it reads for torch.neg over 256 MiB (which reads and writes 256 MiB)."""
+    import statistics
+    res = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        rows = _csv_rows(os.path.join(directory, f"pmc_{ctr}"), "counter_collection.csv")
+        step = _between_markers(rows, "Dispatch_Id")
+        neg = [float(r["Counter_Value"]) for r in rows if "neg" in r["Kernel_Name"]][-5:]
+        scale = (PROBE_COPY_BYTES / 1024) / statistics.median(neg)
+        total = sum(float(r["Counter_Value"]) for r in step)
+        res[ctr] = {"kib_per_step": total / STEP_PROBE_STEPS, "dispatches_per_step":
+                    len(step) / STEP_PROBE_STEPS, "copy_kib": statistics.median(neg),
+                    "scale": round(scale, 6), "bytes_per_step": int(total / STEP_PROBE_STEPS * 1024 * scale)}
+    t = {"workload": "dense 8B-class step, B=16, k=3, T=0.7, 2048-token prompts",
+         "fetch": res["FETCH_SIZE"], "write": res["WRITE_SIZE"],
+         "traffic_bytes_per_step": res["FETCH_SIZE"]["bytes_per_step"] + res["WRITE_SIZE"]["bytes_per_step"],
+         "copy_kernel": "torch.neg over 256 MiB fp32 (reads and writes 268435456 bytes)",
+         "commands": [f"cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc {c} --output-format csv "
+                      f"-d <out>/pmc_{c} -o run -- python3 <repo>/bench.py --pmc-probe-step"
+                      for c in ("FETCH_SIZE", "WRITE_SIZE")] +
+                     ["python3 bench.py --summarize-pmc-step <out>"]}
+    with open(out, "w") as f:
+        json.dump(t, f, indent=1)
+    print(json.dumps(t, indent=1))
+
+
+def measured_step_traffic():
+    try:
+        with open(STEP_TRAFFIC_FILE) as f:
+            return json.load(f).get("traffic_bytes_per_step")
+    except (OSError, ValueError):
+        return None
+
+
+def summarize_trace(directory, steps=None):
+    """Markdown table of one timed step from `rocprofv3 --kernel-trace` of bench.py (the
+    csv under <directory>): every kernel between the two timed-region markers, per step
+    (total, launches, average), the step's span, and the bench line's step time for
+    comparison."""
+    import collections
+    rows = _between_markers(_csv_rows(directory, "kernel_trace.csv"), "Start_Timestamp")
+    if steps is None:
+        steps = sum(1 for r in rows if "spec_commit_kernel" in r["Kernel_Name"])
+    span = (int(rows[-1]["End_Timestamp"]) - int(rows[0]["Start_Timestamp"])) / 1e3 / steps
+    agg = collections.defaultdict(lambda: [0.0, 0])
+    for r in rows:
+        name = r["Kernel_Name"].split("(")[0].replace("void ", "")
+        a = agg[name]
+        a[0] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        a[1] += 1
+    busy = sum(v[0] for v in agg.values()) / steps
+    print(f"timed steps: {steps}; span per step {span:.1f} us; kernel time per step {busy:.1f} us; "
+          f"launches per step {len(rows) / steps:.1f}\n")
+    print("| us per step | launches per step | avg us | % of span | kernel |")
+    print("|---:|---:|---:|---:|---|")
+    for name, (us, n) in sorted(agg.items(), key=lambda kv: -kv[1][0]):
+        print(f"| {us / steps:.1f} | {n / steps:.1f} | {us / n:.2f} | {100 * us / steps / span:.1f} | `{name[:80]}` |")
+
+
 # ------------------------------------------------------------------------------------
 def main():
     ap = argparse.ArgumentParser()
@@ -641,8 +945,22 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-isolated", action="store_true", help="skip the isolated kernels")
     ap.add_argument("--pmc-probe", action="store_true",
-                    help="only launch the roofline kernel and a copy calibration (for rocprofv3 --pmc)")
+                    help="only launch the hot kernels and a copy calibration (for rocprofv3 --pmc)")
+    ap.add_argument("--pmc-probe-step", action="store_true",
+                    help="only replay the step between markers and a copy calibration (for rocprofv3 --pmc)")
+    ap.add_argument("--summarize-pmc-step", metavar="DIR",
+                    help="write profiles/step_traffic.json from the two --pmc-probe-step counter runs")
+    ap.add_argument("--summarize-trace", metavar="DIR",
+                    help="print the per-step kernel table of a rocprofv3 --kernel-trace of bench.py")
+    ap.add_argument("--accepted-steps", type=int, default=32,
+                    help="timed steps of the accepted path (0: skip it)")
     args = ap.parse_args()
+    if args.summarize_pmc_step:
+        summarize_pmc_step(args.summarize_pmc_step)
+        return
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the workload; --gpus {args.gpus} is not "
               "supported (this build runs on a single MI355X)", file=sys.stderr)
@@ -653,6 +971,9 @@ def main():
     if args.pmc_probe:
         pmc_probe()
         return
+    if args.pmc_probe_step:
+        pmc_probe_step(args.batch, args.prompt_len, args.k)
+        return
     temperature, top_p, seed = 0.7, 0.95, 5
     t0 = time.time()
     raw, cfg, model, mtp, keep = build_8b(seed)
@@ -662,10 +983,22 @@ def main():
     value = e2e["emitted"] / e2e["seconds"]
     ms_per_step = e2e["seconds"] * 1000.0 / args.steps
     log(f"e2e: {value:.1f} tok/s, {ms_per_step:.3f} ms/step, hist {e2e['hist']}")
+    # the step's roofline: algorithmic bytes of one graph replay over its HIP-event time
+    sb = step_bytes(cfg, args.batch, args.k, e2e["ctx_sum_mean"],
+                    args.batch * (1 + e2e["mean_accepted"]), logits=not dec.greedy_argmax)
+    gbs = sb["total"] / (ms_per_step * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": measured_step_traffic()}
+    log(f"step: {sb['total'] / 1e9:.2f} GB algorithmic, {gbs:.0f} GB/s, frac {roof['frac']}")
     parts = verify_breakdown(dec)
-    roof = gdn_layer_roofline(model, dec)
-    log(f"gdn_layer: {roof['avg_us']} us, {roof['achieved']} GB/s")
-    kernels = {"gdn_layer_verify": roof}
+    kernels = {"in_step": in_step_kernels(model, mtp, dec)}
+    for key, v in kernels["in_step"].items():
+        log(f"in step {key}: {v.get('avg_us', v.get('us_per_step'))} us, frac {v['frac']}")
+    accepted = None
+    if args.accepted_steps > 0:
+        accepted = accepted_path(model, mtp, cfg, args.batch, args.prompt_len, args.k,
+                                 args.accepted_steps, seed)
+        log(f"accepted path: {accepted['ms_per_step']} ms/step, {accepted['tok_s']} tok/s")
     cpu_legs = not args.no_cpu
     if cpu_legs:
         torch.set_num_threads(os.cpu_count())
@@ -706,8 +1039,11 @@ def main():
         "accepted_length_hist": e2e["hist"], "mean_accepted": round(e2e["mean_accepted"], 4),
         "verify_step_us": round(parts["verify_forward_us"], 1), "step_parts_us":
             {k_: round(v, 1) for k_, v in parts.items()},
-        "roofline": {k_: roof[k_] for k_ in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
-        "roofline_kernel": roof["kernel"],
+        "roofline": roof,
+        "roofline_kernel": "the whole speculative step: one graph replay (draft chain, verify "
+                           "forward, acceptance, commit)",
+        "roofline_bytes": {k_: int(v) for k_, v in sb.items()},
+        "accepted_path": accepted,
         "projection_paths": projection_paths(model, mtp, args.batch, args.k),
         "kernels": kernels,
         "cpu_baseline": cpu,
