@@ -728,7 +728,6 @@ def cpu_baseline(raw, cfg, keep, dec, k, temperature, top_p, seed):
 # `python3 bench.py --pmc-probe`, calibrated by a plain copy-like kernel of known size
 # in the same process; the measured figures are committed in profiles/traffic.json
 # ------------------------------------------------------------------------------------
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 PROBE_COPY_BYTES = 256 << 20
 
 
@@ -808,19 +807,6 @@ def pmc_probe(B=16, T=4, launches=20):
     torch.cuda.synchronize()
     log(f"pmc probe: {launches} launches each of {', '.join(PROBE_ORDER)}; "
         f"5 x neg over {PROBE_COPY_BYTES} bytes")
-
-
-def measured_traffic(kernel, shape):
-    """HBM bytes per launch from the committed counter runs, if they cover this kernel
-    and shape (None otherwise)."""
-    try:
-        with open(TRAFFIC_FILE) as f:
-            t = json.load(f)
-    except (OSError, ValueError):
-        return None
-    if t.get("kernel") != kernel or t.get("shape") != shape:
-        return None
-    return t.get("traffic_bytes")
 
 
 STEP_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "step_traffic.json")
