@@ -724,9 +724,10 @@ def cpu_baseline(raw, cfg, keep, dec, k, temperature, top_p, seed):
 
 
 # ------------------------------------------------------------------------------------
-# HBM traffic of the roofline kernel: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs over
-# `python3 bench.py --pmc-probe`, calibrated by a plain copy-like kernel of known size
-# in the same process; the measured figures are committed in profiles/traffic.json
+# HBM traffic: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs over `python3 bench.py
+# --pmc-probe` (the hot kernels one by one) and `--pmc-probe-step` (whole steps), each
+# calibrated by a plain copy-like kernel of known size in the same process; the
+# figures are committed under profiles/ (step_traffic.json is the bench line's traffic)
 # ------------------------------------------------------------------------------------
 PROBE_COPY_BYTES = 256 << 20
 
