@@ -179,17 +179,26 @@ def verify_breakdown(dec, iters=20):
     st = {}
     st["draft_chain_us"] = time_fn(dec._draft_chain, iters)
 
+    lm = model.lm_head
+
     def verify():
         # the verify pass over 1 + k positions (KV rows / GDN snapshots are written but
-        # not committed, so repeating it is idempotent)
+        # not committed, so repeating it is idempotent), ending in the step's lm_head:
+        # logits with the penalty and row maxima fused when the step samples
         hidden, normed = model.hidden_states(ids, dec.cache)
-        return model.lm_head(normed)
+        if dec.fused_logits:
+            lg, rm = ops.gemm_logits(normed.reshape(-1, lm.K), lm.tiled, lm.N, lm.K,
+                                     out=dec.verify_logits.view(-1, lm.N), rowmax=dec.verify_rmax,
+                                     seen=dec.seen, penalty=dec.penalty, extra=dec.drafts,
+                                     T=k + 1, grid=lm.grid())
+            return lg.view(B, k + 1, -1), rm
+        return model.lm_head(normed), None
     st["verify_forward_us"] = time_fn(verify, iters)
-    logits = verify()
+    logits, rmax = verify()
     st["accept_us"] = time_fn(lambda: ops.spec_accept(
         logits, None, dec.drafts, dec.temperature, 0, dec.top_p, dec.seed, 0,
         offset_dev=dec.offset, workspace=dec.spec_ws, n_accepted=dec.n_acc,
-        next_token=dec.next_tok), iters)
+        next_token=dec.next_tok, target_rowmax=rmax), iters)
     return st
 
 
@@ -732,7 +741,8 @@ def cpu_baseline(raw, cfg, keep, dec, k, temperature, top_p, seed):
 PROBE_COPY_BYTES = 256 << 20
 
 
-PROBE_ORDER = ("gdn_layer", "gemm_qkv", "gemm_gate_up", "gemm_down", "attn_step", "spec_accept_c4")
+PROBE_ORDER = ("gdn_layer", "gemm_qkv", "gemm_gate_up", "gemm_down", "attn_step", "spec_accept_c4",
+               "lm_head_logits_step", "spec_accept_rowmax_step")
 
 
 def pmc_probe(B=16, T=4, launches=20):
@@ -746,6 +756,10 @@ def pmc_probe(B=16, T=4, launches=20):
                       (the step merges it in lollm_gemm_rmsnorm's second kernel)
       attn_step       lollm_attn_verify, B=16, T=4, 32 q / 4 kv heads, contexts U[2052, 2308]
       spec_accept_c4  lollm_spec_accept, B=64, k=3, V=151936 with sampled drafts
+      lm_head_logits_step      lollm_gemm_logits, the step's verify lm_head: 64 rows x
+                      N=151936 x K=4096 with the repetition penalty and the row maxima
+      spec_accept_rowmax_step  lollm_spec_accept_rowmax on those (16, 4, 151936) logits with
+                      argmax drafts (the step's acceptance: each target row read once)
     Each GEMM rotates over enough weight copies (> 512 MB) that every launch streams its
     weights from HBM, as a step that walks every layer does."""
     import torch
@@ -801,6 +815,19 @@ def pmc_probe(B=16, T=4, launches=20):
                           for i in range(k)], 1)
     for _ in range(launches):
         ops.spec_accept(tgt, drf, drafts, 0.7, 0, 0.95, 7, 0)
+    del tgt, drf
+    Vs, Ks = 151936, 4096
+    Wl = ops.gemm_tile_weights((0.02 * torch.randn(Vs, Ks, device="cuda", generator=g)).bfloat16())
+    xl = torch.randn(M, Ks, device="cuda", generator=g).bfloat16()
+    seen = ops.new_seen(B, Vs, "cuda")
+    ops.seen_mark(seen, torch.randint(0, Vs, (B, 2048), device="cuda", generator=g).int(), Vs)
+    dr = torch.randint(0, Vs, (B, T - 1), device="cuda", generator=g).int()
+    for _ in range(launches):
+        lg, rm = ops.gemm_logits(xl, Wl, Vs, Ks, seen=seen, penalty=1.05, extra=dr, T=T,
+                                 grid=gemm_grid(Vs, cus, M))
+    for _ in range(launches):
+        ops.spec_accept(lg.view(B, T, Vs), None, dr, 0.7, 0, 0.95, 7, 0, target_rowmax=rm)
+    del Wl
     x = torch.randn(PROBE_COPY_BYTES // 4, device="cuda", generator=g)
     y = torch.empty_like(x)
     for _ in range(5):
@@ -887,6 +914,74 @@ def summarize_pmc_step(directory, out=STEP_TRAFFIC_FILE):
     print(json.dumps(t, indent=1))
 
 
+def summarize_pmc_probe(directory):
+    """The hot-kernel table of `bench.py --pmc-probe`: FETCH_SIZE / WRITE_SIZE (rocprofv3
+    --pmc, in <directory>/pmc_FETCH_SIZE and pmc_WRITE_SIZE) and durations (a
+    --kernel-trace run in <directory>/pmc_trace) per launch, medians over each item's
+    launches, counters scaled by the torch.neg calibration, against each kernel's
+    algorithmic bytes."""
+    import statistics
+    import torch
+    from lollm_amd.qwen3_5.config import Qwen3_5Config, dense_8b_config_dict
+    cfg = Qwen3_5Config.from_hf(dense_8b_config_dict())
+
+    def by_kernel(rows, key, val):
+        out = {}
+        for r in sorted(rows, key=lambda r: int(r[key])):
+            out.setdefault(r["Kernel_Name"].split("(")[0].replace("void ", ""), []).append(val(r))
+        return out
+    F = by_kernel(_csv_rows(os.path.join(directory, "pmc_FETCH_SIZE"), "counter_collection.csv"),
+                  "Dispatch_Id", lambda r: float(r["Counter_Value"]))
+    W = by_kernel(_csv_rows(os.path.join(directory, "pmc_WRITE_SIZE"), "counter_collection.csv"),
+                  "Dispatch_Id", lambda r: float(r["Counter_Value"]))
+    D = by_kernel(_csv_rows(os.path.join(directory, "pmc_trace"), "kernel_trace.csv"),
+                  "Start_Timestamp",
+                  lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    neg = next(n for n in F if "neg" in n)
+    fs = PROBE_COPY_BYTES / 1024 / statistics.median(F[neg][-5:])
+    ws = PROBE_COPY_BYTES / 1024 / statistics.median(W[neg][-5:])
+    lens = torch.randint(2052, 2309, (16,), generator=torch.Generator().manual_seed(3))
+    V, M = 151936, 64
+    gm = lambda N, K, out: N * K * 2 + M * K * 2 + M * out * 2  # noqa: E731
+    items = [  # label, kernel, which of its launches, algorithmic bytes
+        ("gdn_layer B16 T4 (4 records replayed)", "lollm::gdn_layer_verify_kernel", slice(0, 20),
+         gdn_layer_bytes(cfg, 16, 4, 64)),
+        ("gemm q|gate|k|v 64x18432x4096", "lollm::gemm_stream_kernel<6>", slice(0, 20), gm(18432, 4096, 18432)),
+        ("gemm gate|up 64x24576x4096 (SwiGLU)", "lollm::gemm_stream_kernel<6>", slice(20, 40), gm(24576, 4096, 12288)),
+        ("gemm down 64x4096x12288", "lollm::gemm_stream_kernel<4>", slice(0, 20), gm(4096, 12288, 4096)),
+        ("  its merge", "lollm::gemm_fixup_kernel", slice(0, 20), None),
+        ("attention, the step's shape", "lollm::attn_verify_kernel", slice(0, 20),
+         int(lens.sum()) * 4 * 256 * 4 + 3 * 16 * 4 * 32 * 256 * 2),
+        ("  attn_combine", "lollm::attn_combine_kernel", slice(0, 20), None),
+        ("C4 acceptance: row_stats (448 rows, max found by the kernel)", "lollm::row_stats_kernel",
+         slice(0, 20), 64 * 7 * V * 2),
+        ("  spec_partial", "lollm::spec_partial_kernel", slice(0, 20), None),
+        ("  spec_final", "lollm::spec_final_kernel", slice(0, 20), None),
+        ("step lm_head with penalty and row maxima 64x151936x4096", "lollm::gemm_stream_kernel<4>",
+         slice(20, 40), gm(V, 4096, V)),
+        ("  its merge", "lollm::gemm_fixup_kernel", slice(20, 40), None),
+        ("step acceptance: row_stats (64 rows, maxima given)", "lollm::row_stats_known_kernel",
+         slice(0, 20), 64 * V * 2),
+        ("  spec_partial", "lollm::spec_partial_kernel", slice(20, 40), None),
+        ("  spec_final", "lollm::spec_final_kernel", slice(20, 40), None),
+    ]
+    print(f"calibration: {neg[:50]}: FETCH_SIZE scale {fs:.5f}, WRITE_SIZE scale {ws:.5f}\n")
+    print("| kernel | us | HBM bytes (fetch + write) | algorithmic bytes | traffic / algorithmic | frac of 8 TB/s |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for label, k, sl, alg in items:
+        if k not in F or not F[k][sl]:
+            print(f"| {label} | (not in the runs) | | | | |")
+            continue
+        f = statistics.median(F[k][sl]) * 1024 * fs
+        w = statistics.median(W[k][sl]) * 1024 * ws
+        t = statistics.median(D[k][sl])
+        if alg:
+            print(f"| {label} | {t:.2f} | {int(f + w)} | {alg} | {(f + w) / alg:.3f} | "
+                  f"{alg / t / 1e3 / PEAK_HBM_GBS:.3f} |")
+        else:
+            print(f"| {label} | {t:.2f} | {int(f + w)} | | | |")
+
+
 def measured_step_traffic():
     try:
         with open(STEP_TRAFFIC_FILE) as f:
@@ -937,6 +1032,8 @@ def main():
                     help="only replay the step between markers and a copy calibration (for rocprofv3 --pmc)")
     ap.add_argument("--summarize-pmc-step", metavar="DIR",
                     help="write profiles/step_traffic.json from the two --pmc-probe-step counter runs")
+    ap.add_argument("--summarize-pmc", metavar="DIR",
+                    help="print the hot-kernel traffic table of the --pmc-probe counter and trace runs")
     ap.add_argument("--summarize-trace", metavar="DIR",
                     help="print the per-step kernel table of a rocprofv3 --kernel-trace of bench.py")
     ap.add_argument("--accepted-steps", type=int, default=32,
@@ -947,6 +1044,9 @@ def main():
         return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
+        return
+    if args.summarize_pmc:
+        summarize_pmc_probe(args.summarize_pmc)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the workload; --gpus {args.gpus} is not "

@@ -118,6 +118,22 @@ int lollm_spec_accept(const void* target, const void* draft, const int32_t* draf
                       int32_t* next_token, void* workspace, long long workspace_bytes,
                       void* stream);
 
+/* lollm_spec_accept with the target rows' maxima given: target_rowmax (B (k+1), rowmax_ld)
+ * u16, row r's maximum order key of the bf16 logits being the largest of its first
+ * rowmax_slots entries -- as lollm_gemm_logits writes them for the verify lm_head.  Each
+ * target row is then read once (counts straight from the stream, no maximum pass);
+ * results are bit-identical to lollm_spec_accept on the same logits.
+ *
+ * Replaces, with lollm_gemm_logits: the verify pass's logits, the repetition penalty and
+ * the maximum / softmax / sort of sample_next (src/qwen3_5/mtp.py:141-155,
+ * src/generate.py:17-37) as separate passes over the (B, 1 + k, V) logits. */
+int lollm_spec_accept_rowmax(const void* target, const uint16_t* target_rowmax,
+                             long long rowmax_ld, int rowmax_slots, const void* draft,
+                             const int32_t* drafts, int B, int k, int V, float inv_temperature,
+                             int top_k, float top_p, uint64_t seed, uint64_t offset,
+                             const uint64_t* offset_dev, int32_t* n_accepted, int32_t* next_token,
+                             void* workspace, long long workspace_bytes, void* stream);
+
 /* lollm_spec_accept with no workspace argument and no device allocation, for callers that
  * cannot allocate: code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc.  No counterpart in the reference.  The workspace is a fixed array inside the
@@ -234,6 +250,27 @@ long long lollm_gemm_argmax_workspace_bytes(int M, int N, int K, int grid);
 int lollm_gemm_argmax(const void* A, long long lda, const void* Wt, int M, int N, int K,
                       int32_t* out, long long out_stride, void* workspace, long long workspace_bytes,
                       int grid, void* stream);
+
+/* The lm_head with the repetition penalty and the sampler's row maxima fused: C (M, ldc)
+ * bf16 = A W^T (as lollm_gemm, 64-column groups), each logit of row m = (s, t) with
+ * s = m / T penalised in place when its token is in seen[s] (seen_words u32 words per
+ * row, bit tok % 32 of word tok / 32) or among extra[s * extra_stride + j] for
+ * j < n_extra0 + t (seen NULL: no penalty) -- x > 0 ? x / penalty : x * penalty in fp32
+ * on the bf16 logit, rounded once, the bits of lollm_repetition_penalty -- and rowmax
+ * (M, rowmax_ld) u16 with, per row, lollm_gemm_rowmax_slots(grid) slots whose largest
+ * entry is the maximum order key of the stored row (order key of bf16 bits b:
+ * b & 0x8000 ? ~b & 0xFFFF : b | 0x8000).  Every slot is written by every call.
+ *
+ * Replaces: lm_head (src/qwen3_5/modeling_qwen3_5.py:99) on the verify rows, the
+ * repetition penalty of sample_next (src/generate.py:18-22), and the maximum pass of its
+ * softmax (generate.py:26-31), which lollm_spec_accept_rowmax then skips.
+ * Workspace and supported shapes as lollm_gemm; with extra, n_extra0 + T - 1 <= 8. */
+int lollm_gemm_rowmax_slots(int grid);
+int lollm_gemm_logits(const void* A, long long lda, const void* Wt, int M, int N, int K, void* C,
+                      long long ldc, uint16_t* rowmax, long long rowmax_ld, const uint32_t* seen,
+                      int seen_words, const int32_t* extra, int extra_stride, int n_extra0, int T,
+                      float penalty, void* workspace, long long workspace_bytes, int grid,
+                      void* stream);
 
 /* A projection that feeds the residual stream, with the residual add and the next
  * RMSNorm fused into the GEMM's second kernel: C = A W^T (as lollm_gemm, epilogue 0),

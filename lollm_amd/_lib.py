@@ -35,6 +35,8 @@ SIGNATURES = {
     "lollm_spec_workspace_bytes": ([_I, _I, _I], ctypes.c_longlong),
     "lollm_spec_accept": ([_P, _P, _P, _I, _I, _I, _F, _I, _F, _U64, _U64, _P, _P, _P, _P,
                            ctypes.c_longlong, _P], _I),
+    "lollm_spec_accept_rowmax": ([_P, _P, ctypes.c_longlong, _I, _P, _P, _I, _I, _I, _F, _I, _F,
+                                  _U64, _U64, _P, _P, _P, _P, ctypes.c_longlong, _P], _I),
     "lollm_spec_accept_noalloc": ([_P, _P, _P, _I, _I, _I, _F, _I, _F, _U64, _U64, _P, _P, _P,
                                    _P], _I),
     "lollm_sample_workspace_bytes": ([_I], ctypes.c_longlong),
@@ -61,6 +63,10 @@ SIGNATURES = {
     "lollm_gemm_workspace_bytes": ([_I, _I, _I, _I], ctypes.c_longlong),
     "lollm_gemm": ([_P, ctypes.c_longlong, _P, _P, ctypes.c_longlong, _I, _I, _I, _I, _P,
                     ctypes.c_longlong, _I, _P], _I),
+    "lollm_gemm_rowmax_slots": ([_I], _I),
+    "lollm_gemm_logits": ([_P, ctypes.c_longlong, _P, _I, _I, _I, _P, ctypes.c_longlong, _P,
+                           ctypes.c_longlong, _P, _I, _P, _I, _I, _I, _F, _P, ctypes.c_longlong,
+                           _I, _P], _I),
     "lollm_gemm_rmsnorm": ([_P, ctypes.c_longlong, _P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _P,
                             ctypes.c_longlong, _I, _P], _I),
     "lollm_greedy_accept": ([_P, _P, _I, _I, _P, _P, _P], _I),

@@ -43,7 +43,7 @@ constexpr int GM_P = 4;                     // weight units in flight per wave
 constexpr int GM_MAXW = 1024;               // grid limit (piece table)
 constexpr int GM_PB = 8;                    // piece loads a merge issues together
 
-enum { GM_EPI_NONE = 0, GM_EPI_SWIGLU = 1, GM_EPI_ARGMAX = 2 };
+enum { GM_EPI_NONE = 0, GM_EPI_SWIGLU = 1, GM_EPI_ARGMAX = 2, GM_EPI_LOGITS = 3 };
 
 // Row argmax without the logits (lollm_gemm_argmax): each (row, 16-column n-tile) keeps
 // the packed maximum ((order key of the bf16 value) << 32 | ~column), so the highest
@@ -68,7 +68,90 @@ struct GemmArgs {
   int M, N, K, G, SK, nw, epi, U;
   int rowmajor;          // piece layout: 0 = accumulator order (float4 (i, wave, lane)), 1 = row major
   uint64_t* am;          // GM_EPI_ARGMAX: (M, N / 16) packed row maxima per n-tile
+  // GM_EPI_LOGITS: the bf16 logits with the repetition penalty applied in place, and per
+  // row the maximum order key of the stored values in 2 nw slots (row stride rmax_ld):
+  // slot w = the groups workgroup w finished whole, slot nw + w = the cut group whose
+  // last unit workgroup w holds (merged by the fixup kernel; 0 where there is none)
+  uint16_t* rmax;
+  long long rmax_ld;
+  const uint32_t* seen;  // (M / T, seen_words) bitmaps of the penalised tokens, or null
+  int seen_words;
+  const int32_t* extra;  // extra penalised tokens: row m = (s, t) also counts
+  int extra_stride;      //   extra[s * extra_stride + j] for j < n_extra0 + t
+  int n_extra0, T;
+  float pen;
 };
+
+// The penalty context of one row for GM_EPI_LOGITS: its extra penalised tokens (at most
+// GM_MAXEX, checked on the host); the seen-bitmap word of a column goes with it.
+constexpr int GM_MAXEX = 8;
+struct GmRowEx {
+  int n;
+  int32_t ex[GM_MAXEX];
+};
+
+__device__ __forceinline__ void gm_row_ex(const GemmArgs& a, int m, GmRowEx& r) {
+  r.n = 0;
+  if (!a.seen || !a.extra) return;
+  const int mm = m < a.M ? m : a.M - 1;
+  const int sq = mm / a.T, t = mm - sq * a.T;
+  r.n = a.n_extra0 + t;
+  const int32_t* ex = a.extra + (size_t)sq * a.extra_stride;
+#pragma unroll
+  for (int j = 0; j < GM_MAXEX; ++j) r.ex[j] = j < r.n ? ex[j] : -1;
+}
+
+// bits col .. col + 3 (col % 4 == 0) of row m's seen bitmap, in bits 0..3
+__device__ __forceinline__ uint32_t gm_seen4(const GemmArgs& a, int m, int col) {
+  if (!a.seen) return 0u;
+  const int mm = m < a.M ? m : a.M - 1;
+  const int sq = mm / a.T;
+  return a.seen[(size_t)sq * a.seen_words + (col >> 5)] >> (col & 31);
+}
+
+// The bf16 logits of columns col .. col + 3 of a row (output tile values v) with the
+// repetition penalty of src/generate.py:18-22 applied where the token is in the row's
+// context (seen bits w, extra tokens r): bf16(v), then for a penalised token
+// y = x > 0 ? x / pen : x * pen in fp32 rounded once to bf16 -- the bits
+// lollm_repetition_penalty gives on the stored logits.
+__device__ __forceinline__ void gm_logits4(const GemmArgs& a, const float* v, int col, uint32_t w,
+                                           const GmRowEx& r, uint32_t* bits) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) bits[e] = f32_to_bf16(v[e]);
+  if (!a.seen) return;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    bool p = (w >> e) & 1u;
+#pragma unroll
+    for (int j = 0; j < GM_MAXEX; ++j) p |= j < r.n && r.ex[j] == col + e;
+    if (p) {
+      const float x = __uint_as_float(bits[e] << 16);
+      bits[e] = f32_to_bf16(x > 0.f ? x / a.pen : x * a.pen);
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t gm_ord16(uint32_t b) {
+  return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+}
+
+// Row-maximum slots of a GM_EPI_LOGITS call, GM_RM_SLOTS per workgroup and row: in the
+// main kernels slot GM_RM_SLOTS w + v holds the maximum order key over the whole groups
+// wave v of workgroup w stored (the k-split kernel's 4 waves, the stream kernel's 2 column
+// halves, the rest 0); slot GM_RM_SLOTS nw + w that of the cut group whose last unit
+// workgroup w holds (written by the fixup kernel; 0 where there is none).  Every slot
+// of rows < M is written by every call, so nothing needs clearing.
+constexpr int GM_RM_SLOTS = 4;
+
+__device__ __forceinline__ void gm_rowmax_put(const GemmArgs& a, int m, int slot, uint32_t x) {
+  if (m < a.M) a.rmax[(size_t)m * a.rmax_ld + slot] = (uint16_t)x;
+}
+
+// lanes l and l ^ 16, l ^ 32, l ^ 48 hold the same row: their maximum
+__device__ __forceinline__ uint32_t gm_rowmax_lanes(uint32_t x) {
+  x = max(x, (uint32_t)__shfl_xor((int)x, 16, 64));
+  return max(x, (uint32_t)__shfl_xor((int)x, 32, 64));
+}
 
 __device__ __forceinline__ void gm_lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -134,14 +217,29 @@ constexpr int GS_SLOT = 16384;
 constexpr int GS_THREADS = 448;
 constexpr int GS_NT = 2;                    // cache policy of the weight DMA: non-temporal
 
+// GM_EPI_LOGITS: sw = gm_seen4 of the lane's columns (0 when the caller has no penalty
+// context ready: it is then loaded here), rx = the row's extra tokens, rm = the lane's
+// row maximum so far.
 template <int NT>
 __device__ __forceinline__ void gs_emit_tile(const GemmArgs& a, const gm_f32x4& v, int i, int j,
-                                             int g, bool whole, int w, int lane) {
+                                             int g, bool whole, int w, int lane, uint32_t& rm,
+                                             uint32_t sw, const GmRowEx& rx) {
   const int l16 = lane & 15, g4 = lane >> 4;
   const int m = 16 * i + l16;
   const int t = NT * g + j;                  // n-tile of the tiled weight
   if (whole) {
-    if (a.epi == GM_EPI_ARGMAX) {
+    if (a.epi == GM_EPI_LOGITS) {
+      if (m < a.M) {
+        const int col = 16 * t + 4 * g4;
+        const float vv[4] = {v[0], v[1], v[2], v[3]};
+        uint32_t b[4];
+        gm_logits4(a, vv, col, sw, rx, b);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rm = max(rm, gm_ord16(b[e]));
+        *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+            make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+      }
+    } else if (a.epi == GM_EPI_ARGMAX) {
       const int col = 16 * t + 4 * g4;
       uint64_t best = gm_key(v[0], col);
 #pragma unroll
@@ -203,7 +301,14 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int w = blockIdx.x;
   const int u0 = gm_begin(a.U, w, a.nw), u1 = gm_begin(a.U, w + 1, a.nw);
-  if (u0 >= u1) return;                      // the whole workgroup: no barrier is left waiting
+  if (u0 >= u1) {                            // the whole workgroup: no barrier is left waiting
+    if (a.epi == GM_EPI_LOGITS && threadIdx.x < 64) {
+#pragma unroll
+      for (int v = 0; v < GM_RM_SLOTS; ++v) gm_rowmax_put(a, threadIdx.x, GM_RM_SLOTS * w + v, 0);
+      gm_rowmax_put(a, threadIdx.x, GM_RM_SLOTS * a.nw + w, 0);
+    }
+    return;
+  }
   const int kt = a.K / 32;
   if (wave == 4 || wave == 5) {
     const int lw = wave - 4;
@@ -262,7 +367,26 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
 #pragma unroll
       for (int jj = 0; jj < HALF; ++jj) acc[q][ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
   bool whole_from_start = (u0 % a.SK) == 0;
+  uint32_t rm[2] = {0u, 0u};                 // GM_EPI_LOGITS: row maxima (order keys)
+  // GM_EPI_LOGITS with a penalty: each row's extra tokens, and the seen words of the
+  // group's columns loaded at the group's first unit, long before its epilogue needs them
+  GmRowEx rx[2];
+  uint32_t sw[2][HALF];
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii) {
+    gm_row_ex(a, 16 * (2 * wm + ii) + l16, rx[ii]);
+#pragma unroll
+    for (int jj = 0; jj < HALF; ++jj) sw[ii][jj] = 0u;
+  }
   for (int u = u0; u < u1; ++u) {
+    if (a.epi == GM_EPI_LOGITS && a.seen && (u == u0 || u % a.SK == 0)) {
+      const int g = u / a.SK;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int jj = 0; jj < HALF; ++jj)
+          sw[ii][jj] = gm_seen4(a, 16 * (2 * wm + ii) + l16, 16 * (NT * g + HALF * wn + jj) + 4 * g4);
+    }
     // this wave's reads of the previous unit are complete before the loaders may refill it
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     const unsigned char* wb = wring + ((u - u0) % WSLOTS) * WSLOT;
@@ -295,12 +419,26 @@ __global__ __launch_bounds__(GS_THREADS) void gemm_stream_kernel(GemmArgs a) {
           gm_f32x4 fin = acc[0][ii][jj];
 #pragma unroll
           for (int q = 1; q < GM_KS; ++q) fin += acc[q][ii][jj];
-          gs_emit_tile<NT>(a, fin, 2 * wm + ii, HALF * wn + jj, g, whole, w, lane);
+          gs_emit_tile<NT>(a, fin, 2 * wm + ii, HALF * wn + jj, g, whole, w, lane, rm[ii],
+                           sw[ii][jj], rx[ii]);
 #pragma unroll
           for (int q = 0; q < GM_KS; ++q) acc[q][ii][jj] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
         }
       whole_from_start = true;
     }
+  }
+  if (a.epi == GM_EPI_LOGITS) {
+    // wave (wn, wm): slot wn of its 32 rows' column half, slot 2 + wn cleared
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const uint32_t x = gm_rowmax_lanes(rm[ii]);
+      if (g4 == 0) {
+        const int m = 16 * (2 * wm + ii) + l16;
+        gm_rowmax_put(a, m, GM_RM_SLOTS * w + wn, x);
+        gm_rowmax_put(a, m, GM_RM_SLOTS * w + 2 + wn, 0);
+      }
+    }
+    if (wave == 0) gm_rowmax_put(a, lane, GM_RM_SLOTS * a.nw + w, 0);
   }
 }
 
@@ -322,7 +460,14 @@ __global__ __launch_bounds__(256, 2) void gemm_ksplit_kernel(GemmArgs a) {
   const int l16 = lane & 15, g4 = lane >> 4;
   const int w = blockIdx.x;
   const int u0 = gm_begin(a.U, w, a.nw), u1 = gm_begin(a.U, w + 1, a.nw);
-  if (u0 >= u1) return;
+  if (u0 >= u1) {
+    if (a.epi == GM_EPI_LOGITS && tid < 64) {
+#pragma unroll
+      for (int v = 0; v < GM_RM_SLOTS; ++v) gm_rowmax_put(a, tid, GM_RM_SLOTS * w + v, 0);
+      gm_rowmax_put(a, tid, GM_RM_SLOTS * a.nw + w, 0);
+    }
+    return;
+  }
   const int kt = a.K / 32;
   const uint16_t* wlane = a.Wt + (size_t)wave * 512 + lane * 8;
   const uint16_t* alane[MT];
@@ -356,6 +501,9 @@ __global__ __launch_bounds__(256, 2) void gemm_ksplit_kernel(GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   }
   bool whole_from_start = (u0 % a.SK) == 0;
+  uint32_t rm[MT];                            // GM_EPI_LOGITS: row maxima (order keys)
+#pragma unroll
+  for (int i = 0; i < MT; ++i) rm[i] = 0u;
 
   auto finish = [&](int g, bool whole) {
     gm_lds_barrier();   // the previous group's reads of red are done
@@ -371,7 +519,14 @@ __global__ __launch_bounds__(256, 2) void gemm_ksplit_kernel(GemmArgs a) {
         gm_f32x4 fin = red[((j * 4) * MT + i) * 64 + lane];
 #pragma unroll
         for (int v = 1; v < 4; ++v) fin += red[((j * 4 + v) * MT + i) * 64 + lane];
-        gs_emit_tile<NT>(a, fin, i, j, g, whole, w, lane);
+        uint32_t swk = 0u;
+        GmRowEx rxk;
+        rxk.n = 0;
+        if (a.epi == GM_EPI_LOGITS && whole) {
+          swk = gm_seen4(a, 16 * i + l16, 16 * (NT * g + j) + 4 * g4);
+          gm_row_ex(a, 16 * i + l16, rxk);
+        }
+        gs_emit_tile<NT>(a, fin, i, j, g, whole, w, lane, rm[i], swk, rxk);
       }
     }
 #pragma unroll
@@ -408,6 +563,15 @@ __global__ __launch_bounds__(256, 2) void gemm_ksplit_kernel(GemmArgs a) {
     GM_KUNIT(0) GM_KUNIT(1) GM_KUNIT(2) GM_KUNIT(3)
   }
 #undef GM_KUNIT
+  if (a.epi == GM_EPI_LOGITS) {
+    // wave v emitted n-tiles v, v + 4, ... of every row: slot v
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const uint32_t x = gm_rowmax_lanes(rm[i]);
+      if (g4 == 0) gm_rowmax_put(a, 16 * i + l16, GM_RM_SLOTS * w + wave, x);
+    }
+    if (wave == 0) gm_rowmax_put(a, lane, GM_RM_SLOTS * a.nw + w, 0);
+  }
 }
 
 // Merge the pieces of m-tile blockIdx.y of group blockIdx.x: the live piece slots are
@@ -422,6 +586,15 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
   const int wf = gm_owner(a.U, g * a.SK, a.nw), wl = gm_owner(a.U, g * a.SK + a.SK - 1, a.nw);
   if (wf == wl) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // GM_EPI_LOGITS: the penalty context of the lane's row and columns, loaded first
+  uint32_t fx_sw = 0u;
+  GmRowEx fx_rx;
+  fx_rx.n = 0;
+  if (a.epi == GM_EPI_LOGITS && a.seen) {
+    const int mr = 16 * i + (lane & 15);
+    fx_sw = gm_seen4(a, mr, GM_COLS * g + 16 * wave + 4 * (lane >> 4));
+    gm_row_ex(a, mr, fx_rx);
+  }
   if (wave == 0) {
     int cnt = 0;
     for (int base = wf; base <= wl; base += 64) {
@@ -451,7 +624,27 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs a) {
       if (k0 + j < np) { s.x += p[j].x; s.y += p[j].y; s.z += p[j].z; s.w += p[j].w; }
   }
   // lane holds row m, tiled columns 4 g4 .. + 3 of n-tile 4 g + wave
-  if (a.epi == GM_EPI_ARGMAX) {
+  if (a.epi == GM_EPI_LOGITS) {
+    __shared__ uint32_t rmx[4][16];
+    uint32_t x = 0;
+    if (m < a.M) {
+      const int col = GM_COLS * g + 16 * wave + 4 * g4;
+      const float sv[4] = {s.x, s.y, s.z, s.w};
+      uint32_t b[4];
+      gm_logits4(a, sv, col, fx_sw, fx_rx, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x = max(x, gm_ord16(b[e]));
+      *reinterpret_cast<uint2*>(a.C + (size_t)m * a.ldc + col) =
+          make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+    }
+    x = gm_rowmax_lanes(x);
+    if (g4 == 0) rmx[wave][lane & 15] = x;
+    __syncthreads();
+    if (tid < 16) {
+      const uint32_t r = max(max(rmx[0][tid], rmx[1][tid]), max(rmx[2][tid], rmx[3][tid]));
+      gm_rowmax_put(a, 16 * i + tid, GM_RM_SLOTS * a.nw + wl, r);
+    }
+  } else if (a.epi == GM_EPI_ARGMAX) {
     const int col = GM_COLS * g + 16 * wave + 4 * g4;
     const float sv[4] = {s.x, s.y, s.z, s.w};
     uint64_t best = gm_key(sv[0], col);
@@ -644,7 +837,8 @@ static int gemm_grid(int grid) {
 static bool gemm_shape_ok(int M, int N, int K, int epi) {
   if (M <= 0 || M > 64 || N <= 0 || K <= 0) return false;
   if (N % GM_COLS || K % GM_KC) return false;
-  if (epi != GM_EPI_NONE && epi != GM_EPI_SWIGLU && epi != GM_EPI_ARGMAX) return false;
+  if (epi != GM_EPI_NONE && epi != GM_EPI_SWIGLU && epi != GM_EPI_ARGMAX && epi != GM_EPI_LOGITS)
+    return false;
   return true;
 }
 
@@ -678,10 +872,15 @@ static int gemm_group_tiles(int N, int nw) {
   return 4;
 }
 
+struct GemmLogitsArgs {   // the GM_EPI_LOGITS fields of GemmArgs
+  uint16_t* rmax; long long rmax_ld; const uint32_t* seen; int seen_words; const int32_t* extra;
+  int extra_stride, n_extra0, T; float pen;
+};
+
 static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, void* C,
                      long long ldc, int M, int N, int K, int epilogue, void* workspace,
                      long long workspace_bytes, int grid, int rowmajor, hipStream_t st,
-                     bool allow_wide = false) {
+                     bool allow_wide = false, const GemmLogitsArgs* lg = nullptr) {
   if (!A || !Wt || !C || !workspace) return LOLLM_EINVAL;
   if (!gemm_shape_ok(M, N, K, epilogue)) return LOLLM_EUNSUPPORTED;
   const long long outc = epilogue == GM_EPI_SWIGLU ? N / 2 : N;
@@ -699,8 +898,16 @@ static int gemm_main(GemmArgs& a, const void* A, long long lda, const void* Wt, 
   a.U = a.G * a.SK;
   a.rowmajor = rowmajor;
   a.am = nullptr;
+  a.rmax = nullptr; a.rmax_ld = 0; a.seen = nullptr; a.seen_words = 0; a.extra = nullptr;
+  a.extra_stride = 0; a.n_extra0 = 0; a.T = 1; a.pen = 1.f;
   if (epilogue == GM_EPI_ARGMAX)
     a.am = (uint64_t*)((char*)workspace + ((gemm_ws_bytes(M, N, nw) + 255) / 256) * 256);
+  if (epilogue == GM_EPI_LOGITS) {
+    if (!lg) return LOLLM_EINVAL;
+    a.rmax = lg->rmax; a.rmax_ld = lg->rmax_ld; a.seen = lg->seen; a.seen_words = lg->seen_words;
+    a.extra = lg->extra; a.extra_stride = lg->extra_stride; a.n_extra0 = lg->n_extra0;
+    a.T = lg->T; a.pen = lg->pen;
+  }
   switch ((M + 15) / 16) {
     case 1:
       if (nt == 6) hipLaunchKernelGGL((gemm_ksplit_kernel<1, 6>), dim3(nw), dim3(256), 0, st, a);
@@ -770,6 +977,40 @@ LOLLM_API int lollm_gemm_argmax(const void* A, long long lda, const void* Wt, in
   }
   hipLaunchKernelGGL(gemm_argmax_final_kernel, dim3(M), dim3(GM_AF_THREADS), 0, st,
                      (const uint64_t*)a.am, N / 16, out, out_stride);
+  return launch_status();
+}
+
+LOLLM_API int lollm_gemm_rowmax_slots(int grid) {
+  const int nw = gemm_grid(grid);
+  if (nw <= 0 || nw > GM_MAXW) return -1;
+  return (GM_RM_SLOTS + 1) * nw;
+}
+
+LOLLM_API int lollm_gemm_logits(const void* A, long long lda, const void* Wt, int M, int N, int K,
+                                void* C, long long ldc, uint16_t* rowmax, long long rowmax_ld,
+                                const uint32_t* seen, int seen_words, const int32_t* extra,
+                                int extra_stride, int n_extra0, int T, float penalty,
+                                void* workspace, long long workspace_bytes, int grid,
+                                void* stream) {
+  if (!rowmax) return LOLLM_EINVAL;
+  const int slots = lollm_gemm_rowmax_slots(grid);
+  if (slots < 0) return LOLLM_EUNSUPPORTED;
+  if (rowmax_ld < slots) return LOLLM_EINVAL;
+  if (seen) {
+    if (T <= 0 || M % T || seen_words < (N + 31) / 32 || n_extra0 < 0) return LOLLM_EINVAL;
+    if (extra && extra_stride < n_extra0 + T - 1) return LOLLM_EINVAL;
+    if (extra && n_extra0 + T - 1 > GM_MAXEX) return LOLLM_EUNSUPPORTED;
+    if (!(penalty > 0.f) || !(penalty < 3.0e38f)) return LOLLM_EINVAL;
+  }
+  GemmLogitsArgs lg{rowmax, rowmax_ld, seen, seen_words, seen ? extra : nullptr, extra_stride,
+                    n_extra0, T > 0 ? T : 1, penalty};
+  hipStream_t st = (hipStream_t)stream;
+  GemmArgs a;
+  int rc = gemm_main(a, A, lda, Wt, C, ldc, M, N, K, GM_EPI_LOGITS, workspace, workspace_bytes,
+                     grid, 0, st, false, &lg);
+  if (rc) return rc;
+  if (a.G % a.nw == 0) return LOLLM_OK;
+  hipLaunchKernelGGL(gemm_fixup_kernel, dim3(a.G, (M + 15) / 16), dim3(256), 0, st, a);
   return launch_status();
 }
 

@@ -330,6 +330,106 @@ __device__ __forceinline__ void hist_chunk(uint4 u, uint32_t km2, int32_t dlim, 
   }
 }
 
+// The rest of a sampled row's statistics once its maximum is known (top_bits: the bf16
+// bits of the largest logit): the distances that need counting, the per-key counts
+// (count(km2, dlim) fills hist; km2 = the maximum key mod 2^16 in both halves), then
+// block scans for the top-k / top-p cut points and the kept mass Z.  hist must be zero
+// and visible to every thread before the call.
+template <typename Count>
+__device__ __forceinline__ void row_stats_counts(uint32_t top_bits, float inv_temp, int top_k,
+                                                 float top_p, RowStat* out, uint32_t* hist,
+                                                 uint64_t* s64, int32_t* shared_cut_p,
+                                                 uint64_t* z_sh_p, Count count) {
+  const int tid = threadIdx.x;
+  int32_t& shared_cut = *shared_cut_p;
+  uint64_t& z_sh = *z_sh_p;
+  RowStat st;
+  st.greedy = 0;
+  st.argmax = -1;   // only greedy rows use it
+  const int32_t km = skey(top_bits);
+  st.kmax = km;
+  const float xmax = key_value(km);
+  const float c = inv_temp * 1.44269504088896341f;
+  // ---- which distances need counting: all below SP_NBINS when top-k reads the counts;
+  //      without top-k only the mass (count x weight) is read, so distances whose weight
+  //      test t = (x - xmax) c >= -40 fails (weight 0) are skipped.  t does not increase
+  //      with the distance, so those distances are a suffix: bisect for its start over
+  //      the distances of real keys (skey >= -(0x7FFF - SP_MAG0)). ----
+  int32_t dlim = SP_NBINS - 1;
+  if (top_k <= 0) {
+    if (!((xmax - xmax) * c >= -40.0f)) {
+      dlim = -1;   // the maximum is inf or NaN: every weight is zero
+    } else {
+      int lo = 0, hi = min(SP_NBINS - 1, km + (0x7FFF - SP_MAG0)) + 1;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if ((key_value(km - mid) - xmax) * c >= -40.0f) lo = mid; else hi = mid;
+      }
+      dlim = lo;
+    }
+  }
+  // ---- per-key counts below the max ----
+  const uint32_t km2 = ((uint32_t)km & 0xFFFFu) * 0x10001u;
+  count(km2, dlim);
+  __syncthreads();
+  // ---- cut points and kept mass: thread t owns bins [8t, 8t + 8) ----
+  constexpr int PER = SP_NBINS / SP_THREADS;
+  uint32_t cnt[PER];
+  uint64_t mass[PER];
+  uint32_t csum = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int d = tid * PER + j;
+    cnt[j] = hist[d];
+    mass[j] = cnt[j] ? (uint64_t)cnt[j] * weight_of(key_value(km - d), xmax, c) : 0;
+    csum += cnt[j];
+  }
+  if (tid == 0) shared_cut = SP_NBINS - 1;
+  __syncthreads();
+  if (top_k > 0) {
+    uint64_t ctot;
+    const uint64_t cinc = block_inclusive_scan<uint64_t>((uint64_t)csum, s64, &ctot);
+    const uint64_t c0 = cinc - csum;
+    if (c0 < (uint64_t)top_k && cinc >= (uint64_t)top_k) {
+      uint64_t run = c0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        run += cnt[j];
+        if (run >= (uint64_t)top_k) { shared_cut = tid * PER + j; break; }
+      }
+    }
+    __syncthreads();
+  }
+  const int32_t cut_k = shared_cut;
+  uint64_t msum = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (tid * PER + j <= cut_k) msum += mass[j];
+  uint64_t W;
+  const uint64_t minc = block_inclusive_scan<uint64_t>(msum, s64, &W);
+  st.cut = cut_k;
+  st.Z = W;
+  if (top_p > 0.0f && top_p < 1.0f) {
+    const uint32_t p24 = (uint32_t)(top_p * 16777216.0f);
+    const uint64_t tm = (uint64_t)(((u128)W * p24) >> 24);
+    const uint64_t m0 = minc - msum;
+    if (m0 <= tm && minc > tm) {
+      uint64_t run = m0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        if (tid * PER + j > cut_k) break;
+        run += mass[j];
+        if (run > tm) { shared_cut = tid * PER + j; z_sh = run; break; }
+      }
+    }
+    __syncthreads();
+    st.cut = shared_cut;
+    st.Z = z_sh;
+  }
+  if (tid == 0) *out = st;
+}
+
+
 // Sampled rows only (inv_temp > 0); greedy rows take the split argmax below.  Rows
 // [0, rows0) are read from x0, the rest from x1 (target and draft rows in one launch).
 __global__ __launch_bounds__(SP_THREADS, 8) void row_stats_kernel(const uint16_t* __restrict__ x0,
@@ -398,102 +498,64 @@ __global__ __launch_bounds__(SP_THREADS, 8) void row_stats_kernel(const uint16_t
     }
     top_bits = ord_bits((uint32_t)block_max<uint64_t>((uint64_t)max((m2 & 0xFFFFu), (m2 >> 16)), s64));
   }
-  RowStat st;
-  st.greedy = 0;
-  st.argmax = -1;   // only greedy rows use it
-  const int32_t km = skey(top_bits);
-  st.kmax = km;
-  const float xmax = key_value(km);
-  const float c = inv_temp * 1.44269504088896341f;
-  // ---- which distances need counting: all below SP_NBINS when top-k reads the counts;
-  //      without top-k only the mass (count x weight) is read, so distances whose weight
-  //      test t = (x - xmax) c >= -40 fails (weight 0) are skipped.  t does not increase
-  //      with the distance, so those distances are a suffix: bisect for its start over
-  //      the distances of real keys (skey >= -(0x7FFF - SP_MAG0)). ----
-  int32_t dlim = SP_NBINS - 1;
-  if (top_k <= 0) {
-    if (!((xmax - xmax) * c >= -40.0f)) {
-      dlim = -1;   // the maximum is inf or NaN: every weight is zero
-    } else {
-      int lo = 0, hi = min(SP_NBINS - 1, km + (0x7FFF - SP_MAG0)) + 1;
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if ((key_value(km - mid) - xmax) * c >= -40.0f) lo = mid; else hi = mid;
-      }
-      dlim = lo;
+  row_stats_counts(top_bits, inv_temp, top_k, top_p, stats + row, hist, s64,
+                   &shared_cut, &z_sh, [&](uint32_t km2, int32_t dlim) {
+#pragma unroll
+    for (int i = 0; i < SP_REG; ++i) {
+      const int ch = i * SP_THREADS + tid;
+      if (ch < nch) hist_chunk(reg[i], km2, dlim, hist);
     }
-  }
-  // ---- per-key counts below the max (from registers) ----
-  const uint32_t km2 = ((uint32_t)km & 0xFFFFu) * 0x10001u;
+    for (int c0 = SP_REG * SP_THREADS + tid; c0 < nch; c0 += SP_TAIL * SP_THREADS) {
+      uint4 tl[SP_TAIL];
 #pragma unroll
-  for (int i = 0; i < SP_REG; ++i) {
-    const int ch = i * SP_THREADS + tid;
-    if (ch < nch) hist_chunk(reg[i], km2, dlim, hist);
-  }
-  for (int c0 = SP_REG * SP_THREADS + tid; c0 < nch; c0 += SP_TAIL * SP_THREADS) {
-    uint4 tl[SP_TAIL];
+      for (int u = 0; u < SP_TAIL; ++u) tl[u] = x4[min(c0 + u * SP_THREADS, nch - 1)];
 #pragma unroll
-    for (int u = 0; u < SP_TAIL; ++u) tl[u] = x4[min(c0 + u * SP_THREADS, nch - 1)];
-#pragma unroll
-    for (int u = 0; u < SP_TAIL; ++u)
-      if (c0 + u * SP_THREADS < nch) hist_chunk(tl[u], km2, dlim, hist);
-  }
-  __syncthreads();
-  // ---- cut points and kept mass: thread t owns bins [8t, 8t + 8) ----
-  constexpr int PER = SP_NBINS / SP_THREADS;
-  uint32_t cnt[PER];
-  uint64_t mass[PER];
-  uint32_t csum = 0;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int d = tid * PER + j;
-    cnt[j] = hist[d];
-    mass[j] = cnt[j] ? (uint64_t)cnt[j] * weight_of(key_value(km - d), xmax, c) : 0;
-    csum += cnt[j];
-  }
-  if (tid == 0) shared_cut = SP_NBINS - 1;
-  __syncthreads();
-  if (top_k > 0) {
-    uint64_t ctot;
-    const uint64_t cinc = block_inclusive_scan<uint64_t>((uint64_t)csum, s64, &ctot);
-    const uint64_t c0 = cinc - csum;
-    if (c0 < (uint64_t)top_k && cinc >= (uint64_t)top_k) {
-      uint64_t run = c0;
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        run += cnt[j];
-        if (run >= (uint64_t)top_k) { shared_cut = tid * PER + j; break; }
-      }
+      for (int u = 0; u < SP_TAIL; ++u)
+        if (c0 + u * SP_THREADS < nch) hist_chunk(tl[u], km2, dlim, hist);
     }
-    __syncthreads();
-  }
-  const int32_t cut_k = shared_cut;
-  uint64_t msum = 0;
+  });
+}
+
+// Sampled rows whose maxima are given: row r's maximum order key is the largest of
+// rmax[r * rmax_ld + 0 .. rmax_slots) (the row-maximum slots of lollm_gemm_logits), so
+// the row is read once, straight into the counts: no maximum pass and no second read of
+// the row.  One workgroup per CU (128 registers per thread): the first SP_KREG 16-byte
+// chunks per thread -- the whole row at V <= 163840 -- are requested together, so a row
+// costs one memory round trip; any rest follows in batches.
+constexpr int SP_KREG = 20;
+
+__global__ __launch_bounds__(SP_THREADS, 4) void row_stats_known_kernel(
+    const uint16_t* __restrict__ x, int V, float inv_temp, int top_k, float top_p,
+    RowStat* stats, const uint16_t* __restrict__ rmax, long long rmax_ld, int rmax_slots) {
+  __shared__ uint32_t hist[SP_NBINS];
+  __shared__ uint64_t s64[16];
+  __shared__ int32_t shared_cut;
+  __shared__ uint64_t z_sh;
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  const int nch = V >> 3;
+  const uint4* x4 = reinterpret_cast<const uint4*>(x + (size_t)row * V);
+  uint4 reg[SP_KREG];
 #pragma unroll
-  for (int j = 0; j < PER; ++j)
-    if (tid * PER + j <= cut_k) msum += mass[j];
-  uint64_t W;
-  const uint64_t minc = block_inclusive_scan<uint64_t>(msum, s64, &W);
-  st.cut = cut_k;
-  st.Z = W;
-  if (top_p > 0.0f && top_p < 1.0f) {
-    const uint32_t p24 = (uint32_t)(top_p * 16777216.0f);
-    const uint64_t tm = (uint64_t)(((u128)W * p24) >> 24);
-    const uint64_t m0 = minc - msum;
-    if (m0 <= tm && minc > tm) {
-      uint64_t run = m0;
+  for (int i = 0; i < SP_KREG; ++i) reg[i] = x4[min(i * SP_THREADS + tid, nch - 1)];
+  uint32_t mo = 0;
+  for (int i = tid; i < rmax_slots; i += SP_THREADS) mo = max(mo, (uint32_t)rmax[(size_t)row * rmax_ld + i]);
+  for (int i = tid; i < SP_NBINS; i += SP_THREADS) hist[i] = 0;
+  const uint32_t top_bits = ord_bits((uint32_t)block_max<uint64_t>((uint64_t)mo, s64));
+  row_stats_counts(top_bits, inv_temp, top_k, top_p, stats + row, hist, s64, &shared_cut, &z_sh,
+                   [&](uint32_t km2, int32_t dlim) {
 #pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        if (tid * PER + j > cut_k) break;
-        run += mass[j];
-        if (run > tm) { shared_cut = tid * PER + j; z_sh = run; break; }
-      }
+    for (int i = 0; i < SP_KREG; ++i)
+      if (i * SP_THREADS + tid < nch) hist_chunk(reg[i], km2, dlim, hist);
+    for (int c0 = SP_KREG * SP_THREADS + tid; c0 < nch; c0 += SP_TAIL * SP_THREADS) {
+      uint4 tl[SP_TAIL];
+#pragma unroll
+      for (int u = 0; u < SP_TAIL; ++u) tl[u] = x4[min(c0 + u * SP_THREADS, nch - 1)];
+#pragma unroll
+      for (int u = 0; u < SP_TAIL; ++u)
+        if (c0 + u * SP_THREADS < nch) hist_chunk(tl[u], km2, dlim, hist);
     }
-    __syncthreads();
-    st.cut = shared_cut;
-    st.Z = z_sh;
-  }
-  if (tid == 0) stats[row] = st;
+  });
 }
 
 // Greedy rows: 16 workgroups per row each reduce a slice to a packed
@@ -1058,11 +1120,15 @@ LOLLM_API long long lollm_sample_workspace_bytes(int rows) {
   return stats_bytes(rows);
 }
 
-LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int32_t* drafts,
-                                int B, int k, int V, float inv_temperature, int top_k, float top_p,
-                                uint64_t seed, uint64_t offset, const uint64_t* offset_dev,
-                                int32_t* n_accepted, int32_t* next_token, void* workspace,
-                                long long workspace_bytes, void* stream) {
+// lollm_spec_accept and lollm_spec_accept_rowmax: with target_rmax, the target rows'
+// statistics take their maxima from those slots (one read per row); draft rows, and
+// every row without target_rmax, the full row_stats pass.
+static int spec_accept_impl(const void* target, const uint16_t* target_rmax, long long rmax_ld,
+                            int rmax_slots, const void* draft, const int32_t* drafts, int B, int k,
+                            int V, float inv_temperature, int top_k, float top_p, uint64_t seed,
+                            uint64_t offset, const uint64_t* offset_dev, int32_t* n_accepted,
+                            int32_t* next_token, void* workspace, long long workspace_bytes,
+                            void* stream) {
   if (!target || !n_accepted || !next_token || !workspace || B <= 0 || k < 0) return LOLLM_EINVAL;
   if (k > 0 && !drafts) return LOLLM_EINVAL;
   if (k > 64) return LOLLM_EUNSUPPORTED;
@@ -1073,8 +1139,19 @@ LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int
   RowStat* st_t = (RowStat*)workspace;
   RowStat* st_d = st_t + rt;
   uint64_t* part = (uint64_t*)(st_d + rd);
-  int rc = launch_row_stats((const uint16_t*)target, rt, (const uint16_t*)draft, k > 0 ? rd : 0, V,
-                            inv_temperature, top_k, top_p, st_t, part, st);
+  int rc;
+  if (target_rmax && inv_temperature > 0.0f) {
+    hipLaunchKernelGGL(row_stats_known_kernel, dim3(rt), dim3(SP_THREADS), 0, st,
+                       (const uint16_t*)target, V, inv_temperature, top_k, top_p, st_t, target_rmax,
+                       rmax_ld, rmax_slots);
+    if ((rc = launch_status())) return rc;
+    rc = k > 0 && rd > 0 ? launch_row_stats((const uint16_t*)draft, rd, nullptr, 0, V,
+                                            inv_temperature, top_k, top_p, st_d, part, st)
+                         : 0;
+  } else {
+    rc = launch_row_stats((const uint16_t*)target, rt, (const uint16_t*)draft, k > 0 ? rd : 0, V,
+                          inv_temperature, top_k, top_p, st_t, part, st);
+  }
   if (rc) return rc;
   // the draw: B x ns workgroups sum the draw's weights over ns vocabulary slices (one
   // round of workgroups: one 1024-thread workgroup fits a CU), then one workgroup per
@@ -1103,6 +1180,29 @@ LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int
                      (const uint16_t*)draft, drafts, k, V, inv_temperature, seed, offset, offset_dev,
                      st_t, draft ? st_d : nullptr, ns, (const u128*)apart, n_accepted, next_token);
   return launch_status();
+}
+
+LOLLM_API int lollm_spec_accept(const void* target, const void* draft, const int32_t* drafts,
+                                int B, int k, int V, float inv_temperature, int top_k, float top_p,
+                                uint64_t seed, uint64_t offset, const uint64_t* offset_dev,
+                                int32_t* n_accepted, int32_t* next_token, void* workspace,
+                                long long workspace_bytes, void* stream) {
+  return spec_accept_impl(target, nullptr, 0, 0, draft, drafts, B, k, V, inv_temperature, top_k,
+                          top_p, seed, offset, offset_dev, n_accepted, next_token, workspace,
+                          workspace_bytes, stream);
+}
+
+LOLLM_API int lollm_spec_accept_rowmax(const void* target, const uint16_t* target_rowmax,
+                                       long long rowmax_ld, int rowmax_slots, const void* draft,
+                                       const int32_t* drafts, int B, int k, int V,
+                                       float inv_temperature, int top_k, float top_p,
+                                       uint64_t seed, uint64_t offset, const uint64_t* offset_dev,
+                                       int32_t* n_accepted, int32_t* next_token, void* workspace,
+                                       long long workspace_bytes, void* stream) {
+  if (!target_rowmax || rowmax_slots <= 0 || rowmax_ld < rowmax_slots) return LOLLM_EINVAL;
+  return spec_accept_impl(target, target_rowmax, rowmax_ld, rowmax_slots, draft, drafts, B, k, V,
+                          inv_temperature, top_k, top_p, seed, offset, offset_dev, n_accepted,
+                          next_token, workspace, workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------- allocation-free

@@ -274,6 +274,57 @@ def gemm_argmax(x, tiled, N, K, out=None, grid=0):
     return out
 
 
+def gemm_rowmax_slots(grid=0):
+    """Row-maximum slots per row that lollm_gemm_logits writes on `grid` workgroups."""
+    n = _lib.lib().lollm_gemm_rowmax_slots(grid)
+    if n < 0:
+        raise ValueError(f"unsupported grid {grid}")
+    return n
+
+
+def gemm_logits(x, tiled, N, K, out=None, rowmax=None, *, seen=None, penalty=1.0, extra=None,
+                n_extra0=0, T=1, grid=0):
+    """Logits x W^T (bf16) with the repetition penalty applied in place to row m = (s, t)
+    (s = m // T) for the tokens of seen[s] and extra[s, :n_extra0 + t] when seen is given
+    (the bits of repetition_penalty on the stored logits), and the rows' maxima in
+    `rowmax` (M, gemm_rowmax_slots(grid)) uint16 slots (lollm_gemm_logits; the input of
+    spec_accept(..., target_rowmax=rowmax)).  Returns (out, rowmax)."""
+    lead = x.shape[:-1]
+    M = x.numel() // K
+    if x.shape[-1] != K or M > GEMM_MAX_ROWS or M <= 0:
+        raise ValueError(f"gemm_logits takes 1..{GEMM_MAX_ROWS} rows of {K} features")
+    x = x.contiguous()
+    _need(x, "x", torch.bfloat16)
+    _need(tiled, "tiled", torch.bfloat16, (N * K,))
+    if out is None:
+        out = torch.empty(*lead, N, dtype=torch.bfloat16, device=x.device)
+    _need(out, "out", torch.bfloat16, (*lead, N))
+    slots = gemm_rowmax_slots(grid)
+    if rowmax is None:
+        rowmax = torch.empty(M, slots, dtype=torch.int16, device=x.device)
+    if rowmax.dtype != torch.int16 or rowmax.dim() != 2 or rowmax.shape[0] != M or \
+            rowmax.shape[1] != slots or rowmax.stride(1) != 1 or not rowmax.is_cuda:
+        raise ValueError(f"rowmax must be ({M}, {slots}) int16 rows on the device")
+    stride = 0
+    if seen is not None:
+        _need(seen, "seen", torch.int32)
+        if M % T or seen.shape[0] != M // T or seen.shape[1] < seen_words(N):
+            raise ValueError("seen must be (M / T, >= ceil(N / 32)) int32")
+        if extra is not None:
+            if extra.dtype != torch.int32 or extra.dim() != 2 or extra.shape[0] != M // T or \
+                    extra.stride(1) != 1:
+                raise ValueError("extra must be (M / T, n) int32 with unit column stride")
+            stride = extra.stride(0)
+    ws = gemm_workspace(gemm_workspace_bytes(M, N, K, grid), x.device)
+    rc = _lib.lib().lollm_gemm_logits(
+        _ptr(x), K, _ptr(tiled), M, N, K, _ptr(out), N, _ptr(rowmax), rowmax.stride(0),
+        None if seen is None else _ptr(seen), 0 if seen is None else seen.shape[1],
+        None if (seen is None or extra is None) else _ptr(extra), stride, int(n_extra0), int(T),
+        float(penalty), _ptr(ws), ws.numel(), grid, _stream())
+    _lib.check(rc, "lollm_gemm_logits")
+    return out, rowmax
+
+
 def gemm_rmsnorm_supported(M, N, K, grid=0):
     """Whether lollm_gemm_rmsnorm takes this shape (N <= 8192 and at least one
     (64-column, 128-k) unit per workgroup)."""
@@ -330,9 +381,12 @@ def inv_temperature(temperature: float) -> float:
 
 
 def spec_accept(target, draft, drafts, temperature, top_k=0, top_p=1.0, seed=0, offset=0, *,
-                offset_dev=None, workspace=None, n_accepted=None, next_token=None):
+                offset_dev=None, workspace=None, n_accepted=None, next_token=None,
+                target_rowmax=None):
     """target (B, k+1, V) bf16; draft (B, k, V) bf16 or None (argmax drafts);
-    drafts (B, k) int32.  Returns (n_accepted (B,), next_token (B,)) int32."""
+    drafts (B, k) int32.  target_rowmax: the (B (k+1), slots) row-maximum slots that
+    gemm_logits wrote with the target logits (lollm_spec_accept_rowmax: each target row
+    read once; same results).  Returns (n_accepted (B,), next_token (B,)) int32."""
     B, T, V = target.shape
     k = T - 1
     _need(target, "target", torch.bfloat16)
@@ -349,12 +403,20 @@ def spec_accept(target, draft, drafts, temperature, top_k=0, top_p=1.0, seed=0, 
         n_accepted = torch.empty(B, dtype=torch.int32, device=target.device)
     if next_token is None:
         next_token = torch.empty(B, dtype=torch.int32, device=target.device)
-    rc = _lib.lib().lollm_spec_accept(
-        _ptr(target), _ptr(draft), _ptr(drafts), B, k, V, inv_temperature(temperature),
-        int(top_k or 0), float(top_p if top_p is not None else 1.0), seed, offset,
-        _ptr(offset_dev), _ptr(n_accepted), _ptr(next_token), _ptr(workspace),
-        workspace.numel(), _stream())
-    _lib.check(rc, "lollm_spec_accept")
+    args = (B, k, V, inv_temperature(temperature), int(top_k or 0),
+            float(top_p if top_p is not None else 1.0), seed, offset, _ptr(offset_dev),
+            _ptr(n_accepted), _ptr(next_token), _ptr(workspace), workspace.numel(), _stream())
+    if target_rowmax is not None:
+        rm = target_rowmax
+        if rm.dtype != torch.int16 or rm.dim() != 2 or rm.shape[0] != B * T or rm.stride(1) != 1 \
+                or not rm.is_cuda:
+            raise ValueError(f"target_rowmax must be ({B * T}, slots) int16 rows on the device")
+        rc = _lib.lib().lollm_spec_accept_rowmax(_ptr(target), _ptr(rm), rm.stride(0), rm.shape[1],
+                                                 _ptr(draft), _ptr(drafts), *args)
+        _lib.check(rc, "lollm_spec_accept_rowmax")
+    else:
+        rc = _lib.lib().lollm_spec_accept(_ptr(target), _ptr(draft), _ptr(drafts), *args)
+        _lib.check(rc, "lollm_spec_accept")
     return n_accepted, next_token
 
 

@@ -186,6 +186,18 @@ class SpecDecoder:
         if self.greedy_argmax:   # reserve its workspace before any capture
             ops.gemm_workspace(ops._lib.lib().lollm_gemm_argmax_workspace_bytes(
                 batch * (k + 1), lm.N, lm.K, lm.grid()), dev)
+        # sampled verify: the lm_head writes the logits with the repetition penalty applied
+        # and the rows' maxima (lollm_gemm_logits), so the acceptance reads each row once
+        # (lollm_spec_accept_rowmax); set False to run lm_head, penalty and acceptance as
+        # separate passes (same bits)
+        self.fused_logits = (not self.greedy_argmax and temperature > 0 and lm.tiled is not None
+                             and lm.path(batch * (k + 1)) == "gemm")
+        self.verify_logits = self.verify_rmax = None
+        if self.fused_logits:
+            self.verify_logits = torch.empty(batch, k + 1, cfg.vocab_size, dtype=torch.bfloat16,
+                                             device=dev)
+            self.verify_rmax = torch.empty(batch * (k + 1), ops.gemm_rowmax_slots(lm.grid()),
+                                           dtype=torch.int16, device=dev)
         # per-draft-position index tensors (fixed across steps, so a graph can hold them)
         self.mtp_len = [torch.full((batch,), j, **i32) for j in range(k + 1)]
         self.graph = None
@@ -281,14 +293,24 @@ class SpecDecoder:
                             out=self.verify_amax.view(-1), grid=lm.grid())
             ops.greedy_accept(self.verify_amax, self.drafts, self.n_acc, self.next_tok)
         else:
-            logits = model.lm_head(normed)
-            if self.seen is not None:
+            rmax = None
+            if self.fused_logits:
+                lm = model.lm_head
                 # position t's context holds the pending token and the drafts before t
-                ops.repetition_penalty(logits, self.seen, self.penalty, extra=self.drafts)
+                logits, rmax = ops.gemm_logits(normed.reshape(-1, lm.K), lm.tiled, lm.N, lm.K,
+                                               out=self.verify_logits.view(-1, lm.N),
+                                               rowmax=self.verify_rmax, seen=self.seen,
+                                               penalty=self.penalty, extra=self.drafts,
+                                               T=k + 1, grid=lm.grid())
+                logits = logits.view(B, k + 1, -1)
+            else:
+                logits = model.lm_head(normed)
+                if self.seen is not None:
+                    ops.repetition_penalty(logits, self.seen, self.penalty, extra=self.drafts)
             ops.spec_accept(logits, self.draft_logits, self.drafts, self.temperature, self.top_k,
                             self.top_p, self.seed, 0, offset_dev=self.offset,
                             workspace=self.spec_ws, n_accepted=self.n_acc,
-                            next_token=self.next_tok)
+                            next_token=self.next_tok, target_rowmax=rmax)
         ops.spec_commit(verify_ids, self.n_acc, self.next_tok, cache.lengths, cache.rec_half,
                         cache.replay, cache.conv_off, self.pending, self.out_tokens, self.out_count,
                         hidden.contiguous(), self.h_last, self.offset, cache.spec_slots,

@@ -7,6 +7,8 @@ Checked here (the benchmark only times this workload):
   * one Gated DeltaNet layer and one gated-attention layer of the verify pass, on the
     prefilled cache (context 2048), against the CPU oracle at the bf16 bar;
   * graph replay == eager steps, token for token, with temperature 0.7 / top-p 0.95;
+  * the fused verify lm_head (penalty and row maxima in the GEMM, one read per row in
+    the acceptance) == the separate passes, token for token, with a repetition penalty;
   * the whole 32-layer verify pass against the oracle's model_forward (two sequences,
     fp32 and bf16 flows, from the GPU-prefilled cache) at the bf16 bar;
   * rollback == a shorter history, bit for bit: verify 4 tokens, keep a + 1 (a = 0..3
@@ -113,6 +115,29 @@ def test_c5_graph_replay_equals_eager(dense8b):
         del dec
     assert toks[0] == toks[1]
     assert all(len(t) == 5 for t in toks[0])       # random weights accept nothing here
+
+
+def test_c5_fused_logits_equal_separate_passes(dense8b):
+    """The sampled step (T = 0.7, top-p 0.95, repetition penalty 1.05) at full size, with
+    the verify lm_head writing penalised logits and row maxima in one kernel and the
+    acceptance reading each row once (lollm_gemm_logits + lollm_spec_accept_rowmax),
+    emits exactly the tokens of the separate passes (lm_head, lollm_repetition_penalty,
+    lollm_spec_accept), step after step."""
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    model, mtp, _, cfg, prompts, _ = dense8b
+    print("case C5 fused logits vs separate passes", flush=True)
+    toks = []
+    for fused in (True, False):
+        dec = SpecDecoder(model, mtp, B, L + 5 * (K + 1) + 8, k=K, temperature=0.7, top_p=0.95,
+                          seed=5, out_capacity=5 * (K + 1) + 4, repetition_penalty=1.05)
+        assert dec.fused_logits
+        dec.fused_logits = fused
+        dec.prefill(prompts)
+        for _ in range(4):
+            dec.step()
+        toks.append((dec.tokens(), dec.accept_hist.cpu().tolist()))
+        del dec
+    assert toks[0] == toks[1]
 
 
 class _AsFloat(dict):

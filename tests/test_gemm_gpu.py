@@ -256,6 +256,42 @@ def test_gemm_argmax_equals_gemm_then_greedy(M, N, K, grid):
     assert torch.equal(got.cpu().long(), logits.float().cpu().argmax(-1))
 
 
+@pytest.mark.parametrize("M,T,N,K,grid", [(64, 4, 2048, 512, 0), (64, 4, 8192, 256, 32),
+                                         (16, 1, 4096, 384, 7), (48, 3, 1024, 128, 1024)])
+@pytest.mark.parametrize("pen", [None, 1.3, 0.9])
+def test_gemm_logits_equals_gemm_then_penalty(M, T, N, K, grid, pen):
+    """lollm_gemm_logits (the verify lm_head with the repetition penalty and the row
+    maxima fused) stores exactly the bits of lollm_gemm followed by
+    lollm_repetition_penalty (src/generate.py:18-22 over each row's context: the seen
+    bitmap plus the drafts before the position), with groups cut and merged (grid 0,
+    1024), whole (grid 32 over 128 groups) and on the k-split kernel (16 rows); and the
+    largest of each row's slots is the row's maximum order key."""
+    from lollm_amd import ops
+    print(f"case gemm_logits M={M} T={T} N={N} K={K} grid={grid} pen={pen}", flush=True)
+    x, W = case(M, N, K, seed=M + N + K + 3)
+    Wt = ops.gemm_tile_weights(W.cuda())
+    xd = x.cuda()
+    S = M // T
+    g = torch.Generator().manual_seed(N + K)
+    seen = extra = None
+    want = ops.gemm(xd, Wt, N, K, grid=grid)
+    if pen is not None:
+        seen = ops.new_seen(S, N, "cuda")
+        ops.seen_mark(seen, torch.randint(0, N, (S, N // 8), generator=g).int().cuda(), N)
+        extra = torch.randint(0, N, (S, T + 2), generator=g).int().cuda()
+        extra[:, 1] = extra[:, 0]                        # a repeated draft token
+        ops.repetition_penalty(want.view(S, T, N), seen, pen, extra=extra, n_extra0=1)
+    got, rm = ops.gemm_logits(xd, Wt, N, K, seen=seen, penalty=pen or 1.0, extra=extra,
+                              n_extra0=1, T=T, grid=grid)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16).cpu(), want.view(torch.int16).cpu())
+    b = want.view(torch.int16).int().cpu() & 0xFFFF
+    o = torch.where((b & 0x8000) != 0, (~b) & 0xFFFF, b | 0x8000)
+    slots = rm.cpu().int() & 0xFFFF
+    assert torch.equal(slots.max(-1).values, o.max(-1).values)
+    assert rm.shape[1] == ops.gemm_rowmax_slots(grid)
+
+
 def test_gemm_argmax_ties_and_strided_out():
     """Equal columns: the lowest index wins; the token lands in one column of a (M, k)
     table (row stride k), the others untouched."""

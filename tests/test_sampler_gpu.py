@@ -64,6 +64,45 @@ def test_spec_accept_bit_exact_full_vocab(with_draft, temp, top_k, top_p):
         assert np.array_equal(nt.cpu().numpy(), nt_ref)
 
 
+def order_key_slots(x, slots=5, at=2):
+    """The row-maximum slots lollm_gemm_logits writes, built on the host for rows x
+    (rows, V) bf16: slot `at` holds each row's largest order key (bf16 bits b:
+    b & 0x8000 ? ~b & 0xFFFF : b | 0x8000), the other slots lower keys (0 and the row's
+    first key), so the consumer must take the maximum over all of them."""
+    b = x.reshape(-1, x.shape[-1]).view(torch.int16).int() & 0xFFFF
+    o = torch.where((b & 0x8000) != 0, (~b) & 0xFFFF, b | 0x8000)
+    out = torch.zeros(o.shape[0], slots, dtype=torch.int32)
+    out[:, at] = o.max(-1).values
+    out[:, (at + 1) % slots] = o[:, 0]
+    return torch.where(out >= 32768, out - 65536, out).to(torch.int16)
+
+
+@pytest.mark.parametrize("with_draft", [True, False])
+@pytest.mark.parametrize("temp,top_k,top_p", [(0.7, 0, 0.95), (0.7, 20, 0.8), (1.7, 50, 0.5)])
+def test_spec_accept_rowmax_bit_exact(with_draft, temp, top_k, top_p):
+    """lollm_spec_accept_rowmax (the target rows' maxima given, each row read once) on the
+    full-vocabulary acceptance workload, and on rows whose logits are all negative (the
+    order-key maximum), equals the C oracle bit for bit."""
+    from lollm_amd import ops
+    print(f"case accept rowmax draft={with_draft} T={temp} top_k={top_k} top_p={top_p}", flush=True)
+    B, k, V = 64, 3, 151936
+    tgt, drf = acceptance_case(B, k, V, seed=5)
+    tgt[:3] = -(tgt[:3].float().abs() + 0.01).bfloat16()       # rows with no logit >= 0
+    inv = S.inv_temperature(temp)
+    drafts = np.stack([S.sample_rows(drf[:, i].contiguous(), inv, top_k, top_p, 7, 0, 0, k + 1 + i)
+                       for i in range(k)], 1).astype(np.int32)
+    if not with_draft:
+        drf = None
+    rm = order_key_slots(tgt).cuda()
+    for off in (0, 9):
+        na_ref, nt_ref = S.spec_accept(tgt, drf, drafts, inv, top_k, top_p, 7, off)
+        na, nt = ops.spec_accept(tgt.cuda(), None if drf is None else drf.cuda(),
+                                 torch.from_numpy(drafts).cuda(), temp, top_k, top_p, 7, off,
+                                 target_rowmax=rm)
+        assert np.array_equal(na.cpu().numpy(), na_ref)
+        assert np.array_equal(nt.cpu().numpy(), nt_ref)
+
+
 def test_spec_accept_small_vocab_ties_and_edges():
     """Tiny vocabulary with heavy ties, flushed keys and argmax-drawn drafts; many
     offsets so accepts, residual draws and bonus draws all occur."""
