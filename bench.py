@@ -175,7 +175,6 @@ def verify_breakdown(dec, iters=20):
     import torch
     from lollm_amd import ops
     B, k, model = dec.B, dec.k, dec.model
-    ids = torch.cat([dec.pending.view(B, 1), dec.drafts], 1).long()
     st = {}
     st["draft_chain_us"] = time_fn(dec._draft_chain, iters)
 
@@ -185,7 +184,7 @@ def verify_breakdown(dec, iters=20):
         # the verify pass over 1 + k positions (KV rows / GDN snapshots are written but
         # not committed, so repeating it is idempotent), ending in the step's lm_head:
         # logits with the penalty and row maxima fused when the step samples
-        hidden, normed = model.hidden_states(ids, dec.cache)
+        hidden, normed = dec.verify_hidden()
         if dec.fused_logits:
             lg, rm = ops.gemm_logits(normed.reshape(-1, lm.K), lm.tiled, lm.N, lm.K,
                                      out=dec.verify_logits.view(-1, lm.N), rowmax=dec.verify_rmax,

@@ -170,6 +170,19 @@ int lollm_philox_uniform_u24(uint64_t seed, uint64_t offset, int rows, int slots
 int lollm_rmsnorm(const void* x, const void* residual, void* x_out, const void* w, void* y,
                   int rows, int H, float eps, void* stream);
 
+/* The verify block's input in one kernel: the ids [pending, draft_1 .. draft_k] of the
+ * verify pass (src/qwen3_5/mtp.py:141-142, `two`), their embedding rows
+ * (modeling_qwen3_5.py:86) and layer 0's input RMSNorm (modeling_qwen3_5.py:48), with
+ * lollm_rmsnorm's arithmetic, so the bits equal the concatenation + lookup + norm it
+ * replaces.  first (B) int32, drafts (B, k) int32 (may be NULL when k == 0); ids (B, 1 + k)
+ * int32 receives the ids as given (clamped into [0, vocab) only for the lookup); x, y
+ * (B (1 + k), H) bf16 receive the embedding rows and their norm; kv_len (B) int32, if not
+ * NULL, receives lengths[b] + 1 + k.  table (vocab, H) bf16, w (H) bf16.  Supported:
+ * H % 8 == 0, H <= 8192. */
+int lollm_verify_input(const int32_t* first, const int32_t* drafts, int k, const void* table,
+                       int vocab, const void* w, float eps, const int32_t* lengths, int32_t* ids,
+                       void* x, void* y, int32_t* kv_len, int B, int H, void* stream);
+
 /* The MTP head's fc input from draft token ids (src/qwen3_5/mtp.py:61-73, with the
  * embedding lookup the draft chain does before it): out (B, 2H) bf16, row b =
  * [RMSNorm_{1+w_emb}(table[tok[b]]) | RMSNorm_{1+w_hidden}(hidden[b])], each half with

@@ -44,6 +44,7 @@ SIGNATURES = {
                            ctypes.c_longlong, _P], _I),
     "lollm_philox_uniform_u24": ([_U64, _U64, _I, _I, _P, _P], _I),
     "lollm_rmsnorm": ([_P, _P, _P, _P, _P, _I, _I, _F, _P], _I),
+    "lollm_verify_input": ([_P, _P, _I, _P, _I, _P, _F, _P, _P, _P, _P, _P, _I, _I, _P], _I),
     "lollm_mtp_input": ([_P, ctypes.c_longlong, _P, ctypes.c_longlong, _P, _I, _P, _P, _P, _I, _I,
                          _F, _P], _I),
     "lollm_gemm_argmax_workspace_bytes": ([_I, _I, _I, _I], ctypes.c_longlong),

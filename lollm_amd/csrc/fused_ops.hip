@@ -5,6 +5,8 @@
 //                modeling_qwen3_5.py:59-60 (x <- x + h, then y = norm(x))
 //   mtp_input    (src/qwen3_5/mtp.py:61-73) the MTP head's fc input from token ids:
 //                embedding lookup, both pre-fc RMSNorms and the concatenation
+//   verify_input (src/qwen3_5/mtp.py:141-142 + modeling_qwen3_5.py embedding and layer
+//                0's input norm) the verify block's ids, embedding rows and their norm
 //   swiglu       (blocks.py:341-342) silu(gate) * up on a fused [gate | up] GEMM output
 //   attn_prologue (blocks.py:214-227 + RoPE blocks.py:166-183 + kv.py:26-33):
 //                split q_proj's per-head [query | gate], QK-norm (1 + w), partial
@@ -115,6 +117,32 @@ __global__ __launch_bounds__(RMS_THREADS) void mtp_input_kernel(const int32_t* _
   } else {
     rms_row(hidden + (size_t)b * ldh, nullptr, nullptr, w_hid, y + H, H, eps, red);
   }
+}
+
+// The verify block's input: ids[b] = [first[b], drafts[b, 0 .. k)] (T = k + 1 tokens),
+// x[b, t] = table[ids[b, t]] (the embedding rows that open the residual stream) and
+// y[b, t] = RMSNorm_{1+w}(x[b, t]) (layer 0's input norm, the row arithmetic of
+// lollm_rmsnorm, so the bits equal the concatenation + embedding + norm it replaces);
+// kv_len[b] = lengths[b] + T.  Workgroup (b, t); ids are clamped into the table for the
+// lookup and stored as given.
+__global__ __launch_bounds__(RMS_THREADS) void verify_input_kernel(
+    const int32_t* __restrict__ first, const int32_t* __restrict__ drafts, int k,
+    const uint16_t* __restrict__ table, int V, const uint16_t* __restrict__ w,
+    uint16_t* __restrict__ x, uint16_t* __restrict__ y, int32_t* __restrict__ ids,
+    const int32_t* __restrict__ lengths, int32_t* __restrict__ kv_len, int H, float eps) {
+  __shared__ float red[RMS_THREADS / 64];
+  const int b = blockIdx.x, t = blockIdx.y, T = k + 1;
+  const int id0 = t == 0 ? first[b] : drafts[(size_t)b * k + t - 1];
+  const size_t row = (size_t)b * T + t;
+  if (threadIdx.x == 0) {
+    ids[row] = id0;
+    if (t == 0 && kv_len) kv_len[b] = lengths[b] + T;
+  }
+  const int id = id0 < 0 ? 0 : (id0 >= V ? V - 1 : id0);
+  const uint16_t* src = table + (size_t)id * H;
+  for (int c = threadIdx.x; c < H / 8; c += RMS_THREADS)
+    reinterpret_cast<uint4*>(x + row * H)[c] = reinterpret_cast<const uint4*>(src)[c];
+  rms_row(src, nullptr, nullptr, w, y + row * H, H, eps, red);
 }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
@@ -446,6 +474,20 @@ LOLLM_API int lollm_mtp_input(const int32_t* tok, long long tok_stride, const vo
   hipLaunchKernelGGL(mtp_input_kernel, dim3(B, 2), dim3(RMS_THREADS), 0, (hipStream_t)stream, tok,
                      tok_stride, (const uint16_t*)hidden, ld_hidden, (const uint16_t*)table, vocab,
                      (const uint16_t*)w_emb, (const uint16_t*)w_hidden, (uint16_t*)out, H, eps);
+  return launch_status();
+}
+
+LOLLM_API int lollm_verify_input(const int32_t* first, const int32_t* drafts, int k,
+                                 const void* table, int vocab, const void* w, float eps,
+                                 const int32_t* lengths, int32_t* ids, void* x, void* y,
+                                 int32_t* kv_len, int B, int H, void* stream) {
+  if (!first || !table || !w || !ids || !x || !y || B <= 0 || H <= 0 || vocab <= 0 || k < 0)
+    return LOLLM_EINVAL;
+  if ((k > 0 && !drafts) || (kv_len && !lengths)) return LOLLM_EINVAL;
+  if (H % 8 || H > 8192 || B > 65535 || k + 1 > 65535) return LOLLM_EUNSUPPORTED;
+  hipLaunchKernelGGL(verify_input_kernel, dim3(B, k + 1), dim3(RMS_THREADS), 0,
+                     (hipStream_t)stream, first, drafts, k, (const uint16_t*)table, vocab,
+                     (const uint16_t*)w, (uint16_t*)x, (uint16_t*)y, ids, lengths, kv_len, H, eps);
   return launch_status();
 }
 

@@ -21,17 +21,17 @@
 //
 // Kernels:
 //   row_stats    one 1024-thread workgroup per row (target and draft rows in one
-//                launch), two per CU (64 registers per thread): the first 8 x 16 B per
-//                thread of the row stay in registers, the rest is read in batches of 4
-//                per thread for the maximum and again (mostly from cache) for the counts
-//                (12% faster at 448 rows than holding all 19 per thread, one row per CU),
-//                giving the
-//                max key (a packed signed 16-bit max of the raw bits, one op per two
-//                tokens; rows with no logit >= +0 take the order-key max), then a per-key
-//                count histogram over the NBINS keys below the max in LDS (distances
-//                computed two tokens at a time in packed 16-bit arithmetic; without top-k,
-//                tokens whose weight test fails are not counted) and block scans for the
-//                top-k / top-p cut points and the kept mass Z;
+//                launch), two per CU (64 registers per thread), one HBM pass: the first
+//                8 x 16 B per thread of the row stay in registers and give a lower bound
+//                of the max key; the whole row is counted as it streams into a per-key
+//                histogram in LDS over a window of 2 NBINS keys ending NBINS above that
+//                bound (distances computed two tokens at a time in packed 16-bit
+//                arithmetic), which holds the NBINS keys below the row's max key
+//                whenever the max lies within NBINS keys of the bound (otherwise the row
+//                is counted again); then block scans for the top-k / top-p cut points
+//                and the kept mass Z;
+//   row_stats_known  the same for rows whose max key is given (the verify lm_head's
+//                row-maximum slots): the whole row in registers, counted directly;
 //   argmax_*     greedy rows: the row split over 16 workgroups, partial maxima
 //                merged by a second tiny kernel (a greedy row needs no histogram);
 //   spec_partial / spec_final  the k accept tests in parallel, then the residual or
@@ -153,12 +153,6 @@ typedef short sp_s2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(sp_us2, a),
                                                                 __builtin_bit_cast(sp_us2, b)));
-}
-
-// Signed 16-bit maximum of the raw bf16 halves: for non-negative bf16 the bit pattern
-// orders like the value, and every negative pattern is below every non-negative one.
-__device__ __forceinline__ sp_s2 max_s16x2(sp_s2 m, uint32_t w) {
-  return __builtin_elementwise_max(m, __builtin_bit_cast(sp_s2, w));
 }
 
 // Distances below the row's maximum key, kmax - skey(b), of the two bf16 of w as 16-bit
@@ -432,12 +426,28 @@ __device__ __forceinline__ void row_stats_counts(uint32_t top_bits, float inv_te
 
 // Sampled rows only (inv_temp > 0); greedy rows take the split argmax below.  Rows
 // [0, rows0) are read from x0, the rest from x1 (target and draft rows in one launch).
+// One HBM pass: the maximum is not known while the row streams, so the keys are
+// counted into a window of SP_WIN keys that ends SP_NBINS keys above the maximum of
+// the first SP_REG chunks per thread (a lower bound of the row's maximum km); any
+// maximum up to that end leaves every distance 0 .. SP_NBINS - 1 below km inside the
+// window, so the histogram of row_stats_counts is the window from (end - km) on.  A row
+// whose maximum lies further above is read and counted again in a zeroed window.
+// Without top-k every key in the window is counted (the counts whose weight test fails
+// weigh 0 in the mass and are read for nothing else).
+constexpr int SP_WIN = 2 * SP_NBINS;
+
+// The order-key maximum of a chunk's 8 tokens, folded into m2 (two 16-bit halves).
+__device__ __forceinline__ uint32_t ord_max_chunk(uint32_t m2, const uint4& u) {
+  return max_u16x2(max_u16x2(m2, ord_pair(u.x)),
+                   max_u16x2(max_u16x2(ord_pair(u.y), ord_pair(u.z)), ord_pair(u.w)));
+}
+
 __global__ __launch_bounds__(SP_THREADS, 8) void row_stats_kernel(const uint16_t* __restrict__ x0,
                                                                int rows0,
                                                                const uint16_t* __restrict__ x1,
                                                                int V, float inv_temp, int top_k,
                                                                float top_p, RowStat* stats) {
-  __shared__ uint32_t hist[SP_NBINS];
+  __shared__ uint32_t win[SP_WIN];
   __shared__ uint64_t s64[16];
   __shared__ int32_t shared_cut;
   __shared__ uint64_t z_sh;
@@ -446,72 +456,54 @@ __global__ __launch_bounds__(SP_THREADS, 8) void row_stats_kernel(const uint16_t
   const int nch = V >> 3;
   const uint16_t* src = row < rows0 ? x0 + (size_t)row * V : x1 + (size_t)(row - rows0) * V;
   const uint4* x4 = reinterpret_cast<const uint4*>(src);
-  // ---- the row into registers (one HBM pass); zero the histogram meanwhile ----
+  // ---- the first SP_REG chunks per thread into registers; zero the window meanwhile ----
   uint4 reg[SP_REG];
 #pragma unroll
-  for (int i = 0; i < SP_REG; ++i) {
-    const int c = i * SP_THREADS + tid;
-    reg[i] = c < nch ? x4[c] : make_uint4(0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u);
-  }
-  for (int i = tid; i < SP_NBINS; i += SP_THREADS) hist[i] = 0;
-  // ---- the maximum: signed 16-bit maximum of the raw halves (one packed op per two
-  //      tokens; padding is -0, the lowest pattern of that order) ----
-  sp_s2 mraw = {(short)-32768, (short)-32768};
+  for (int i = 0; i < SP_REG; ++i) reg[i] = x4[min(i * SP_THREADS + tid, nch - 1)];
+  for (int i = tid; i < SP_WIN; i += SP_THREADS) win[i] = 0u;
+  uint32_t m2 = 0;   // order keys: 0 is below every token's
 #pragma unroll
-  for (int i = 0; i < SP_REG; ++i) {
-    mraw = max_s16x2(mraw, reg[i].x);
-    mraw = max_s16x2(mraw, reg[i].y);
-    mraw = max_s16x2(mraw, reg[i].z);
-    mraw = max_s16x2(mraw, reg[i].w);
-  }
-  // the rest of the row in batches (addresses clamped into the row: a repeated chunk
-  // cannot change a maximum)
+  for (int i = 0; i < SP_REG; ++i)
+    if (i * SP_THREADS + tid < nch) m2 = ord_max_chunk(m2, reg[i]);
+  // the window's end (block_max's barriers also publish the zeroed window)
+  const int32_t k0 =
+      skey(ord_bits((uint32_t)block_max<uint64_t>((uint64_t)max(m2 & 0xFFFFu, m2 >> 16), s64)));
+  const int32_t kend = k0 + SP_NBINS;
+  const uint32_t ke2 = ((uint32_t)kend & 0xFFFFu) * 0x10001u;
+#pragma unroll
+  for (int i = 0; i < SP_REG; ++i)
+    if (i * SP_THREADS + tid < nch) hist_chunk(reg[i], ke2, SP_WIN - 1, win);
+  // the rest of the row in batches, counted as it arrives (addresses clamped into the
+  // row; the repeats are neither counted nor maximised)
   for (int c0 = SP_REG * SP_THREADS + tid; c0 < nch; c0 += SP_TAIL * SP_THREADS) {
     uint4 tl[SP_TAIL];
 #pragma unroll
     for (int u = 0; u < SP_TAIL; ++u) tl[u] = x4[min(c0 + u * SP_THREADS, nch - 1)];
 #pragma unroll
     for (int u = 0; u < SP_TAIL; ++u)
-      mraw = max_s16x2(max_s16x2(max_s16x2(max_s16x2(mraw, tl[u].x), tl[u].y), tl[u].z), tl[u].w);
-  }
-  const int32_t mx =
-      (int32_t)block_max<uint64_t>((uint64_t)(max((int32_t)mraw.x, (int32_t)mraw.y) + 32768), s64) -
-      32768;
-  uint32_t top_bits = (uint32_t)mx;
-  if (mx < 0) {
-    // no logit is >= +0: the maximum in the full order of the keys (packed order keys,
-    // two tokens per max)
-    uint32_t m2 = 0;
-#pragma unroll
-    for (int i = 0; i < SP_REG; ++i) {
-      const int c = i * SP_THREADS + tid;
-      if (c < nch) {
-        m2 = max_u16x2(m2, ord_pair(reg[i].x));
-        m2 = max_u16x2(m2, ord_pair(reg[i].y));
-        m2 = max_u16x2(m2, ord_pair(reg[i].z));
-        m2 = max_u16x2(m2, ord_pair(reg[i].w));
+      if (c0 + u * SP_THREADS < nch) {
+        m2 = ord_max_chunk(m2, tl[u]);
+        hist_chunk(tl[u], ke2, SP_WIN - 1, win);
       }
-    }
-    for (int c = SP_REG * SP_THREADS + tid; c < nch; c += SP_THREADS) {
-      const uint4 u = x4[c];
-      m2 = max_u16x2(max_u16x2(m2, ord_pair(u.x)), max_u16x2(ord_pair(u.y), max_u16x2(ord_pair(u.z), ord_pair(u.w))));
-    }
-    top_bits = ord_bits((uint32_t)block_max<uint64_t>((uint64_t)max((m2 & 0xFFFFu), (m2 >> 16)), s64));
   }
-  row_stats_counts(top_bits, inv_temp, top_k, top_p, stats + row, hist, s64,
-                   &shared_cut, &z_sh, [&](uint32_t km2, int32_t dlim) {
-#pragma unroll
-    for (int i = 0; i < SP_REG; ++i) {
-      const int ch = i * SP_THREADS + tid;
-      if (ch < nch) hist_chunk(reg[i], km2, dlim, hist);
-    }
-    for (int c0 = SP_REG * SP_THREADS + tid; c0 < nch; c0 += SP_TAIL * SP_THREADS) {
+  const uint32_t top_bits =
+      ord_bits((uint32_t)block_max<uint64_t>((uint64_t)max(m2 & 0xFFFFu, m2 >> 16), s64));
+  const int32_t km = skey(top_bits);
+  const bool inside = km <= kend;   // the same in every thread
+  row_stats_counts(top_bits, inv_temp, top_k, top_p, stats + row, inside ? win + (kend - km) : win,
+                   s64, &shared_cut, &z_sh, [&](uint32_t km2, int32_t dlim) {
+    if (inside) return;
+    // the maximum lies above the window: count the whole row again below km
+    __syncthreads();
+    for (int i = tid; i < SP_NBINS; i += SP_THREADS) win[i] = 0u;
+    __syncthreads();
+    for (int c0 = tid; c0 < nch; c0 += SP_TAIL * SP_THREADS) {
       uint4 tl[SP_TAIL];
 #pragma unroll
       for (int u = 0; u < SP_TAIL; ++u) tl[u] = x4[min(c0 + u * SP_THREADS, nch - 1)];
 #pragma unroll
       for (int u = 0; u < SP_TAIL; ++u)
-        if (c0 + u * SP_THREADS < nch) hist_chunk(tl[u], km2, dlim, hist);
+        if (c0 + u * SP_THREADS < nch) hist_chunk(tl[u], km2, dlim, win);
     }
   });
 }

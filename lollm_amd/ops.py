@@ -482,6 +482,42 @@ def mtp_input(tok, hidden, table, w_emb, w_hidden, eps, out=None):
     return out
 
 
+def verify_input(first, drafts, table, w, eps, lengths=None, *, ids=None, x=None, y=None,
+                 kv_len=None):
+    """The verify block's input in one kernel (lollm_verify_input): ids = [first | drafts]
+    (B, 1 + k) int32, x = table[ids] and y = RMSNorm_{1+w}(x), both (B, 1 + k, H) bf16, and,
+    with lengths, kv_len = lengths + 1 + k.  first (B,) int32, drafts (B, k) int32.
+    Returns (ids, x, y, kv_len)."""
+    B = first.numel()
+    V, H = table.shape
+    if first.dtype != torch.int32 or first.dim() != 1 or not first.is_cuda:
+        raise ValueError("first must be a (B,) int32 device tensor")
+    k = 0 if drafts is None else drafts.shape[1]
+    if drafts is not None:
+        _need(drafts, "drafts", torch.int32, (B, k))
+    _need(table, "table", torch.bfloat16)
+    _need(w, "w", torch.bfloat16, (H,))
+    T = k + 1
+    dev = table.device
+    ids = torch.empty(B, T, dtype=torch.int32, device=dev) if ids is None else ids
+    x = torch.empty(B, T, H, dtype=torch.bfloat16, device=dev) if x is None else x
+    y = torch.empty(B, T, H, dtype=torch.bfloat16, device=dev) if y is None else y
+    _need(ids, "ids", torch.int32, (B, T))
+    _need(x, "x", torch.bfloat16, (B, T, H))
+    _need(y, "y", torch.bfloat16, (B, T, H))
+    if lengths is not None:
+        _need(lengths, "lengths", torch.int32, (B,))
+        kv_len = torch.empty(B, dtype=torch.int32, device=dev) if kv_len is None else kv_len
+        _need(kv_len, "kv_len", torch.int32, (B,))
+    else:
+        kv_len = None
+    rc = _lib.lib().lollm_verify_input(_ptr(first), _ptr(drafts), k, _ptr(table), V, _ptr(w),
+                                       float(eps), _ptr(lengths), _ptr(ids), _ptr(x), _ptr(y),
+                                       _ptr(kv_len), B, H, _stream())
+    _lib.check(rc, "lollm_verify_input")
+    return ids, x, y, kv_len
+
+
 def rmsnorm(x, w, eps, residual=None, x_out=None, out=None):
     """y = RMSNorm_{1+w}(x) or, with residual, x_out = x + residual, y = norm(x_out).
     x: (..., H) bf16.  Returns y, or (y, x_out) when residual is given."""

@@ -109,22 +109,28 @@ class Qwen3_5Model:
 
     __call__ = forward
 
-    def hidden_states(self, input_ids, cache):
+    def hidden_states(self, input_ids, cache, inputs=None):
         """The decoder stack; returns (pre-norm hidden, final-normed hidden).  Writes
         the KV rows / GDN records of the T new tokens but does not commit them.  The
-        caller has checked the capacity (cache.reserve(T))."""
+        caller has checked the capacity (cache.reserve(T)).  inputs: the block's
+        (embedding rows, layer 0's input norm of them, lengths + T) when already formed
+        (lollm_verify_input), else they are formed here."""
         B, T = input_ids.shape
         cfg = self.cfg
-        x = self.model.embed_tokens(input_ids.to(self.device))
         lengths = cache.lengths
-        kv_len = lengths + T
+        if inputs is None:
+            x = self.model.embed_tokens(input_ids.to(self.device))
+            kv_len = lengths + T
+            h_first = None
+        else:
+            x, h_first, kv_len = inputs
         ws = self.attn_workspace(B, T, cache.max_len)
         # each residual-stream projection (o_proj / out_proj / down_proj) is issued with
         # the residual add and the norm that follows it (modeling_qwen3_5.py:59-60)
         pending = None   # (down_proj, its input): opens the next layer
         for i, layer in enumerate(self.model.layers):
             if pending is None:
-                h_in = layer.input_layernorm(x)
+                h_in = layer.input_layernorm(x) if h_first is None else h_first
             else:
                 h_in, x = pending[0].add_norm(pending[1], x, layer.input_layernorm)
             if layer.layer_type == "full_attention":

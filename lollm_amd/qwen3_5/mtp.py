@@ -198,6 +198,13 @@ class SpecDecoder:
                                              device=dev)
             self.verify_rmax = torch.empty(batch * (k + 1), ops.gemm_rowmax_slots(lm.grid()),
                                            dtype=torch.int16, device=dev)
+        # the verify block's ids, embedding rows, layer 0 input norm and key counts, formed
+        # by one kernel (lollm_verify_input)
+        H = cfg.hidden_size
+        self.verify_ids = torch.zeros(batch, k + 1, **i32)
+        self.verify_x = torch.zeros(batch, k + 1, H, dtype=torch.bfloat16, device=dev)
+        self.verify_y = torch.zeros(batch, k + 1, H, dtype=torch.bfloat16, device=dev)
+        self.verify_kv_len = torch.zeros(batch, **i32)
         # per-draft-position index tensors (fixed across steps, so a graph can hold them)
         self.mtp_len = [torch.full((batch,), j, **i32) for j in range(k + 1)]
         self.graph = None
@@ -282,11 +289,24 @@ class SpecDecoder:
         if live:
             self._grew()
 
+    def verify_hidden(self):
+        """The verify pass over [pending | drafts] (mtp.py:141-142): the block's ids,
+        embedding rows and layer 0 norm in one kernel, then the decoder stack; returns
+        (pre-norm hidden, final-normed hidden) as Qwen3_5Model.hidden_states."""
+        m = self.model
+        ops.verify_input(self.pending, self.drafts, m.model.embed_tokens.weight,
+                         m.model.layers[0].input_layernorm.weight,
+                         m.model.layers[0].input_layernorm.eps, self.cache.lengths,
+                         ids=self.verify_ids, x=self.verify_x, y=self.verify_y,
+                         kv_len=self.verify_kv_len)
+        return m.hidden_states(self.verify_ids, self.cache,
+                               inputs=(self.verify_x, self.verify_y, self.verify_kv_len))
+
     def _step_kernels(self):
         B, k, model, cache = self.B, self.k, self.model, self.cache
         self._draft_chain()
-        verify_ids = torch.cat([self.pending.view(B, 1), self.drafts], 1)
-        hidden, normed = model.hidden_states(verify_ids, cache)   # int32 ids: no widening copy
+        hidden, normed = self.verify_hidden()
+        verify_ids = self.verify_ids
         if self.greedy_argmax:
             lm = model.lm_head
             ops.gemm_argmax(normed.reshape(-1, lm.K), lm.tiled, lm.N, lm.K,

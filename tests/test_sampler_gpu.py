@@ -205,3 +205,34 @@ def test_sample_rows_negative_and_extreme_rows(temp, top_k, top_p):
         ref = S.sample_rows(rows, inv, top_k, top_p, 23, off, row_base=1, slot=2)
         got = ops.sample_rows(rows.cuda(), temp, top_k, top_p, 23, off, row_base=1, slot=2)
         assert np.array_equal(got.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("temp,top_k,top_p", [(0.7, 0, 0.95), (1.3, 40, 0.9)])
+def test_sample_rows_maximum_above_the_count_window(temp, top_k, top_p):
+    """The statistics kernel counts keys in one pass over a window placed by the maximum
+    of each thread's first 8 chunks (the first 65536 tokens); a row whose maximum lies
+    more than 8192 keys above that is counted again: a far larger finite maximum, +inf
+    and NaN past the first 65536 tokens, and a maximum exactly at the window's edge."""
+    from lollm_amd import ops
+    print(f"case window edge rows T={temp} top_k={top_k} top_p={top_p}", flush=True)
+    V = 151936
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn(5, V, generator=gen) * 3
+    x[0, :65536] = -1.0e30                          # far below the rest: second pass
+    x[1, 150000] = float("inf")
+    x[2, 100000] = float("nan")
+    # row 3: the first 65536 tokens at one key, a maximum exactly 8192 keys above it
+    # (the last key the window holds), row 4 one key past it
+    lo = 0x3F80                                     # bf16 1.0
+    x[3, :65536] = 1.0
+    x[4, :65536] = 1.0
+    x[3, 65536:] = 0.5
+    x[4, 65536:] = 0.5
+    x[3, 70000] = torch.tensor([lo + 8192], dtype=torch.int16).view(torch.bfloat16).float()
+    x[4, 70000] = torch.tensor([lo + 8193], dtype=torch.int16).view(torch.bfloat16).float()
+    rows = x.bfloat16()
+    inv = S.inv_temperature(temp)
+    for off in (0, 2):
+        ref = S.sample_rows(rows, inv, top_k, top_p, 29, off, row_base=0, slot=0)
+        got = ops.sample_rows(rows.cuda(), temp, top_k, top_p, 29, off, row_base=0, slot=0)
+        assert np.array_equal(got.cpu().numpy(), ref)
