@@ -265,16 +265,6 @@ __global__ __launch_bounds__(256) void attn_small_kernel(
   const int pos = lengths[b];
   const int rpos = rope_pos ? rope_pos[b] : pos;
   const size_t cbase = ((size_t)b * Hkv + kvh) * max_len;
-  // the cached K and V rows the scores and the output read (lane: dims 4 lane .. + 3),
-  // every row of the short cache requested here, before anything else: they depend on
-  // nothing this kernel computes (row pos, written below, is taken from knew / vnew)
-  uint2 kold[AS_MAXL], vold[AS_MAXL];
-#pragma unroll
-  for (int j = 0; j < AS_MAXL; ++j) {
-    const size_t r = cbase + (j < max_len ? j : max_len - 1);
-    kold[j] = *reinterpret_cast<const uint2*>(kc + r * D + 4 * lane);
-    vold[j] = *reinterpret_cast<const uint2*>(vc + r * D + 4 * lane);
-  }
   // every input of this (sequence, kv head) in one batch: k, v, the n_rep query heads and
   // their gates (the heads' norms below then run side by side, not one after another)
   const float kx = bf16_to_f32(src[(long long)Hq * 2 * D + kvh * D + d]);
@@ -355,7 +345,7 @@ __global__ __launch_bounds__(256) void attn_small_kernel(
 #pragma unroll
           for (int e = 0; e < 4; ++e) kv4[e] = knew[4 * lane + e];
         } else {
-          const uint2 u = kold[j];
+          const uint2 u = *reinterpret_cast<const uint2*>(kc + (cbase + j) * D + 4 * lane);
           kv4[0] = __uint_as_float(u.x << 16); kv4[1] = __uint_as_float(u.x & 0xffff0000u);
           kv4[2] = __uint_as_float(u.y << 16); kv4[3] = __uint_as_float(u.y & 0xffff0000u);
         }
@@ -381,7 +371,7 @@ __global__ __launch_bounds__(256) void attn_small_kernel(
 #pragma unroll
           for (int e = 0; e < 4; ++e) vv4[e] = vnew[4 * lane + e];
         } else {
-          const uint2 u = vold[j];
+          const uint2 u = *reinterpret_cast<const uint2*>(vc + (cbase + j) * D + 4 * lane);
           vv4[0] = __uint_as_float(u.x << 16); vv4[1] = __uint_as_float(u.x & 0xffff0000u);
           vv4[2] = __uint_as_float(u.y << 16); vv4[3] = __uint_as_float(u.y & 0xffff0000u);
         }
