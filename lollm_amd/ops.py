@@ -183,6 +183,8 @@ def attn_verify(q, k_cache, v_cache, kv_len, gate=None, *, grid=0, scale=None,
 # ------------------------------------------------------------------------------------
 GEMM_NONE, GEMM_SWIGLU = 0, 1
 GEMM_MAX_ROWS = 64
+# lollm_gemm_logits with extra penalised tokens: at most this many per row (n_extra0 + T - 1)
+GEMM_LOGITS_MAX_EXTRA = 8
 _gemm_ws = {}
 
 

@@ -189,9 +189,11 @@ class SpecDecoder:
         # sampled verify: the lm_head writes the logits with the repetition penalty applied
         # and the rows' maxima (lollm_gemm_logits), so the acceptance reads each row once
         # (lollm_spec_accept_rowmax); set False to run lm_head, penalty and acceptance as
-        # separate passes (same bits)
+        # separate passes (same bits; taken by itself past lollm_gemm_logits' limit of
+        # penalised draft tokens per row)
         self.fused_logits = (not self.greedy_argmax and temperature > 0 and lm.tiled is not None
-                             and lm.path(batch * (k + 1)) == "gemm")
+                             and lm.path(batch * (k + 1)) == "gemm"
+                             and (self.seen is None or k <= ops.GEMM_LOGITS_MAX_EXTRA))
         self.verify_logits = self.verify_rmax = None
         if self.fused_logits:
             self.verify_logits = torch.empty(batch, k + 1, cfg.vocab_size, dtype=torch.bfloat16,

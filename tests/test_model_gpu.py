@@ -216,3 +216,34 @@ def test_graph_replay_matches_eager(micro, pen, draft):
                 dec.step()
         outs.append(dec.tokens())
     assert outs[0] == outs[1]
+
+
+def test_sampled_penalised_step_beyond_the_fused_extra_limit(micro):
+    """k = 9 drafts with a repetition penalty: more penalised draft tokens per verify row
+    than lollm_gemm_logits takes (8), so the decoder runs the lm_head, the penalty and the
+    acceptance as separate passes; with k = 8 it fuses them.  Both run, and the k = 8
+    decoder's tokens equal those of the same decoder forced onto the separate passes."""
+    model, mtp, _, cfg = micro
+    from lollm_amd import ops
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    print("case sampled penalised k=9 / k=8", flush=True)
+    g = torch.Generator().manual_seed(12)
+    prompts = torch.randint(0, cfg.vocab_size, (2, 10), generator=g)
+    dec = SpecDecoder(model, mtp, 2, 120, k=9, temperature=0.7, top_p=0.95, seed=3,
+                      repetition_penalty=1.2)
+    assert not dec.fused_logits
+    dec.prefill(prompts.cuda())
+    for _ in range(3):
+        dec.step()
+    assert all(len(t) >= 3 for t in dec.tokens())
+    outs = []
+    for fused in (True, False):
+        dec = SpecDecoder(model, mtp, 2, 120, k=ops.GEMM_LOGITS_MAX_EXTRA, temperature=0.7,
+                          top_p=0.95, seed=3, repetition_penalty=1.2)
+        assert dec.fused_logits
+        dec.fused_logits = fused
+        dec.prefill(prompts.cuda())
+        for _ in range(3):
+            dec.step()
+        outs.append(dec.tokens())
+    assert outs[0] == outs[1]
