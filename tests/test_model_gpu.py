@@ -247,3 +247,37 @@ def test_sampled_penalised_step_beyond_the_fused_extra_limit(micro):
             dec.step()
         outs.append(dec.tokens())
     assert outs[0] == outs[1]
+
+
+@pytest.mark.parametrize("B,k,temp,top_k,pen,draft", [
+    (20, 3, 0.7, 0, 1.1, "argmax"),    # 80 verify rows: every verify projection on hipBLASLt
+    (1, 1, 0.0, 0, 1.0, "argmax"),     # the reference's own shape (generate_mtp, k = 1)
+    (5, 8, 1.0, 20, 1.3, "sample"),    # sampled drafts, top-k, the fused lm_head's limit
+    (16, 3, 0.7, 0, 1.0, "argmax"),    # the benchmark's sampling, no penalty
+])
+def test_decoder_configurations_graph_equals_eager(micro, B, k, temp, top_k, pen, draft):
+    """SpecDecoder across batch sizes (the GEMM and hipBLASLt paths of the verify pass),
+    draft counts, sampling settings and draft modes: three graph replays give the tokens
+    of three eager steps."""
+    model, mtp, _, cfg = micro
+    from lollm_amd.qwen3_5.mtp import SpecDecoder
+    print(f"case decoder B={B} k={k} T={temp} top_k={top_k} pen={pen} draft={draft}", flush=True)
+    g = torch.Generator().manual_seed(B * 7 + k)
+    prompts = torch.randint(0, cfg.vocab_size, (B, 12), generator=g)
+    outs = []
+    for use_graph in (False, True):
+        dec = SpecDecoder(model, mtp, B, 12 + 4 * (k + 1) + 8, k=k, temperature=temp,
+                          top_k=top_k, top_p=0.95, seed=5, repetition_penalty=pen, draft=draft)
+        dec.prefill(prompts.cuda())
+        dec.step()
+        if use_graph:
+            dec.capture()
+        for _ in range(3):
+            if use_graph:
+                dec.replay()
+                torch.cuda.synchronize()
+            else:
+                dec.step()
+        outs.append(dec.tokens())
+    assert outs[0] == outs[1]
+    assert all(len(t) >= 4 for t in outs[0])
