@@ -40,6 +40,20 @@ def test_bad_arguments_are_rejected_before_any_launch():
     assert rc == 1
     with pytest.raises(RuntimeError, match="invalid argument"):
         _lib.check(rc, "lollm_gdn_verify")
+    # the step's other entry points: null buffers are refused before any HIP call
+    assert L.lollm_verify_input(None, None, 3, None, 100, None, 1e-6, None, None, None, None,
+                                None, 16, 4096, None) == 1
+    assert L.lollm_gemm_logits(None, 4096, None, 64, 151936, 4096, None, 151936, None, 5, None,
+                               0, None, 0, 0, 4, 1.0, None, 0, 256, None) == 1
+    assert L.lollm_spec_accept_rowmax(None, None, 5, 5, None, None, 16, 3, 151936, 1.4, 0,
+                                      0.95, 7, 0, None, None, None, None, 0, None) == 1
+    assert L.lollm_spec_accept(None, None, None, 16, 3, 151936, 1.4, 0, 0.95, 7, 0, None,
+                               None, None, None, 0, None) == 1
+    assert L.lollm_attn_prologue(None, None, None, None, None, None, 0, 16, 4, 32, 4, 256, 64,
+                                 1e-6, None, None, None, None, 2048, None) == 1
+    assert L.lollm_mtp_input(None, 1, None, 4096, None, 100, None, None, None, 16, 4096, 1e-6,
+                             None) == 1
+    assert L.lollm_rmsnorm(None, None, None, None, None, 64, 4096, 1e-6, None) == 1
 
 
 def test_missing_library_raises(monkeypatch, tmp_path):
