@@ -103,6 +103,31 @@ def test_spec_accept_rowmax_bit_exact(with_draft, temp, top_k, top_p):
         assert np.array_equal(nt.cpu().numpy(), nt_ref)
 
 
+@pytest.mark.parametrize("with_draft", [True, False])
+def test_spec_accept_rowmax_vocab_beyond_register_rows(with_draft):
+    """A vocabulary larger than the rows the given-maxima statistics kernel holds in
+    registers (20 x 1024 chunks of 8 = 163840 tokens): the rest of each row is counted
+    from a second batch of loads.  Bit-exact against the C oracle."""
+    from lollm_amd import ops
+    print(f"case accept rowmax V=172032 draft={with_draft}", flush=True)
+    B, k, V = 8, 2, 172032
+    tgt, drf = acceptance_case(B, k, V, seed=6)
+    tgt[1, :, 170000] = 30.0                                  # the maximum in the tail
+    inv = S.inv_temperature(0.8)
+    drafts = np.stack([S.sample_rows(drf[:, i].contiguous(), inv, 0, 0.9, 3, 0, 0, k + 1 + i)
+                       for i in range(k)], 1).astype(np.int32)
+    if not with_draft:
+        drf = None
+    rm = order_key_slots(tgt).cuda()
+    for off in (0, 5):
+        na_ref, nt_ref = S.spec_accept(tgt, drf, drafts, inv, 0, 0.9, 3, off)
+        na, nt = ops.spec_accept(tgt.cuda(), None if drf is None else drf.cuda(),
+                                 torch.from_numpy(drafts).cuda(), 0.8, 0, 0.9, 3, off,
+                                 target_rowmax=rm)
+        assert np.array_equal(na.cpu().numpy(), na_ref)
+        assert np.array_equal(nt.cpu().numpy(), nt_ref)
+
+
 def test_spec_accept_small_vocab_ties_and_edges():
     """Tiny vocabulary with heavy ties, flushed keys and argmax-drawn drafts; many
     offsets so accepts, residual draws and bonus draws all occur."""
