@@ -189,8 +189,9 @@ def test_spec_accept_full_vocab_late_rejections_and_bonus():
 
 @pytest.mark.parametrize("temp", [0.0, 0.8])
 def test_sample_rows_vocab_beyond_register_rows(temp):
-    """A vocabulary larger than the rows the statistics kernel holds in registers
-    (19 x 1024 chunks of 8 = 155648 tokens): the tail is re-read from memory."""
+    """A 200000-token vocabulary, larger than the test workloads elsewhere, with the
+    maximum of one row far into the part the statistics kernel counts as it streams
+    (past its first 8 chunks of 8 tokens per thread)."""
     from lollm_amd import ops
     V = 200000
     gen = torch.Generator().manual_seed(5)
